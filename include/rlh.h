@@ -1,0 +1,208 @@
+/* rlh.h — C ABI of the MI355X (gfx950) Qwen3 token loop.
+ *
+ * This is the drop-in boundary behind the reference's Rust API. A Rust host
+ * keeps `Model::forward_into` / `KvCache` / the sampler and binds these
+ * symbols through a thin FFI crate (the binding is shown in INTEGRATION.md).
+ * Plain C types only: pointers, sizes and status codes; no torch or HIP
+ * types cross the boundary.
+ *
+ * Conventions
+ *  - Every entry returning `int` returns RLH_OK (0) on success and a negative
+ *    RLH_E* code on failure; `rlh_last_error()` then describes the failure
+ *    (thread-local). Nothing here aborts on bad input: shape, type and
+ *    context errors are reported, where the reference would `assert!`
+ *    (src/ops.rs:70-71, 153-154).
+ *  - Host pointers (`const void* host_bytes`, `float* logits`, ...) are
+ *    borrowed for the duration of the call only.
+ *  - A model is immutable after rlh_model_finalize and may be shared by
+ *    several caches. A cache owns one HIP stream and its device KV memory;
+ *    calls on one cache must be serialised by the caller, as the reference
+ *    requires `&mut KvCache` (src/model.rs:353-359; server.rs:5-10).
+ *  - Numerics follow the reference's AVX2 production path bit for bit:
+ *    decode (`rlh_forward_one`) and batched prefill (`rlh_forward_batch`,
+ *    integer semantics of RUST_LLAMA_BATCH_INT=1, src/ops.rs:192-236) return
+ *    the same f32 logits, K/V rows and hidden states as that path.
+ */
+#ifndef RLH_H
+#define RLH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define RLH_OK 0
+#define RLH_EINVAL (-1)   /* bad argument, shape or type                      */
+#define RLH_ENOMEM (-2)   /* device or host allocation failed                 */
+#define RLH_EDEVICE (-3)  /* HIP runtime error                                */
+#define RLH_ESTATE (-4)   /* wrong call order (e.g. model not finalized)      */
+#define RLH_ECTX (-5)     /* position at or beyond the cache's max_ctx        */
+#define RLH_EUNSUP (-6)   /* valid ggml type with no kernel on this path      */
+
+/* ---- ggml tensor types (src/quant.rs:26-41, ids as in GGUF) ----------- */
+#define RLH_TYPE_F32 0u
+#define RLH_TYPE_F16 1u
+#define RLH_TYPE_Q4_0 2u
+#define RLH_TYPE_Q4_1 3u
+#define RLH_TYPE_Q5_0 6u
+#define RLH_TYPE_Q5_1 7u
+#define RLH_TYPE_Q8_0 8u
+#define RLH_TYPE_Q4_K 12u
+#define RLH_TYPE_Q5_K 13u
+#define RLH_TYPE_Q6_K 14u
+#define RLH_TYPE_BF16 30u
+
+/* ---- tensor kinds (GGUF names resolved by Model::load, src/model.rs:164-218) */
+#define RLH_T_TOKEN_EMBD 0   /* token_embd.weight                   */
+#define RLH_T_OUTPUT_NORM 1  /* output_norm.weight                  */
+#define RLH_T_OUTPUT 2       /* output.weight (absent when tied)    */
+#define RLH_T_ATTN_NORM 3    /* blk.{l}.attn_norm.weight            */
+#define RLH_T_ATTN_Q 4       /* blk.{l}.attn_q.weight               */
+#define RLH_T_ATTN_K 5       /* blk.{l}.attn_k.weight               */
+#define RLH_T_ATTN_V 6       /* blk.{l}.attn_v.weight               */
+#define RLH_T_ATTN_OUTPUT 7  /* blk.{l}.attn_output.weight          */
+#define RLH_T_ATTN_Q_NORM 8  /* blk.{l}.attn_q_norm.weight          */
+#define RLH_T_ATTN_K_NORM 9  /* blk.{l}.attn_k_norm.weight          */
+#define RLH_T_FFN_NORM 10    /* blk.{l}.ffn_norm.weight             */
+#define RLH_T_FFN_GATE 11    /* blk.{l}.ffn_gate.weight             */
+#define RLH_T_FFN_UP 12      /* blk.{l}.ffn_up.weight               */
+#define RLH_T_FFN_DOWN 13    /* blk.{l}.ffn_down.weight             */
+#define RLH_T_ATTN_Q_BIAS 14 /* blk.{l}.attn_q.bias (Qwen2 only)    */
+#define RLH_T_ATTN_K_BIAS 15 /* blk.{l}.attn_k.bias                 */
+#define RLH_T_ATTN_V_BIAS 16 /* blk.{l}.attn_v.bias                 */
+
+/* Model hyper-parameters: the fields of `Config` (src/model.rs:15-29). */
+typedef struct rlh_config {
+  uint32_t n_layer, n_embd, n_ff, n_head, n_head_kv, head_dim;
+  float rope_theta, rms_eps;
+  uint32_t n_ctx, vocab_size;
+  uint32_t has_qk_norm, has_output;
+} rlh_config;
+
+typedef struct rlh_model rlh_model;
+typedef struct rlh_cache rlh_cache;
+
+/* Description of the last failure on this thread ("" if none). */
+const char* rlh_last_error(void);
+/* Library version string. */
+const char* rlh_version(void);
+
+/* Bytes of one row of `cols` elements (GgmlType::row_size, quant.rs:69-73);
+ * 0 for an unknown type or a length that is not a whole number of blocks. */
+uint64_t rlh_row_bytes(uint32_t ggml_type, uint64_t cols);
+
+/* ---- model ---------------------------------------------------------------
+ * Replaces Model::load (src/model.rs:150-239): the caller resolves tensors
+ * (from GGUF or a generator) and hands them over one by one. */
+int rlh_model_create(const rlh_config* cfg, rlh_model** out);
+/* Copies one tensor to device memory (the host bytes are borrowed only for
+ * the call, as Tensor borrows the mmap, src/tensor.rs:6-35). Norm and bias
+ * vectors are converted to f32 as Model::load does (model.rs:156-162).
+ * `layer` is ignored for the global kinds. n_cols = elements per row. */
+int rlh_model_set_tensor(rlh_model* m, int kind, int layer, uint32_t ggml_type, const void* host_bytes,
+                         uint64_t n_cols, uint64_t n_rows);
+/* Validates that every tensor the forward pass needs is present with
+ * consistent shapes (the arch gate and "missing tensor" errors of
+ * model.rs:41-52, 794-808), builds the RoPE tables and freezes the model. */
+int rlh_model_finalize(rlh_model* m);
+void rlh_model_destroy(rlh_model* m);
+/* Device bytes held by the model's weights. */
+uint64_t rlh_model_weight_bytes(const rlh_model* m);
+
+/* ---- KV cache ------------------------------------------------------------
+ * Replaces Model::new_cache / KvCache (src/model.rs:107-134, 339-342):
+ * f32 K and V per layer in the same [pos][kv_head][head_dim] layout.
+ * max_ctx is clamped to cfg.n_ctx exactly as model.rs:340 does. */
+int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out);
+int rlh_cache_reset(rlh_cache* c); /* KvCache::reset: len = 0, no zeroing */
+uint64_t rlh_cache_len(const rlh_cache* c);
+uint64_t rlh_cache_max_ctx(const rlh_cache* c);
+void rlh_cache_destroy(rlh_cache* c);
+
+/* ---- forward pass ----------------------------------------------------------
+ * All three return once `logits` (host, >= vocab_size floats, may be NULL to
+ * skip the copy) holds the last token's logits. */
+/* Model::forward_one with logits (src/model.rs:585-738): one decode step at
+ * `pos`; writes K/V at pos; cache len becomes pos + 1. */
+int rlh_forward_one(rlh_model* m, rlh_cache* c, uint32_t token, uint64_t pos, float* logits);
+/* Model::forward_batch (src/model.rs:384-583): n tokens from start_pos,
+ * truncated to max_ctx - start_pos (model.rs:392); logits of the last one. */
+int rlh_forward_batch(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
+                      float* logits);
+/* Model::forward_into (src/model.rs:353-375): n > 1 -> batch, n == 1 -> one. */
+int rlh_forward_into(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
+                     float* logits);
+/* Greedy argmax of the logits computed by the last forward call on this
+ * cache, on device: strict '>' so the lowest index wins ties, as the
+ * sampler's greedy fast path (src/sampler.rs:62-70) and main.rs argmax
+ * (main.rs:453-463) choose. */
+int rlh_greedy_next(rlh_model* m, rlh_cache* c, uint32_t* token);
+/* The greedy token loop of cmd_bench (src/main.rs:500-516) run on device:
+ * starting from `first` at position cache len, n_steps decode steps, each
+ * feeding the argmax of the previous step. out_tokens[i] receives the token
+ * fed at step i, out_tokens[n_steps] the argmax after the last step. EOS is
+ * not checked (the bench protocol here fixes the token count). Stops early
+ * with RLH_ECTX when the cache is full. */
+int rlh_generate_greedy(rlh_model* m, rlh_cache* c, uint32_t first, uint64_t n_steps, uint32_t* out_tokens);
+
+/* ---- inspection for parity tests --------------------------------------------- */
+/* Residual stream after `layer` for the tokens of the last forward call
+ * (n_tokens x n_embd f32, token-major). Requires rlh_cache_set_debug(c, 1)
+ * before that call. */
+int rlh_cache_set_debug(rlh_cache* c, int enable);
+int rlh_debug_layer_hidden(rlh_cache* c, int layer, float* out, uint64_t max_tokens);
+/* K or V rows [0, n_pos) of one layer: n_pos x (n_head_kv*head_dim) f32. */
+int rlh_cache_read_kv(rlh_cache* c, int layer, int which_v, uint64_t n_pos, float* out);
+
+/* ---- op-level entries (host buffers in and out) ----------------------------------
+ * Each uploads its inputs, runs the device kernel the forward pass uses and
+ * copies results back. */
+/* simd::quantize_q8 (src/simd.rs:104-203, AVX2 rounding: ties to even):
+ * qs[n], scales[n/32], sums[n/32], sums16[n/16]; n must be a multiple of 32. */
+int rlh_quantize_q8(const float* x, uint64_t n, int8_t* qs, float* scales, int32_t* sums, int32_t* sums16);
+/* quant::dequant_row (src/quant.rs:191-385) over n elements. */
+int rlh_dequant(uint32_t ggml_type, const void* bytes, uint64_t n, float* out);
+/* ops::matmul (src/ops.rs:67-141), integer path: y = W x with x quantized
+ * to Q8 blocks once. */
+int rlh_matvec(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const float* x, float* y);
+/* ops::matmul_batch with RUST_LLAMA_BATCH_INT=1 (src/ops.rs:192-236):
+ * ys[k*rows + r] (token-major). */
+int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const float* xs, uint64_t n,
+                     float* ys);
+/* Exact integer partial dots of W against Q8 activation bytes (the values
+ * the float combines of simd.rs:581/663/863/891 consume): per row,
+ * Q4_K/Q8_0/Q4_0 -> cols/32 values (one per 32-value block),
+ * Q6_K -> cols/16 values (one per 16-value half-block, unsigned u = q+32). */
+int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
+
+/* ---- measurement ---------------------------------------------------------------------
+ * Runs one resident weight matrix's decode matvec `iters` times on the
+ * cache's stream and reports the average kernel duration (HIP events on that
+ * stream) in microseconds. kind/layer select the tensor. */
+int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int layer, int iters, double* avg_us);
+/* Average duration of one captured decode step (graph launch) over `iters`
+ * steps at the cache's current length, in microseconds; the cache position
+ * advances by `iters`. */
+int rlh_profile_decode(rlh_model* m, rlh_cache* c, int iters, double* avg_us);
+
+/* ---- synthetic models (host only) ------------------------------------------------------
+ * The reference ships no quantizer; these are this project's encoders for
+ * the same block layouts, used to write seeded synthetic models. */
+int rlh_quantize_row(uint32_t ggml_type, const float* src, uint64_t n, void* dst);
+/* Elements [offset, offset+n) of the N(mean, std) stream of (seed, tensor_id). */
+void rlh_synth_normal(uint64_t seed, uint64_t tensor_id, uint64_t offset, uint64_t n, float mean, float stdv,
+                      float* out);
+/* Fills dst (rows * rlh_row_bytes(type, cols) bytes) with a quantized
+ * N(mean, std) matrix; row r holds stream elements [r*cols, (r+1)*cols). */
+int rlh_synth_tensor(uint64_t seed, uint64_t tensor_id, uint32_t ggml_type, uint64_t rows, uint64_t cols, float mean,
+                     float stdv, void* dst, int nthreads);
+/* n token ids uniform over [0, vocab). */
+void rlh_synth_tokens(uint64_t seed, uint64_t n, uint32_t vocab, uint32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RLH_H */

@@ -1,0 +1,925 @@
+// engine.hip — host orchestrator of the gfx950 Qwen3 token loop and the C ABI
+// declared in include/rlh.h.
+//
+// Mirrors src/model.rs: a Model (device-resident weights, immutable after
+// finalize) and a KvCache (device f32 K/V per layer + workspace + one HIP
+// stream). The decode step (Model::forward_one, model.rs:585-738) is captured
+// once per cache as a HIP graph whose kernels read the token id and position
+// from device memory, so the same graph replays for every position.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/rlh.h"
+#include "kernels.h"
+#include "rlh_format.h"
+
+using namespace rlh;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                              \
+  do {                                                                                            \
+    hipError_t e_ = (expr);                                                                       \
+    if (e_ != hipSuccess) return fail(RLH_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+int block_size(uint32_t ty) {  // quant.rs:44-50
+  switch (ty) {
+    case RLH_TYPE_F32: case RLH_TYPE_F16: case RLH_TYPE_BF16: return 1;
+    case RLH_TYPE_Q4_0: case RLH_TYPE_Q4_1: case RLH_TYPE_Q5_0: case RLH_TYPE_Q5_1: case RLH_TYPE_Q8_0: return 32;
+    case RLH_TYPE_Q4_K: case RLH_TYPE_Q5_K: case RLH_TYPE_Q6_K: return 256;
+    default: return 0;
+  }
+}
+int type_size(uint32_t ty) {  // quant.rs:53-66
+  switch (ty) {
+    case RLH_TYPE_F32: return 4;
+    case RLH_TYPE_F16: case RLH_TYPE_BF16: return 2;
+    case RLH_TYPE_Q4_0: return 18;
+    case RLH_TYPE_Q4_1: return 20;
+    case RLH_TYPE_Q5_0: return 22;
+    case RLH_TYPE_Q5_1: return 24;
+    case RLH_TYPE_Q8_0: return 34;
+    case RLH_TYPE_Q4_K: return 144;
+    case RLH_TYPE_Q5_K: return 176;
+    case RLH_TYPE_Q6_K: return 210;
+    default: return 0;
+  }
+}
+
+// Types whose device layout and dequantisation exist (the embedding gather
+// and the parity entries); matvec_supported() is the subset with a matvec.
+bool layout_supported(uint32_t ty) {
+  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
+         ty == RLH_TYPE_F32 || ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Host-side f16 -> f32 for norm/bias conversion (exact).
+float h16(uint16_t h) {
+  uint32_t sign = (uint32_t)(h & 0x8000) << 16, exp = (h >> 10) & 0x1f, mant = h & 0x3ff, bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else {
+      uint32_t e = 113;
+      while (!(mant & 0x400)) {
+        mant <<= 1;
+        e--;
+      }
+      bits = sign | (e << 23) | ((mant & 0x3ff) << 13);
+    }
+  } else if (exp == 0x1f) {
+    bits = sign | 0x7f800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 112) << 23) | (mant << 13);
+  }
+  float f;
+  std::memcpy(&f, &bits, 4);
+  return f;
+}
+
+// A weight matrix in device memory (layout: rlh_format.h).
+struct DevTensor {
+  bool set = false;
+  uint32_t ty = 0;
+  uint64_t rows = 0, cols = 0;
+  uint8_t* mem = nullptr;
+  size_t bytes = 0;
+  DevMat dm{};
+};
+
+struct DevVec {
+  float* p = nullptr;
+  uint64_t n = 0;
+};
+
+struct Layer {
+  DevTensor q, k, v, o, gate, up, down;
+  DevVec attn_norm, ffn_norm, q_norm, k_norm, bq, bk, bv;
+};
+
+// Builds the device layout of rows x cols ggml bytes; returns the blob and
+// fills the plane pointers relative to `base`.
+std::vector<uint8_t> to_device_layout(uint32_t ty, const uint8_t* src, uint64_t rows, uint64_t cols, size_t off[4]) {
+  size_t rb = (size_t)type_size(ty) * (cols / block_size(ty));
+  off[0] = off[1] = off[2] = off[3] = 0;
+  if (ty == RLH_TYPE_Q6_K) {
+    size_t nsb = cols / 256, ns = rows * nsb;
+    off[1] = align256(ns * 128);
+    off[2] = off[1] + align256(ns * 64);
+    off[3] = off[2] + align256(ns * 16);
+    std::vector<uint8_t> out(off[3] + align256(ns * 2));
+    for (size_t s = 0; s < ns; s++) {
+      const uint8_t* b = src + s * 210;  // super-blocks are contiguous across rows
+      std::memcpy(&out[s * 128], b, 128);
+      std::memcpy(&out[off[1] + s * 64], b + 128, 64);
+      std::memcpy(&out[off[2] + s * 16], b + 192, 16);
+      std::memcpy(&out[off[3] + s * 2], b + 208, 2);
+    }
+    return out;
+  }
+  if (ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0) {
+    size_t nb = rows * (cols / 32), qb = ty == RLH_TYPE_Q8_0 ? 32 : 16, bs = (size_t)type_size(ty);
+    off[1] = align256(nb * qb);
+    std::vector<uint8_t> out(off[1] + align256(nb * 2));
+    for (size_t b = 0; b < nb; b++) {
+      const uint8_t* p = src + b * bs;
+      out[off[1] + 2 * b] = p[0];
+      out[off[1] + 2 * b + 1] = p[1];
+      std::memcpy(&out[b * qb], p + 2, qb);
+    }
+    return out;
+  }
+  return std::vector<uint8_t>(src, src + rows * rb);
+}
+
+int upload_matrix(DevTensor& t, uint32_t ty, const void* bytes, uint64_t cols, uint64_t rows) {
+  if (!layout_supported(ty))
+    return fail(RLH_EUNSUP, "ggml type " + std::to_string(ty) + " has no device layout on this path");
+  if (cols == 0 || rows == 0 || cols % (uint64_t)block_size(ty) != 0)
+    return fail(RLH_EINVAL, "row length " + std::to_string(cols) + " is not a multiple of the block size");
+  size_t off[4];
+  std::vector<uint8_t> blob = to_device_layout(ty, (const uint8_t*)bytes, rows, cols, off);
+  if (t.mem) (void)hipFree(t.mem);
+  t.mem = nullptr;
+  hipError_t e = hipMalloc((void**)&t.mem, blob.size());
+  if (e != hipSuccess) return fail(RLH_ENOMEM, std::string("hipMalloc weights: ") + hipGetErrorString(e));
+  HIPCHK(hipMemcpy(t.mem, blob.data(), blob.size(), hipMemcpyHostToDevice));
+  t.set = true;
+  t.ty = ty;
+  t.rows = rows;
+  t.cols = cols;
+  t.bytes = blob.size();
+  t.dm.ty = ty;
+  t.dm.rows = (uint32_t)rows;
+  t.dm.cols = (uint32_t)cols;
+  t.dm.row_bytes = (uint32_t)((size_t)type_size(ty) * (cols / block_size(ty)));
+  t.dm.a = t.mem + off[0];
+  t.dm.b = t.mem + off[1];
+  t.dm.c = t.mem + off[2];
+  t.dm.d = t.mem + off[3];
+  return RLH_OK;
+}
+
+// Norm / bias vectors: dequantised to f32 on the host (model.rs:156-162).
+int upload_vec(DevVec& v, uint32_t ty, const void* bytes, uint64_t n) {
+  std::vector<float> f(n);
+  const uint8_t* p = (const uint8_t*)bytes;
+  if (ty == RLH_TYPE_F32) {
+    std::memcpy(f.data(), p, n * 4);
+  } else if (ty == RLH_TYPE_F16) {
+    for (uint64_t i = 0; i < n; i++) f[i] = h16((uint16_t)(p[2 * i] | (p[2 * i + 1] << 8)));
+  } else if (ty == RLH_TYPE_BF16) {
+    for (uint64_t i = 0; i < n; i++) {
+      uint32_t b = (uint32_t)(p[2 * i] | (p[2 * i + 1] << 8)) << 16;
+      std::memcpy(&f[i], &b, 4);
+    }
+  } else {
+    return fail(RLH_EUNSUP, "norm/bias vectors must be F32, F16 or BF16");
+  }
+  if (v.p) (void)hipFree(v.p);
+  v.p = nullptr;
+  hipError_t e = hipMalloc((void**)&v.p, n * 4);
+  if (e != hipSuccess) return fail(RLH_ENOMEM, "hipMalloc vector");
+  HIPCHK(hipMemcpy(v.p, f.data(), n * 4, hipMemcpyHostToDevice));
+  v.n = n;
+  return RLH_OK;
+}
+
+void free_tensor(DevTensor& t) {
+  if (t.mem) (void)hipFree(t.mem);
+  t = DevTensor();
+}
+void free_vec(DevVec& v) {
+  if (v.p) (void)hipFree(v.p);
+  v = DevVec();
+}
+
+int ensure_device() {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return fail(RLH_EDEVICE, "no HIP device available (librlh needs an MI355X / gfx950 GPU)");
+  return RLH_OK;
+}
+
+}  // namespace
+
+struct rlh_model {
+  rlh_config cfg{};
+  DevTensor token_embd, output;
+  DevVec output_norm;
+  std::vector<Layer> layers;
+  float* rope_cs = nullptr;  // [n_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i+1
+  bool finalized = false;
+};
+
+struct rlh_cache {
+  rlh_model* m = nullptr;
+  hipStream_t st = nullptr;
+  uint64_t max_ctx = 0, len = 0;
+  float* kc = nullptr;  // [L][max_ctx][kvd]
+  float* vc = nullptr;
+  // workspace for one token
+  float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *g = nullptr, *u = nullptr,
+        *logits = nullptr, *scratch = nullptr;
+  Q8Buf act_e{}, act_q{}, act_f{};
+  // step state (device): tok, pos, step, argmax out
+  uint32_t* st_dev = nullptr;  // [0]=tok [1]=pos [2]=step [3]=argmax
+  uint32_t* hist = nullptr;    // greedy history [max_ctx + 1]
+  float* pv = nullptr;
+  uint32_t* pi = nullptr;
+  uint32_t nparts = 256;
+  uint32_t* host_st = nullptr;  // pinned staging for tok/pos
+  hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
+  bool debug = false;
+  float* dbg = nullptr;  // [L][kDbgTokens][E]
+  uint64_t dbg_tokens = 0;
+  bool logits_valid = false;
+};
+
+namespace {
+
+constexpr uint64_t kDbgTokens = 64;
+
+float* layer_k(rlh_cache* c, uint32_t l) {
+  const rlh_config& cfg = c->m->cfg;
+  return c->kc + (size_t)l * c->max_ctx * cfg.n_head_kv * cfg.head_dim;
+}
+float* layer_v(rlh_cache* c, uint32_t l) {
+  const rlh_config& cfg = c->m->cfg;
+  return c->vc + (size_t)l * c->max_ctx * cfg.n_head_kv * cfg.head_dim;
+}
+
+enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
+
+// Enqueues one decode step (model.rs:585-738) reading tok = st_dev[0] and
+// pos = st_dev[1]. dbg_slot >= 0 copies the residual after each layer.
+void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
+  rlh_model* m = c->m;
+  const rlh_config& cfg = m->cfg;
+  hipStream_t st = c->st;
+  const uint32_t E = cfg.n_embd, F = cfg.n_ff, H = cfg.n_head, KVH = cfg.n_head_kv, hd = cfg.head_dim;
+  const float eps = cfg.rms_eps;
+  const float scale = 1.0f / std::sqrt((float)hd);  // model.rs:616
+  uint32_t* tok = c->st_dev;
+  uint32_t* pos = c->st_dev + 1;
+  launch_embed(st, m->token_embd.dm, tok, 1, c->x);
+  for (uint32_t l = 0; l < cfg.n_layer; l++) {
+    Layer& L = m->layers[l];
+    launch_rmsnorm_q8(st, c->x, L.attn_norm.p, E, 1, eps, c->act_e, nullptr);
+    launch_matvec(st, L.q.dm, c->act_e, c->q, nullptr);
+    launch_matvec(st, L.k.dm, c->act_e, c->k, nullptr);
+    launch_matvec(st, L.v.dm, c->act_e, c->v, nullptr);
+    launch_qk_norm_rope_kv(st, c->q, c->k, c->v, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
+                           cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
+                           (int)H, (int)KVH, 1, eps);
+    launch_attention(st, c->q, layer_k(c, l), layer_v(c, l), pos, (int)H, (int)KVH, 1, (uint32_t)c->max_ctx, scale,
+                     c->attn, c->act_q);
+    launch_matvec(st, L.o.dm, c->act_q, nullptr, c->x);
+    launch_rmsnorm_q8(st, c->x, L.ffn_norm.p, E, 1, eps, c->act_e, nullptr);
+    launch_matvec(st, L.gate.dm, c->act_e, c->g, nullptr);
+    launch_matvec(st, L.up.dm, c->act_e, c->u, nullptr);
+    launch_swiglu_q8(st, c->g, c->u, F, c->act_f, nullptr);
+    launch_matvec(st, L.down.dm, c->act_f, nullptr, c->x);
+    if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
+      (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
+                           st);
+  }
+  if (kind == STEP_NOLOGITS) return;
+  launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
+  const DevTensor& ow = m->output.set ? m->output : m->token_embd;
+  launch_matvec(st, ow.dm, c->act_e, c->logits, nullptr);
+  if (kind == STEP_GREEDY)
+    launch_argmax(st, c->logits, cfg.vocab_size, c->pv, c->pi, c->nparts, tok, pos, c->st_dev + 2, c->hist);
+}
+
+int capture(rlh_cache* c, StepKind kind, hipGraphExec_t* out) {
+  hipGraph_t g = nullptr;
+  HIPCHK(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
+  enqueue_step(c, kind, -1);
+  HIPCHK(hipStreamEndCapture(c->st, &g));
+  hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+  return RLH_OK;
+}
+
+int run_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
+  if (c->debug) {
+    enqueue_step(c, kind, dbg_slot);
+    HIPCHK(hipGetLastError());
+    return RLH_OK;
+  }
+  hipGraphExec_t g = kind == STEP_LOGITS ? c->g_logits : (kind == STEP_GREEDY ? c->g_greedy : c->g_nologits);
+  HIPCHK(hipGraphLaunch(g, c->st));
+  return RLH_OK;
+}
+
+int set_tok_pos(rlh_cache* c, uint32_t tok, uint32_t pos) {
+  // The previous step may still read the staging words; wait for the stream
+  // before overwriting them.
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->host_st[0] = tok;
+  c->host_st[1] = pos;
+  HIPCHK(hipMemcpyAsync(c->st_dev, c->host_st, 8, hipMemcpyHostToDevice, c->st));
+  return RLH_OK;
+}
+
+// Default stream/context for the op-level entries.
+hipStream_t op_stream() {
+  static hipStream_t s = nullptr;
+  if (!s) (void)hipStreamCreate(&s);
+  return s;
+}
+
+template <typename T>
+struct DevBuf {
+  T* p = nullptr;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  hipError_t alloc(size_t n) { return hipMalloc((void**)&p, std::max<size_t>(n, 1) * sizeof(T)); }
+};
+
+}  // namespace
+
+extern "C" {
+
+const char* rlh_last_error(void) { return g_err.c_str(); }
+const char* rlh_version(void) { return "rlh 0.1 (gfx950)"; }
+
+uint64_t rlh_row_bytes(uint32_t ty, uint64_t cols) {
+  int bs = block_size(ty);
+  if (bs == 0 || cols % (uint64_t)bs != 0) return 0;
+  return (uint64_t)type_size(ty) * (cols / (uint64_t)bs);
+}
+
+int rlh_model_create(const rlh_config* cfg, rlh_model** out) {
+  if (!cfg || !out) return fail(RLH_EINVAL, "null argument");
+  *out = nullptr;
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (cfg->n_layer == 0 || cfg->n_embd == 0 || cfg->n_head == 0 || cfg->n_head_kv == 0 || cfg->n_ff == 0 ||
+      cfg->vocab_size == 0)
+    return fail(RLH_EINVAL, "config has a zero dimension");
+  if (cfg->head_dim != 128)
+    return fail(RLH_EUNSUP, "head_dim " + std::to_string(cfg->head_dim) + " (this path implements head_dim 128)");
+  if (cfg->n_head % cfg->n_head_kv != 0) return fail(RLH_EINVAL, "n_head must be a multiple of n_head_kv");
+  if (cfg->n_embd % 256 != 0 || cfg->n_ff % 256 != 0)
+    return fail(RLH_EUNSUP, "n_embd and n_ff must be multiples of 256");
+  rlh_model* m = new rlh_model();
+  m->cfg = *cfg;
+  m->layers.resize(cfg->n_layer);
+  *out = m;
+  return RLH_OK;
+}
+
+int rlh_model_set_tensor(rlh_model* m, int kind, int layer, uint32_t ty, const void* bytes, uint64_t n_cols,
+                         uint64_t n_rows) {
+  if (!m || !bytes) return fail(RLH_EINVAL, "null argument");
+  if (m->finalized) return fail(RLH_ESTATE, "model is finalized");
+  if (block_size(ty) == 0) return fail(RLH_EINVAL, "unknown ggml type " + std::to_string(ty));
+  Layer* L = nullptr;
+  if (kind >= RLH_T_ATTN_NORM) {
+    if (layer < 0 || (uint32_t)layer >= m->cfg.n_layer) return fail(RLH_EINVAL, "layer out of range");
+    L = &m->layers[layer];
+  }
+  uint64_t n = n_cols * n_rows;
+  switch (kind) {
+    case RLH_T_TOKEN_EMBD: return upload_matrix(m->token_embd, ty, bytes, n_cols, n_rows);
+    case RLH_T_OUTPUT_NORM: return upload_vec(m->output_norm, ty, bytes, n);
+    case RLH_T_OUTPUT: return upload_matrix(m->output, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_NORM: return upload_vec(L->attn_norm, ty, bytes, n);
+    case RLH_T_ATTN_Q: return upload_matrix(L->q, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_K: return upload_matrix(L->k, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_V: return upload_matrix(L->v, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_OUTPUT: return upload_matrix(L->o, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_Q_NORM: return upload_vec(L->q_norm, ty, bytes, n);
+    case RLH_T_ATTN_K_NORM: return upload_vec(L->k_norm, ty, bytes, n);
+    case RLH_T_FFN_NORM: return upload_vec(L->ffn_norm, ty, bytes, n);
+    case RLH_T_FFN_GATE: return upload_matrix(L->gate, ty, bytes, n_cols, n_rows);
+    case RLH_T_FFN_UP: return upload_matrix(L->up, ty, bytes, n_cols, n_rows);
+    case RLH_T_FFN_DOWN: return upload_matrix(L->down, ty, bytes, n_cols, n_rows);
+    case RLH_T_ATTN_Q_BIAS: return upload_vec(L->bq, ty, bytes, n);
+    case RLH_T_ATTN_K_BIAS: return upload_vec(L->bk, ty, bytes, n);
+    case RLH_T_ATTN_V_BIAS: return upload_vec(L->bv, ty, bytes, n);
+    default: return fail(RLH_EINVAL, "unknown tensor kind " + std::to_string(kind));
+  }
+}
+
+static int check_matrix(const DevTensor& t, const char* name, int layer, uint64_t rows, uint64_t cols) {
+  std::string nm = layer >= 0 ? "blk." + std::to_string(layer) + "." + name : std::string(name);
+  if (!t.set) return fail(RLH_ESTATE, "model is missing required tensor '" + nm + ".weight'");
+  if (t.rows != rows || t.cols != cols)
+    return fail(RLH_EINVAL, "tensor '" + nm + "' has shape " + std::to_string(t.rows) + "x" + std::to_string(t.cols) +
+                                ", expected " + std::to_string(rows) + "x" + std::to_string(cols));
+  if (!matvec_supported(t.ty))
+    return fail(RLH_EUNSUP, "tensor '" + nm + "' has ggml type " + std::to_string(t.ty) + " with no matvec kernel");
+  return RLH_OK;
+}
+static int check_vec(const DevVec& v, const char* name, int layer, uint64_t n, bool required) {
+  std::string nm = layer >= 0 ? "blk." + std::to_string(layer) + "." + name : std::string(name);
+  if (!v.p) return required ? fail(RLH_ESTATE, "model is missing required tensor '" + nm + "'") : RLH_OK;
+  if (v.n != n) return fail(RLH_EINVAL, "tensor '" + nm + "' has " + std::to_string(v.n) + " elements");
+  return RLH_OK;
+}
+
+int rlh_model_finalize(rlh_model* m) {
+  if (!m) return fail(RLH_EINVAL, "null model");
+  if (m->finalized) return RLH_OK;
+  const rlh_config& c = m->cfg;
+  uint64_t E = c.n_embd, F = c.n_ff, qd = (uint64_t)c.n_head * c.head_dim, kvd = (uint64_t)c.n_head_kv * c.head_dim;
+  if (!m->token_embd.set) return fail(RLH_ESTATE, "model is missing required tensor 'token_embd.weight'");
+  if (m->token_embd.cols != E || m->token_embd.rows != c.vocab_size)
+    return fail(RLH_EINVAL, "token_embd shape does not match n_embd x vocab_size");
+  int rc;
+  if ((rc = check_vec(m->output_norm, "output_norm.weight", -1, E, true))) return rc;
+  if (m->output.set) {
+    if ((rc = check_matrix(m->output, "output", -1, c.vocab_size, E))) return rc;
+  } else if (!matvec_supported(m->token_embd.ty)) {
+    return fail(RLH_EUNSUP, "tied token_embd type has no matvec kernel for the logits");
+  }
+  for (uint32_t l = 0; l < c.n_layer; l++) {
+    Layer& L = m->layers[l];
+    int li = (int)l;
+    if ((rc = check_vec(L.attn_norm, "attn_norm.weight", li, E, true))) return rc;
+    if ((rc = check_vec(L.ffn_norm, "ffn_norm.weight", li, E, true))) return rc;
+    if ((rc = check_matrix(L.q, "attn_q", li, qd, E))) return rc;
+    if ((rc = check_matrix(L.k, "attn_k", li, kvd, E))) return rc;
+    if ((rc = check_matrix(L.v, "attn_v", li, kvd, E))) return rc;
+    if ((rc = check_matrix(L.o, "attn_output", li, E, qd))) return rc;
+    if ((rc = check_matrix(L.gate, "ffn_gate", li, F, E))) return rc;
+    if ((rc = check_matrix(L.up, "ffn_up", li, F, E))) return rc;
+    if ((rc = check_matrix(L.down, "ffn_down", li, E, F))) return rc;
+    if ((rc = check_vec(L.q_norm, "attn_q_norm.weight", li, c.head_dim, c.has_qk_norm != 0))) return rc;
+    if ((rc = check_vec(L.k_norm, "attn_k_norm.weight", li, c.head_dim, c.has_qk_norm != 0))) return rc;
+    if ((rc = check_vec(L.bq, "attn_q.bias", li, qd, false))) return rc;
+    if ((rc = check_vec(L.bk, "attn_k.bias", li, kvd, false))) return rc;
+    if ((rc = check_vec(L.bv, "attn_v.bias", li, kvd, false))) return rc;
+  }
+  // RoPE table with the host libm, as the reference computes it:
+  // inv_freq = theta^(-2i/hd) (model.rs:221-227), angle = pos * inv_freq,
+  // (sin, cos) = f32::sin_cos (ops.rs:439).
+  uint32_t half = c.head_dim / 2;
+  std::vector<float> inv(half);
+  for (uint32_t i = 0; i < half; i++) {
+    float e = -2.0f * (float)i / (float)c.head_dim;
+    inv[i] = std::pow(c.rope_theta, e);
+  }
+  uint64_t nctx = std::max<uint32_t>(c.n_ctx, 1);
+  std::vector<float> cs((size_t)nctx * c.head_dim);
+  for (uint64_t p = 0; p < nctx; p++) {
+    float pf = (float)p;
+    for (uint32_t i = 0; i < half; i++) {
+      float a = pf * inv[i];
+      cs[p * c.head_dim + 2 * i] = std::cos(a);
+      cs[p * c.head_dim + 2 * i + 1] = std::sin(a);
+    }
+  }
+  hipError_t e = hipMalloc((void**)&m->rope_cs, cs.size() * 4);
+  if (e != hipSuccess) return fail(RLH_ENOMEM, "hipMalloc rope table");
+  HIPCHK(hipMemcpy(m->rope_cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  m->finalized = true;
+  return RLH_OK;
+}
+
+void rlh_model_destroy(rlh_model* m) {
+  if (!m) return;
+  free_tensor(m->token_embd);
+  free_tensor(m->output);
+  free_vec(m->output_norm);
+  for (auto& L : m->layers) {
+    free_tensor(L.q); free_tensor(L.k); free_tensor(L.v); free_tensor(L.o);
+    free_tensor(L.gate); free_tensor(L.up); free_tensor(L.down);
+    free_vec(L.attn_norm); free_vec(L.ffn_norm); free_vec(L.q_norm); free_vec(L.k_norm);
+    free_vec(L.bq); free_vec(L.bk); free_vec(L.bv);
+  }
+  if (m->rope_cs) (void)hipFree(m->rope_cs);
+  delete m;
+}
+
+uint64_t rlh_model_weight_bytes(const rlh_model* m) {
+  if (!m) return 0;
+  uint64_t s = m->token_embd.bytes + m->output.bytes;
+  for (auto& L : m->layers) s += L.q.bytes + L.k.bytes + L.v.bytes + L.o.bytes + L.gate.bytes + L.up.bytes + L.down.bytes;
+  return s;
+}
+
+static void cache_free(rlh_cache* c) {
+  if (c->g_logits) (void)hipGraphExecDestroy(c->g_logits);
+  if (c->g_nologits) (void)hipGraphExecDestroy(c->g_nologits);
+  if (c->g_greedy) (void)hipGraphExecDestroy(c->g_greedy);
+  void* ptrs[] = {c->kc, c->vc, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
+                  c->act_e.qs, c->act_e.d, c->act_e.s, c->act_e.s16, c->act_q.qs, c->act_q.d, c->act_q.s,
+                  c->act_q.s16, c->act_f.qs, c->act_f.d, c->act_f.s, c->act_f.s16, c->st_dev, c->hist, c->pv,
+                  c->pi, c->dbg};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  if (c->host_st) (void)hipHostFree(c->host_st);
+  if (c->st) (void)hipStreamDestroy(c->st);
+  delete c;
+}
+
+static int alloc_q8(Q8Buf& b, uint64_t n) {
+  if (hipMalloc((void**)&b.qs, n) != hipSuccess || hipMalloc((void**)&b.d, n / 32 * 4) != hipSuccess ||
+      hipMalloc((void**)&b.s, n / 32 * 4) != hipSuccess || hipMalloc((void**)&b.s16, n / 16 * 4) != hipSuccess)
+    return fail(RLH_ENOMEM, "hipMalloc Q8 activation");
+  return RLH_OK;
+}
+
+int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
+  if (!m || !out) return fail(RLH_EINVAL, "null argument");
+  *out = nullptr;
+  if (!m->finalized) return fail(RLH_ESTATE, "model is not finalized");
+  const rlh_config& cfg = m->cfg;
+  max_ctx = std::min<uint64_t>(max_ctx, cfg.n_ctx);  // model.rs:340
+  if (max_ctx == 0) return fail(RLH_EINVAL, "max_ctx is 0");
+  size_t lds = (size_t)max_ctx * 4;
+  if (lds > 150 * 1024) return fail(RLH_EUNSUP, "max_ctx above 38400 is not supported by the attention kernel");
+  if (!attention_set_max_lds(std::max<size_t>(lds, 64 * 1024))) return fail(RLH_EDEVICE, "attention LDS attribute");
+  rlh_cache* c = new rlh_cache();
+  c->m = m;
+  c->max_ctx = max_ctx;
+  uint64_t E = cfg.n_embd, F = cfg.n_ff, qd = (uint64_t)cfg.n_head * cfg.head_dim,
+           kvd = (uint64_t)cfg.n_head_kv * cfg.head_dim;
+  size_t kvbytes = (size_t)cfg.n_layer * max_ctx * kvd * 4;
+  bool ok = hipStreamCreate(&c->st) == hipSuccess && hipMalloc((void**)&c->kc, kvbytes) == hipSuccess &&
+            hipMalloc((void**)&c->vc, kvbytes) == hipSuccess && hipMalloc((void**)&c->x, E * 4) == hipSuccess &&
+            hipMalloc((void**)&c->q, qd * 4) == hipSuccess && hipMalloc((void**)&c->k, kvd * 4) == hipSuccess &&
+            hipMalloc((void**)&c->v, kvd * 4) == hipSuccess && hipMalloc((void**)&c->attn, qd * 4) == hipSuccess &&
+            hipMalloc((void**)&c->g, F * 4) == hipSuccess && hipMalloc((void**)&c->u, F * 4) == hipSuccess &&
+            hipMalloc((void**)&c->logits, (size_t)cfg.vocab_size * 4) == hipSuccess &&
+            hipMalloc((void**)&c->scratch, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) == hipSuccess &&
+            hipMalloc((void**)&c->st_dev, 64) == hipSuccess &&
+            hipMalloc((void**)&c->hist, (max_ctx + 2) * 4) == hipSuccess &&
+            hipMalloc((void**)&c->pv, c->nparts * 4) == hipSuccess &&
+            hipMalloc((void**)&c->pi, c->nparts * 4) == hipSuccess &&
+            hipHostMalloc((void**)&c->host_st, 64) == hipSuccess;
+  if (!ok) {
+    cache_free(c);
+    return fail(RLH_ENOMEM, "cache allocation failed");
+  }
+  int rc = alloc_q8(c->act_e, E);
+  if (!rc) rc = alloc_q8(c->act_q, qd);
+  if (!rc) rc = alloc_q8(c->act_f, F);
+  if (rc) {
+    cache_free(c);
+    return rc;
+  }
+  if (hipMemset(c->st_dev, 0, 64) != hipSuccess || hipMemset(c->kc, 0, kvbytes) != hipSuccess ||
+      hipMemset(c->vc, 0, kvbytes) != hipSuccess) {
+    cache_free(c);
+    return fail(RLH_EDEVICE, "cache init");
+  }
+  if ((rc = capture(c, STEP_LOGITS, &c->g_logits)) || (rc = capture(c, STEP_NOLOGITS, &c->g_nologits)) ||
+      (rc = capture(c, STEP_GREEDY, &c->g_greedy))) {
+    std::string msg = g_err;
+    cache_free(c);
+    return fail(rc, msg);
+  }
+  *out = c;
+  return RLH_OK;
+}
+
+int rlh_cache_reset(rlh_cache* c) {
+  if (!c) return fail(RLH_EINVAL, "null cache");
+  c->len = 0;
+  c->logits_valid = false;
+  return RLH_OK;
+}
+uint64_t rlh_cache_len(const rlh_cache* c) { return c ? c->len : 0; }
+uint64_t rlh_cache_max_ctx(const rlh_cache* c) { return c ? c->max_ctx : 0; }
+void rlh_cache_destroy(rlh_cache* c) {
+  if (!c) return;
+  (void)hipStreamSynchronize(c->st);
+  cache_free(c);
+}
+
+int rlh_cache_set_debug(rlh_cache* c, int enable) {
+  if (!c) return fail(RLH_EINVAL, "null cache");
+  c->debug = enable != 0;
+  if (c->debug && !c->dbg) {
+    size_t n = (size_t)c->m->cfg.n_layer * kDbgTokens * c->m->cfg.n_embd;
+    if (hipMalloc((void**)&c->dbg, n * 4) != hipSuccess) return fail(RLH_ENOMEM, "hipMalloc debug buffer");
+    c->dbg_tokens = kDbgTokens;
+  }
+  return RLH_OK;
+}
+
+static int check_forward_args(rlh_model* m, rlh_cache* c) {
+  if (!m || !c) return fail(RLH_EINVAL, "null argument");
+  if (c->m != m) return fail(RLH_EINVAL, "cache belongs to another model");
+  return RLH_OK;
+}
+
+static int copy_logits(rlh_cache* c, float* logits) {
+  if (logits)
+    HIPCHK(hipMemcpyAsync(logits, c->logits, (size_t)c->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  return RLH_OK;
+}
+
+int rlh_forward_one(rlh_model* m, rlh_cache* c, uint32_t token, uint64_t pos, float* logits) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (token >= m->cfg.vocab_size) return fail(RLH_EINVAL, "token id out of range");
+  if (pos >= c->max_ctx) return fail(RLH_ECTX, "position " + std::to_string(pos) + " >= max_ctx");
+  if ((rc = set_tok_pos(c, token, (uint32_t)pos))) return rc;
+  if ((rc = run_step(c, STEP_LOGITS, 0))) return rc;
+  c->len = pos + 1;
+  c->logits_valid = true;
+  return copy_logits(c, logits);
+}
+
+int rlh_forward_batch(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
+                      float* logits) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!tokens && n) return fail(RLH_EINVAL, "null tokens");
+  n = std::min<uint64_t>(n, c->max_ctx > start_pos ? c->max_ctx - start_pos : 0);  // model.rs:392
+  if (n == 0) return RLH_OK;
+  for (uint64_t i = 0; i < n; i++)
+    if (tokens[i] >= m->cfg.vocab_size) return fail(RLH_EINVAL, "token id out of range");
+  for (uint64_t i = 0; i < n; i++) {
+    if ((rc = set_tok_pos(c, tokens[i], (uint32_t)(start_pos + i)))) return rc;
+    if ((rc = run_step(c, i + 1 == n ? STEP_LOGITS : STEP_NOLOGITS, (int64_t)i))) return rc;
+  }
+  c->len = start_pos + n;
+  c->logits_valid = true;
+  return copy_logits(c, logits);
+}
+
+int rlh_forward_into(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
+                     float* logits) {
+  if (n > 1) return rlh_forward_batch(m, c, tokens, n, start_pos, logits);  // model.rs:362-366
+  if (n == 0) return check_forward_args(m, c);
+  if (!tokens) return fail(RLH_EINVAL, "null tokens");
+  return rlh_forward_one(m, c, tokens[0], start_pos, logits);
+}
+
+int rlh_greedy_next(rlh_model* m, rlh_cache* c, uint32_t* token) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!token) return fail(RLH_EINVAL, "null token");
+  if (!c->logits_valid) return fail(RLH_ESTATE, "no logits computed on this cache yet");
+  launch_argmax(c->st, c->logits, m->cfg.vocab_size, c->pv, c->pi, c->nparts, c->st_dev + 3, nullptr, nullptr,
+                nullptr);
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(c->host_st + 3, c->st_dev + 3, 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  *token = c->host_st[3];
+  return RLH_OK;
+}
+
+int rlh_generate_greedy(rlh_model* m, rlh_cache* c, uint32_t first, uint64_t n_steps, uint32_t* out_tokens) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!out_tokens) return fail(RLH_EINVAL, "null out_tokens");
+  if (first >= m->cfg.vocab_size) return fail(RLH_EINVAL, "token id out of range");
+  uint64_t room = c->max_ctx > c->len ? c->max_ctx - c->len : 0;
+  uint64_t n = std::min(n_steps, room);
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->host_st[0] = first;
+  c->host_st[1] = (uint32_t)c->len;
+  c->host_st[2] = 0;
+  HIPCHK(hipMemcpyAsync(c->st_dev, c->host_st, 12, hipMemcpyHostToDevice, c->st));
+  HIPCHK(hipMemcpyAsync(c->hist, c->host_st, 4, hipMemcpyHostToDevice, c->st));
+  for (uint64_t i = 0; i < n; i++)
+    if ((rc = run_step(c, STEP_GREEDY, (int64_t)i))) return rc;
+  HIPCHK(hipMemcpyAsync(out_tokens, c->hist, (n + 1) * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->len += n;
+  if (n > 0) {
+    c->logits_valid = true;
+  }
+  if (n < n_steps) return fail(RLH_ECTX, "cache full after " + std::to_string(n) + " steps");
+  return RLH_OK;
+}
+
+int rlh_debug_layer_hidden(rlh_cache* c, int layer, float* out, uint64_t max_tokens) {
+  if (!c || !out) return fail(RLH_EINVAL, "null argument");
+  if (!c->dbg) return fail(RLH_ESTATE, "debug capture is off (rlh_cache_set_debug)");
+  if (layer < 0 || (uint32_t)layer >= c->m->cfg.n_layer) return fail(RLH_EINVAL, "layer out of range");
+  uint64_t n = std::min(max_tokens, c->dbg_tokens);
+  size_t E = c->m->cfg.n_embd;
+  HIPCHK(hipStreamSynchronize(c->st));
+  HIPCHK(hipMemcpy(out, c->dbg + (size_t)layer * c->dbg_tokens * E, n * E * 4, hipMemcpyDeviceToHost));
+  return RLH_OK;
+}
+
+int rlh_cache_read_kv(rlh_cache* c, int layer, int which_v, uint64_t n_pos, float* out) {
+  if (!c || !out) return fail(RLH_EINVAL, "null argument");
+  if (layer < 0 || (uint32_t)layer >= c->m->cfg.n_layer) return fail(RLH_EINVAL, "layer out of range");
+  if (n_pos > c->max_ctx) return fail(RLH_EINVAL, "n_pos > max_ctx");
+  size_t kvd = (size_t)c->m->cfg.n_head_kv * c->m->cfg.head_dim;
+  HIPCHK(hipStreamSynchronize(c->st));
+  HIPCHK(hipMemcpy(out, which_v ? layer_v(c, layer) : layer_k(c, layer), n_pos * kvd * 4, hipMemcpyDeviceToHost));
+  return RLH_OK;
+}
+
+// ---- op-level entries ----------------------------------------------------
+int rlh_quantize_q8(const float* x, uint64_t n, int8_t* qs, float* scales, int32_t* sums, int32_t* sums16) {
+  if (!x || !qs || !scales || !sums || !sums16) return fail(RLH_EINVAL, "null argument");
+  if (n == 0 || n % 32) return fail(RLH_EINVAL, "n must be a positive multiple of 32");
+  int rc = ensure_device();
+  if (rc) return rc;
+  hipStream_t st = op_stream();
+  DevBuf<float> dx;
+  DevBuf<int8_t> dq;
+  DevBuf<float> dd;
+  DevBuf<int32_t> ds, ds16;
+  if (dx.alloc(n) || dq.alloc(n) || dd.alloc(n / 32) || ds.alloc(n / 32) || ds16.alloc(n / 16))
+    return fail(RLH_ENOMEM, "hipMalloc");
+  HIPCHK(hipMemcpyAsync(dx.p, x, n * 4, hipMemcpyHostToDevice, st));
+  launch_quantize_q8(st, dx.p, (uint32_t)n, Q8Buf{dq.p, dd.p, ds.p, ds16.p});
+  HIPCHK(hipGetLastError());
+  HIPCHK(hipMemcpyAsync(qs, dq.p, n, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(scales, dd.p, n / 32 * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(sums, ds.p, n / 32 * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipMemcpyAsync(sums16, ds16.p, n / 16 * 4, hipMemcpyDeviceToHost, st));
+  HIPCHK(hipStreamSynchronize(st));
+  return RLH_OK;
+}
+
+static int op_upload(DevTensor& t, uint32_t ty, const void* w, uint64_t rows, uint64_t cols) {
+  if (!w) return fail(RLH_EINVAL, "null weights");
+  int rc = ensure_device();
+  if (rc) return rc;
+  return upload_matrix(t, ty, w, cols, rows);
+}
+
+int rlh_dequant(uint32_t ty, const void* bytes, uint64_t n, float* out) {
+  if (!out) return fail(RLH_EINVAL, "null argument");
+  if (block_size(ty) == 0) return fail(RLH_EINVAL, "unknown ggml type");
+  DevTensor t;
+  int rc = op_upload(t, ty, bytes, 1, n);
+  if (rc) return rc;
+  hipStream_t st = op_stream();
+  DevBuf<float> d;
+  if (d.alloc(n)) {
+    free_tensor(t);
+    return fail(RLH_ENOMEM, "hipMalloc");
+  }
+  launch_dequant(st, t.dm, d.p);
+  hipError_t e = hipMemcpyAsync(out, d.p, n * 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  free_tensor(t);
+  if (e != hipSuccess) return fail(RLH_EDEVICE, hipGetErrorString(e));
+  return RLH_OK;
+}
+
+int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const float* x, float* y) {
+  if (!x || !y) return fail(RLH_EINVAL, "null argument");
+  if (!matvec_supported(ty)) return fail(RLH_EUNSUP, "no matvec kernel for ggml type " + std::to_string(ty));
+  if (cols % 256 && !(ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0))
+    return fail(RLH_EINVAL, "cols must be a multiple of 256");
+  if (cols % 32) return fail(RLH_EINVAL, "cols must be a multiple of 32");
+  DevTensor t;
+  int rc = op_upload(t, ty, w, rows, cols);
+  if (rc) return rc;
+  hipStream_t st = op_stream();
+  DevBuf<float> dx, dy, dd;
+  DevBuf<int8_t> dq;
+  DevBuf<int32_t> ds, ds16;
+  if (dx.alloc(cols) || dy.alloc(rows) || dq.alloc(cols) || dd.alloc(cols / 32) || ds.alloc(cols / 32) ||
+      ds16.alloc(cols / 16)) {
+    free_tensor(t);
+    return fail(RLH_ENOMEM, "hipMalloc");
+  }
+  Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
+  hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
+  launch_quantize_q8(st, dx.p, (uint32_t)cols, act);
+  launch_matvec(st, t.dm, act, dy.p, nullptr);
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(y, dy.p, rows * 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  free_tensor(t);
+  if (e != hipSuccess) return fail(RLH_EDEVICE, hipGetErrorString(e));
+  return RLH_OK;
+}
+
+int rlh_matmul_batch(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const float* xs, uint64_t n,
+                     float* ys) {
+  if (!xs || !ys) return fail(RLH_EINVAL, "null argument");
+  for (uint64_t k = 0; k < n; k++) {
+    int rc = rlh_matvec(ty, w, rows, cols, xs + k * cols, ys + k * rows);
+    if (rc) return rc;
+  }
+  return RLH_OK;
+}
+
+int rlh_block_dots(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out) {
+  if (!q8 || !out) return fail(RLH_EINVAL, "null argument");
+  if (!matvec_supported(ty)) return fail(RLH_EUNSUP, "no integer dot for ggml type " + std::to_string(ty));
+  uint32_t per_row = ty == RLH_TYPE_Q6_K ? (uint32_t)(cols / 16) : (uint32_t)(cols / 32);
+  DevTensor t;
+  int rc = op_upload(t, ty, w, rows, cols);
+  if (rc) return rc;
+  hipStream_t st = op_stream();
+  DevBuf<int8_t> dq;
+  DevBuf<int32_t> dout;
+  if (dq.alloc(cols) || dout.alloc(rows * per_row)) {
+    free_tensor(t);
+    return fail(RLH_ENOMEM, "hipMalloc");
+  }
+  hipError_t e = hipMemcpyAsync(dq.p, q8, cols, hipMemcpyHostToDevice, st);
+  launch_block_dots(st, t.dm, dq.p, dout.p, per_row);
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(out, dout.p, rows * per_row * 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  free_tensor(t);
+  if (e != hipSuccess) return fail(RLH_EDEVICE, hipGetErrorString(e));
+  return RLH_OK;
+}
+
+// ---- measurement -----------------------------------------------------------
+static const DevTensor* find_matrix(rlh_model* m, int kind, int layer) {
+  if (kind == RLH_T_TOKEN_EMBD) return &m->token_embd;
+  if (kind == RLH_T_OUTPUT) return m->output.set ? &m->output : &m->token_embd;
+  if (layer < 0 || (uint32_t)layer >= m->cfg.n_layer) return nullptr;
+  Layer& L = m->layers[layer];
+  switch (kind) {
+    case RLH_T_ATTN_Q: return &L.q;
+    case RLH_T_ATTN_K: return &L.k;
+    case RLH_T_ATTN_V: return &L.v;
+    case RLH_T_ATTN_OUTPUT: return &L.o;
+    case RLH_T_FFN_GATE: return &L.gate;
+    case RLH_T_FFN_UP: return &L.up;
+    case RLH_T_FFN_DOWN: return &L.down;
+    default: return nullptr;
+  }
+}
+
+int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int layer, int iters, double* avg_us) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!avg_us || iters <= 0) return fail(RLH_EINVAL, "bad argument");
+  const DevTensor* t = find_matrix(m, kind, layer);
+  if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
+  const Q8Buf& act = t->cols == m->cfg.n_ff ? c->act_f
+                     : t->cols == (uint64_t)m->cfg.n_head * m->cfg.head_dim ? c->act_q
+                                                                           : c->act_e;
+  if (t->cols != m->cfg.n_embd && t->cols != m->cfg.n_ff && t->cols != (uint64_t)m->cfg.n_head * m->cfg.head_dim)
+    return fail(RLH_EINVAL, "matrix width matches no activation buffer");
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  launch_matvec(c->st, t->dm, act, c->scratch, nullptr);  // warm-up
+  HIPCHK(hipEventRecord(e0, c->st));
+  for (int i = 0; i < iters; i++) launch_matvec(c->st, t->dm, act, c->scratch, nullptr);
+  HIPCHK(hipEventRecord(e1, c->st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *avg_us = (double)ms * 1000.0 / iters;
+  return RLH_OK;
+}
+
+int rlh_profile_decode(rlh_model* m, rlh_cache* c, int iters, double* avg_us) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!avg_us || iters <= 0) return fail(RLH_EINVAL, "bad argument");
+  if (c->len + (uint64_t)iters > c->max_ctx) return fail(RLH_ECTX, "not enough room in the cache");
+  if (c->debug) return fail(RLH_ESTATE, "profiling needs debug capture off");
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->host_st[0] = 0;
+  c->host_st[1] = (uint32_t)c->len;
+  c->host_st[2] = 0;
+  HIPCHK(hipMemcpyAsync(c->st_dev, c->host_st, 12, hipMemcpyHostToDevice, c->st));
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  HIPCHK(hipEventRecord(e0, c->st));
+  for (int i = 0; i < iters; i++) HIPCHK(hipGraphLaunch(c->g_greedy, c->st));
+  HIPCHK(hipEventRecord(e1, c->st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  c->len += (uint64_t)iters;
+  c->logits_valid = true;
+  *avg_us = (double)ms * 1000.0 / iters;
+  return RLH_OK;
+}
+
+}  // extern "C"

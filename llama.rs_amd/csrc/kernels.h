@@ -1,0 +1,41 @@
+// kernels.h — host-side launch wrappers of the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rlh_format.h"
+
+namespace rlh {
+
+// Q8 activation rows in device memory (Q8Row, simd.rs:88-101), token-major:
+// qs[n][cols], d[n][cols/32], s[n][cols/32], s16[n][cols/16].
+struct Q8Buf {
+  int8_t* qs;
+  float* d;
+  int32_t* s;
+  int32_t* s16;
+};
+
+bool matvec_supported(uint32_t ty);
+
+void launch_embed(hipStream_t st, const DevMat& w, const uint32_t* tok, uint32_t n_tok, float* x);
+void launch_rmsnorm_q8(hipStream_t st, const float* x, const float* w, uint32_t n, uint32_t n_tok, float eps,
+                       const Q8Buf& out, float* xb);
+void launch_quantize_q8(hipStream_t st, const float* x, uint32_t n, const Q8Buf& out);
+void launch_matvec(hipStream_t st, const DevMat& w, const Q8Buf& act, float* y, float* resid);
+void launch_block_dots(hipStream_t st, const DevMat& w, const int8_t* a, int32_t* out, uint32_t per_row);
+void launch_dequant(hipStream_t st, const DevMat& w, float* out);
+void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, const float* bq, const float* bk,
+                            const float* bv, const float* qn, const float* kn, const float* rope_cs,
+                            const uint32_t* pos0, float* kcache, float* vcache, int H, int KVH, uint32_t n_tok,
+                            float eps);
+void launch_attention(hipStream_t st, const float* q, const float* kcache, const float* vcache, const uint32_t* pos0,
+                      int H, int KVH, uint32_t n_tok, uint32_t t_max, float scale, float* out, const Q8Buf& out_q8);
+void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
+                      float* h_out);
+void launch_argmax(hipStream_t st, const float* x, uint32_t n, float* pv, uint32_t* pi, uint32_t nparts,
+                   uint32_t* tok_out, uint32_t* pos, uint32_t* step, uint32_t* hist);
+// Raises the dynamic-LDS limit of the attention kernel (returns false on error).
+bool attention_set_max_lds(size_t bytes);
+
+}  // namespace rlh

@@ -1,0 +1,223 @@
+// rlh_device.h — device-side building blocks shared by the gfx950 kernels.
+//
+// Everything here reproduces the arithmetic of the reference's AVX2 path
+// operation for operation (one IEEE rounding per operator, FMAs exactly where
+// the reference issues _mm256_fmadd_ps). Sources are built with
+// -ffp-contract=off so the compiler never fuses a*b+c on its own.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rlh_format.h"
+
+namespace rlh {
+
+// ---------------------------------------------------------------------------
+// f16 -> f32 (quant.rs:115-157 with F16C): exact for every half value.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float f16_to_f32(uint32_t h16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+// ---------------------------------------------------------------------------
+// expf bit-identical to the host glibc expf the reference calls through
+// f32::exp (softmax_inplace ops.rs:410, silu ops.rs:394).
+// Method: the table-driven exp of ARM's optimized-routines as glibc builds it
+// for FMA-capable x86-64: x*32/ln2 = k + r, exp(x) = 2^(k/32) * p(r) with a
+// cubic p evaluated in double with FMAs. T[i] = bits(2^(i/32)) - (i << 47).
+// Exhaustively checked against glibc 2.35 expf on every float in
+// [-103.9, 88.7] (tests/test_oracle_expf.py re-checks a dense sample).
+// ---------------------------------------------------------------------------
+__device__ __constant__ static const uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float expf_glibc(float x) {
+  const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
+  const double kShift = 0x1.8p+52;
+  const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+  const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+  const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+  uint32_t ux = __float_as_uint(x);
+  uint32_t abstop = (ux >> 20) & 0x7ff;
+  if (abstop >= 0x42b) {                       // |x| >= 88 or NaN
+    if (ux == 0xff800000u) return 0.0f;        // -inf
+    if (abstop >= 0x7f8) return x + x;         // +inf or NaN
+    if (x > 0x1.62e42ep6f) return __int_as_float(0x7f800000);  // overflow
+    if (x < -0x1.9fe368p6f) return 0.0f;       // underflow
+  }
+  double xd = (double)x;
+  double kd = __builtin_fma(kInvLn2N, xd, kShift);
+  uint64_t ki = (uint64_t)__double_as_longlong(kd);
+  kd -= kShift;
+  double r = __builtin_fma(kInvLn2N, xd, -kd);
+  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  double s = __longlong_as_double((long long)t);
+  double z = __builtin_fma(C0, r, C1);
+  double r2 = r * r;
+  double y = __builtin_fma(C2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y = y * s;
+  return (float)y;
+}
+
+// ---------------------------------------------------------------------------
+// Exact AVX2 reduction tree over 32 "slot" accumulators held in lanes 0..31
+// of a wave: slot 8k+l is lane l of the reference's accumulator a_k.
+//   A_l = (a0_l + a1_l) + (a2_l + a3_l)            (simd.rs:308, 370)
+//   hsum(A) = ((A0+A4)+(A2+A6)) + ((A1+A5)+(A3+A7)) (simd.rs:261-270)
+// Every lane returns the result.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float avx2_tree32(float a) {
+  float b = a + __shfl_down(a, 8);
+  float A = b + __shfl_down(b, 16);
+  float s = A + __shfl_down(A, 4);
+  float t = s + __shfl_down(s, 2);
+  float r = t + __shfl_down(t, 1);
+  return __shfl(r, 0);
+}
+
+// Sum of squares of rmsnorm_core (simd.rs:285-313) for one wave: lanes 0..31
+// own the 32 FMA chains; the 8-wide remainder loop feeds slots 0..7; the
+// scalar tail is added last, in order. Returns ss in every lane.
+__device__ __forceinline__ float rms_sumsq_wave(const float* x, int n) {
+  int lane = threadIdx.x & 63;
+  int n32 = (n / 32) * 32;
+  int n8 = n32 + ((n - n32) / 8) * 8;
+  float acc = 0.0f;
+  if (lane < 32) {
+    for (int i = lane; i < n32; i += 32) acc = __builtin_fmaf(x[i], x[i], acc);
+    if (lane < 8)
+      for (int i = n32 + lane; i < n8; i += 8) acc = __builtin_fmaf(x[i], x[i], acc);
+  }
+  float ss = avx2_tree32(acc);
+  for (int i = n8; i < n; i++) ss = ss + x[i] * x[i];
+  return ss;
+}
+
+// ---------------------------------------------------------------------------
+// quantize_q8 of one 32-value block (simd.rs:126-195), one value per lane of
+// a 32-lane half wave (lane & 31 = position in the block).
+// amax -> d = amax/127 -> inv = 1/d -> q = RNE(v*inv) (_mm256_cvtps_epi32) with
+// packs saturation: out-of-range conversions give INT_MIN -> -128.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int cvtps_packs_i8(float r) {
+  // r is already rounded to an integer value (or NaN/inf).
+  if (!(r >= -2147483648.0f && r < 2147483648.0f)) return -128;  // INT_MIN -> -128
+  int v = (int)r;
+  return v > 127 ? 127 : (v < -128 ? -128 : v);
+}
+
+struct Q8Out {
+  int8_t* qs;      // [n]
+  float* d;        // [n/32]
+  int32_t* s;      // [n/32]
+  int32_t* s16;    // [n/16]
+};
+
+__device__ __forceinline__ void q8_quant_block32(float v, Q8Out o, uint32_t blk) {
+  int l = threadIdx.x & 31;
+  float a = fabsf(v);
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m, 32));
+  float d = a / 127.0f;
+  float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  int q = cvtps_packs_i8(__builtin_rintf(v * inv));
+  int s = q;
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) s += __shfl_xor(s, m, 16);  // half sums
+  int tot = s + __shfl_xor(s, 16, 32);
+  o.qs[(size_t)blk * 32 + l] = (int8_t)q;
+  if (l == 0) {
+    o.d[blk] = d;
+    o.s[blk] = tot;
+    o.s16[(size_t)blk * 2] = s;
+  } else if (l == 16) {
+    o.s16[(size_t)blk * 2 + 1] = s;
+  }
+}
+
+// get_scale_min_k4 (quant.rs:176-185) on the 12 scale bytes.
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = q[j] & 63;
+    m = q[j + 4] & 63;
+  } else {
+    sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// ---------------------------------------------------------------------------
+// Element dequantisation in the device layouts (quant.rs:191-385).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float dq_elem(const DevMat& w, uint32_t row, uint32_t i) {
+  switch (w.ty) {
+    case RLH_TYPE_Q4_K: {
+      uint32_t bi = i >> 8, p = i & 255, g = p >> 6, hi = (p >> 5) & 1, l = p & 31;
+      const uint8_t* sb = w.a + (size_t)row * w.row_bytes + (size_t)bi * 144;
+      float d = f16_to_f32(sb[0] | (sb[1] << 8));
+      float dmin = f16_to_f32(sb[2] | (sb[3] << 8));
+      uint32_t sc, m;
+      scale_min_k4((int)(2 * g + hi), sb + 4, sc, m);
+      float d1 = d * (float)sc;
+      float mm1 = dmin * (float)m;
+      uint32_t q = (sb[16 + 32 * g + l] >> (4 * hi)) & 0xF;
+      return d1 * (float)q - mm1;
+    }
+    case RLH_TYPE_Q6_K: {
+      uint32_t nsb = w.cols >> 8;
+      uint32_t bi = i >> 8, p = i & 255, half = p >> 7, pp = p & 127, quarter = pp >> 5, l = pp & 31;
+      size_t sbi = (size_t)row * nsb + bi;
+      const uint8_t* ql = w.a + sbi * 128 + half * 64;
+      const uint8_t* qh = w.b + sbi * 64 + half * 32;
+      const int8_t* sc = (const int8_t*)(w.c + sbi * 16 + half * 8);
+      const uint8_t* dd = w.d + sbi * 2;
+      float d = f16_to_f32(dd[0] | (dd[1] << 8));
+      uint32_t byte = ql[(quarter & 1) * 32 + l];
+      uint32_t nib = quarter < 2 ? (byte & 0xF) : (byte >> 4);
+      uint32_t h2 = (qh[l] >> (2 * quarter)) & 3;
+      int q = (int)(nib | (h2 << 4)) - 32;
+      return d * (float)sc[(l >> 4) + 2 * quarter] * (float)q;
+    }
+    case RLH_TYPE_Q8_0: {
+      uint32_t nb = w.cols >> 5;
+      size_t b = (size_t)row * nb + (i >> 5);
+      float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
+      return (float)(int8_t)w.a[b * 32 + (i & 31)] * d;
+    }
+    case RLH_TYPE_Q4_0: {
+      uint32_t nb = w.cols >> 5;
+      size_t b = (size_t)row * nb + (i >> 5);
+      float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
+      uint32_t j = i & 31;
+      uint32_t byte = w.a[b * 16 + (j & 15)];
+      float x = (float)((int)(j < 16 ? (byte & 0xF) : (byte >> 4)) - 8);
+      return x * d;
+    }
+    case RLH_TYPE_F32:
+      return ((const float*)(w.a + (size_t)row * w.row_bytes))[i];
+    case RLH_TYPE_F16: {
+      const uint8_t* p = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
+      return f16_to_f32(p[0] | (p[1] << 8));
+    }
+    case RLH_TYPE_BF16: {
+      const uint8_t* p = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
+      return __uint_as_float((uint32_t)(p[0] | (p[1] << 8)) << 16);
+    }
+    default:
+      return 0.0f;
+  }
+}
+
+}  // namespace rlh

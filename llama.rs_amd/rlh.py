@@ -1,0 +1,356 @@
+"""ctypes binding of librlh.so (include/rlh.h) plus the synthetic-model specs.
+
+This is the Python stand-in for the thin FFI crate a Rust host would bind
+(the reference's `Model::forward_into` / `KvCache` surface, src/model.rs).
+It loads the in-tree library and raises if it is missing: there is no CPU
+fallback behind it.
+"""
+import ctypes
+import os
+from dataclasses import dataclass, field
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librlh.so")
+
+# ggml type ids (src/quant.rs:26-41)
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
+BLOCK = {F32: (1, 4), F16: (1, 2), BF16: (1, 2), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22),
+         Q5_1: (32, 24), Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}
+
+# tensor kinds (include/rlh.h)
+T_TOKEN_EMBD, T_OUTPUT_NORM, T_OUTPUT = 0, 1, 2
+T_ATTN_NORM, T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_OUTPUT = 3, 4, 5, 6, 7
+T_ATTN_Q_NORM, T_ATTN_K_NORM, T_FFN_NORM, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN = 8, 9, 10, 11, 12, 13
+T_ATTN_Q_BIAS, T_ATTN_K_BIAS, T_ATTN_V_BIAS = 14, 15, 16
+KIND_NAMES = {0: "token_embd", 1: "output_norm", 2: "output", 3: "attn_norm", 4: "attn_q", 5: "attn_k",
+              6: "attn_v", 7: "attn_output", 8: "attn_q_norm", 9: "attn_k_norm", 10: "ffn_norm",
+              11: "ffn_gate", 12: "ffn_up", 13: "ffn_down", 14: "attn_q_bias", 15: "attn_k_bias",
+              16: "attn_v_bias"}
+
+RLH_OK, RLH_EINVAL, RLH_ENOMEM, RLH_EDEVICE, RLH_ESTATE, RLH_ECTX, RLH_EUNSUP = 0, -1, -2, -3, -4, -5, -6
+
+
+def row_bytes(ty, cols):
+    bs, ts = BLOCK[ty]
+    assert cols % bs == 0
+    return cols // bs * ts
+
+
+class Config(ctypes.Structure):
+    """`Config` of src/model.rs:15-29."""
+    _fields_ = [("n_layer", ctypes.c_uint32), ("n_embd", ctypes.c_uint32), ("n_ff", ctypes.c_uint32),
+                ("n_head", ctypes.c_uint32), ("n_head_kv", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float), ("n_ctx", ctypes.c_uint32),
+                ("vocab_size", ctypes.c_uint32), ("has_qk_norm", ctypes.c_uint32), ("has_output", ctypes.c_uint32)]
+
+
+@dataclass
+class ModelSpec:
+    """Shape and per-tensor ggml types of a synthetic Qwen3 model."""
+    name: str
+    n_layer: int
+    n_embd: int
+    n_ff: int
+    n_head: int
+    n_head_kv: int
+    vocab: int
+    tied: bool
+    types: dict = field(default_factory=dict)   # kind -> ggml type
+    head_dim: int = 128
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-6
+    n_ctx: int = 40960
+
+    def config(self):
+        return Config(self.n_layer, self.n_embd, self.n_ff, self.n_head, self.n_head_kv, self.head_dim,
+                      self.rope_theta, self.rms_eps, self.n_ctx, self.vocab, 1, 0 if self.tied else 1)
+
+    def shapes(self):
+        """(kind, rows, cols) of every matrix of one layer."""
+        E, F, qd, kvd = self.n_embd, self.n_ff, self.n_head * self.head_dim, self.n_head_kv * self.head_dim
+        return [(T_ATTN_Q, qd, E), (T_ATTN_K, kvd, E), (T_ATTN_V, kvd, E), (T_ATTN_OUTPUT, E, qd),
+                (T_FFN_GATE, F, E), (T_FFN_UP, F, E), (T_FFN_DOWN, E, F)]
+
+    def weight_bytes_per_token(self):
+        """Packed bytes of every matrix one decode step reads (7 per layer plus
+        the logits matrix) and one embedding row."""
+        total = 0
+        for kind, rows, cols in self.shapes():
+            total += rows * row_bytes(self.types[kind], cols)
+        total *= self.n_layer
+        out_ty = self.types[T_TOKEN_EMBD] if self.tied else self.types[T_OUTPUT]
+        total += self.vocab * row_bytes(out_ty, self.n_embd)
+        total += row_bytes(self.types[T_TOKEN_EMBD], self.n_embd)
+        return total
+
+    def int8_ops_per_token(self):
+        """2 * sum(rows*cols) over the 7 layer matrices (prefill MACs per token)."""
+        return 2 * self.n_layer * sum(r * c for _, r, c in self.shapes())
+
+
+def _q4km(tied, embd_type, out_type):
+    t = {T_ATTN_Q: Q4_K, T_ATTN_K: Q4_K, T_ATTN_V: Q6_K, T_ATTN_OUTPUT: Q4_K, T_FFN_GATE: Q4_K,
+         T_FFN_UP: Q4_K, T_FFN_DOWN: Q6_K, T_TOKEN_EMBD: embd_type}
+    if not tied:
+        t[T_OUTPUT] = out_type
+    return t
+
+
+def _all(ty, tied=True):
+    t = {k: ty for k in (T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_OUTPUT, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN,
+                         T_TOKEN_EMBD)}
+    if not tied:
+        t[T_OUTPUT] = ty
+    return t
+
+
+# The five Qwen3 workloads of the benchmark plan plus small shapes for tests.
+SPECS = {
+    "qwen3-0.6b-q4km": ModelSpec("qwen3-0.6b-q4km", 28, 1024, 3072, 16, 8, 151936, True, _q4km(True, Q4_K, None)),
+    "qwen3-0.6b-q8_0": ModelSpec("qwen3-0.6b-q8_0", 28, 1024, 3072, 16, 8, 151936, True, _all(Q8_0)),
+    "qwen3-4b-q4km": ModelSpec("qwen3-4b-q4km", 36, 2560, 9728, 32, 8, 151936, True, _q4km(True, Q6_K, None)),
+    "qwen3-8b-q4km": ModelSpec("qwen3-8b-q4km", 36, 4096, 12288, 32, 8, 151936, False, _q4km(False, Q4_K, Q6_K)),
+    "qwen3-32b-q4km": ModelSpec("qwen3-32b-q4km", 64, 5120, 25600, 64, 8, 151936, False, _q4km(False, Q4_K, Q6_K)),
+    # small shapes for parity tests (same code paths, seconds on the CPU oracle)
+    "tiny-q4km": ModelSpec("tiny-q4km", 2, 256, 512, 4, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=512),
+    "tiny-q4km-untied": ModelSpec("tiny-q4km-untied", 2, 512, 768, 4, 1, 2048, False, _q4km(False, Q4_K, Q6_K),
+                                  n_ctx=512),
+    "tiny-q8_0": ModelSpec("tiny-q8_0", 2, 256, 512, 4, 2, 1000, True, _all(Q8_0), n_ctx=512),
+    "tiny-q4_0": ModelSpec("tiny-q4_0", 2, 256, 512, 4, 4, 1000, True, _all(Q4_0), n_ctx=512),
+    "small-q4km": ModelSpec("small-q4km", 4, 1024, 3072, 16, 8, 4096, False, _q4km(False, Q4_K, Q6_K), n_ctx=1024),
+}
+
+
+def tensor_id(kind, layer):
+    return kind * 4096 + max(layer, 0)
+
+
+def synth_model(spec, seed, lib=None, nthreads=None):
+    """Seeded synthetic weights: N(0, 0.02) matrices quantized by this
+    project's encoders, norms 1 + N(0, 0.02) in F32. Returns a list of
+    (kind, layer, type, cols, rows, uint8 array)."""
+    lib = lib or load()
+    nthreads = nthreads or min(16, os.cpu_count() or 1)
+    out = []
+
+    def mat(kind, layer, rows, cols, ty):
+        buf = np.empty(rows * row_bytes(ty, cols), dtype=np.uint8)
+        rc = lib.rlh_synth_tensor(seed, tensor_id(kind, layer), ty, rows, cols, 0.0, 0.02,
+                                  buf.ctypes.data, nthreads)
+        if rc != 0:
+            raise RuntimeError(f"synth tensor {KIND_NAMES[kind]} failed: {rc}")
+        out.append((kind, layer, ty, cols, rows, buf))
+
+    def norm(kind, layer, n):
+        v = np.empty(n, dtype=np.float32)
+        lib.rlh_synth_normal(seed, tensor_id(kind, layer), 0, n, 1.0, 0.02, v.ctypes.data)
+        out.append((kind, layer, F32, n, 1, v.view(np.uint8)))
+
+    E = spec.n_embd
+    mat(T_TOKEN_EMBD, 0, spec.vocab, E, spec.types[T_TOKEN_EMBD])
+    norm(T_OUTPUT_NORM, 0, E)
+    if not spec.tied:
+        mat(T_OUTPUT, 0, spec.vocab, E, spec.types[T_OUTPUT])
+    for l in range(spec.n_layer):
+        norm(T_ATTN_NORM, l, E)
+        norm(T_FFN_NORM, l, E)
+        norm(T_ATTN_Q_NORM, l, spec.head_dim)
+        norm(T_ATTN_K_NORM, l, spec.head_dim)
+        for kind, rows, cols in spec.shapes():
+            mat(kind, l, rows, cols, spec.types[kind])
+    return out
+
+
+def synth_tokens(seed, n, vocab, lib=None):
+    lib = lib or load()
+    out = np.empty(n, dtype=np.uint32)
+    lib.rlh_synth_tokens(seed, n, vocab, out.ctypes.data)
+    return out
+
+
+_lib = None
+
+
+def load():
+    """Loads librlh.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, U32, U64, I32, F = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
+    sig = {
+        "rlh_last_error": (ctypes.c_char_p, []),
+        "rlh_version": (ctypes.c_char_p, []),
+        "rlh_row_bytes": (U64, [U32, U64]),
+        "rlh_model_create": (I32, [ctypes.POINTER(Config), ctypes.POINTER(P)]),
+        "rlh_model_set_tensor": (I32, [P, I32, I32, U32, P, U64, U64]),
+        "rlh_model_finalize": (I32, [P]),
+        "rlh_model_destroy": (None, [P]),
+        "rlh_model_weight_bytes": (U64, [P]),
+        "rlh_cache_create": (I32, [P, U64, ctypes.POINTER(P)]),
+        "rlh_cache_reset": (I32, [P]),
+        "rlh_cache_len": (U64, [P]),
+        "rlh_cache_max_ctx": (U64, [P]),
+        "rlh_cache_destroy": (None, [P]),
+        "rlh_forward_one": (I32, [P, P, U32, U64, P]),
+        "rlh_forward_batch": (I32, [P, P, P, U64, U64, P]),
+        "rlh_forward_into": (I32, [P, P, P, U64, U64, P]),
+        "rlh_greedy_next": (I32, [P, P, ctypes.POINTER(U32)]),
+        "rlh_generate_greedy": (I32, [P, P, U32, U64, P]),
+        "rlh_cache_set_debug": (I32, [P, I32]),
+        "rlh_debug_layer_hidden": (I32, [P, I32, P, U64]),
+        "rlh_cache_read_kv": (I32, [P, I32, I32, U64, P]),
+        "rlh_quantize_q8": (I32, [P, U64, P, P, P, P]),
+        "rlh_dequant": (I32, [U32, P, U64, P]),
+        "rlh_matvec": (I32, [U32, P, U64, U64, P, P]),
+        "rlh_matmul_batch": (I32, [U32, P, U64, U64, P, U64, P]),
+        "rlh_block_dots": (I32, [U32, P, U64, U64, P, P]),
+        "rlh_profile_matvec": (I32, [P, P, I32, I32, I32, ctypes.POINTER(ctypes.c_double)]),
+        "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
+        "rlh_quantize_row": (I32, [U32, P, U64, P]),
+        "rlh_synth_normal": (None, [U64, U64, U64, U64, F, F, P]),
+        "rlh_synth_tensor": (I32, [U64, U64, U32, U64, U64, F, F, P, I32]),
+        "rlh_synth_tokens": (None, [U64, U64, U32, P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+class RlhError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"rlh error {code}: {msg}")
+        self.code = code
+
+
+def check(rc):
+    if rc != 0:
+        raise RlhError(rc, load().rlh_last_error().decode())
+    return rc
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+class Model:
+    """Device-resident model (Model, src/model.rs:136-239)."""
+
+    def __init__(self, spec, tensors):
+        self.lib = load()
+        self.spec = spec
+        cfg = spec.config()
+        h = ctypes.c_void_p()
+        check(self.lib.rlh_model_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self.h = h
+        for kind, layer, ty, cols, rows, buf in tensors:
+            check(self.lib.rlh_model_set_tensor(self.h, kind, layer, ty, buf.ctypes.data, cols, rows))
+        check(self.lib.rlh_model_finalize(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.rlh_model_destroy(self.h)
+            self.h = None
+
+    def new_cache(self, max_ctx):
+        return Cache(self, max_ctx)
+
+
+class Cache:
+    """Device KV cache + stream (KvCache, src/model.rs:107-134)."""
+
+    def __init__(self, model, max_ctx):
+        self.lib = model.lib
+        self.model = model
+        h = ctypes.c_void_p()
+        check(self.lib.rlh_cache_create(model.h, max_ctx, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.rlh_cache_destroy(self.h)
+            self.h = None
+
+    @property
+    def len(self):
+        return self.lib.rlh_cache_len(self.h)
+
+    @property
+    def max_ctx(self):
+        return self.lib.rlh_cache_max_ctx(self.h)
+
+    def reset(self):
+        check(self.lib.rlh_cache_reset(self.h))
+
+    def forward_into(self, tokens, start_pos, logits=None):
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        if logits is None:
+            logits = np.empty(self.model.spec.vocab, dtype=np.float32)
+        check(self.lib.rlh_forward_into(self.model.h, self.h, toks.ctypes.data, len(toks), start_pos,
+                                        logits.ctypes.data))
+        return logits
+
+    def greedy_next(self):
+        t = ctypes.c_uint32()
+        check(self.lib.rlh_greedy_next(self.model.h, self.h, ctypes.byref(t)))
+        return t.value
+
+    def generate_greedy(self, first, n_steps):
+        out = np.empty(n_steps + 1, dtype=np.uint32)
+        check(self.lib.rlh_generate_greedy(self.model.h, self.h, first, n_steps, out.ctypes.data))
+        return out
+
+    def set_debug(self, on):
+        check(self.lib.rlh_cache_set_debug(self.h, 1 if on else 0))
+
+    def layer_hidden(self, layer, n_tokens):
+        out = np.empty((n_tokens, self.model.spec.n_embd), dtype=np.float32)
+        check(self.lib.rlh_debug_layer_hidden(self.h, layer, out.ctypes.data, n_tokens))
+        return out
+
+    def read_kv(self, layer, which_v, n_pos):
+        s = self.model.spec
+        out = np.empty((n_pos, s.n_head_kv * s.head_dim), dtype=np.float32)
+        check(self.lib.rlh_cache_read_kv(self.h, layer, which_v, n_pos, out.ctypes.data))
+        return out
+
+
+def quantize_q8(x):
+    lib = load()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = len(x)
+    qs = np.empty(n, np.int8)
+    d = np.empty(n // 32, np.float32)
+    s = np.empty(n // 32, np.int32)
+    s16 = np.empty(n // 16, np.int32)
+    check(lib.rlh_quantize_q8(x.ctypes.data, n, qs.ctypes.data, d.ctypes.data, s.ctypes.data, s16.ctypes.data))
+    return qs, d, s, s16
+
+
+def dequant(ty, data, n):
+    out = np.empty(n, np.float32)
+    check(load().rlh_dequant(ty, np.ascontiguousarray(data).ctypes.data, n, out.ctypes.data))
+    return out
+
+
+def matvec(ty, w, rows, cols, x):
+    y = np.empty(rows, np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    check(load().rlh_matvec(ty, np.ascontiguousarray(w).ctypes.data, rows, cols, x.ctypes.data, y.ctypes.data))
+    return y
+
+
+def block_dots(ty, w, rows, cols, q8):
+    per = cols // 16 if ty == Q6_K else cols // 32
+    out = np.empty((rows, per), np.int32)
+    q8 = np.ascontiguousarray(q8, dtype=np.int8)
+    check(load().rlh_block_dots(ty, np.ascontiguousarray(w).ctypes.data, rows, cols, q8.ctypes.data,
+                                out.ctypes.data))
+    return out

@@ -1,0 +1,123 @@
+"""End-to-end parity of the device token loop against the CPU oracle.
+
+Reference modes: decode = the AVX2 integer path (ops.rs:93-128); prefill =
+RUST_LLAMA_BATCH_INT=1 (ops.rs:192-236). Bars from the north star:
+per-layer hidden states within 1e-3 relative L2, logits within 2e-3,
+identical greedy tokens. The device path is built to match bit for bit, and
+these tests assert that stronger property (the L2 numbers are printed).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import rlh
+from helpers import bits, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+_models = {}
+
+
+def _get(name, seed=1234):
+    key = (name, seed)
+    if key not in _models:
+        spec = rlh.SPECS[name]
+        tensors = rlh.synth_model(spec, seed)
+        _models[key] = (spec, tensors, rlh.Model(spec, tensors), oracle.OracleModel(spec, tensors))
+    return _models[key]
+
+
+def _greedy_ref(oc, prompt, n_gen):
+    """main.rs:500-516 loop on the oracle: argmax after every step."""
+    lib = oracle.load()
+    logits = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    toks = [lib.orc_argmax(logits.ctypes.data, len(logits))]
+    per_step = []
+    for i in range(n_gen):
+        lg = oc.forward_into(np.array([toks[-1]], np.uint32), len(prompt) + i, oracle.MODE_DEFAULT)
+        per_step.append(lg)
+        toks.append(lib.orc_argmax(lg.ctypes.data, len(lg)))
+    return logits, toks, per_step
+
+
+@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8_0", "tiny-q4_0", "tiny-q4km-untied", "small-q4km"])
+def test_prefill_and_decode_bit_exact(name):
+    print(f"forward parity {name}", flush=True)
+    spec, tensors, m, om = _get(name)
+    n_prompt, n_gen = 12, 10
+    prompt = rlh.synth_tokens(99, n_prompt, spec.vocab)
+    c = m.new_cache(64)
+    oc = om.new_cache(64)
+    c.set_debug(True)
+    oc.enable_dump(n_prompt)
+    logits = c.forward_into(prompt, 0)
+    ref_logits = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    print(f"  prefill logits rel L2 {rel_l2(logits, ref_logits):.3e}")
+    for l in range(spec.n_layer):
+        h = c.layer_hidden(l, n_prompt)
+        r = oc.hidden(l, n_prompt)
+        assert rel_l2(h, r) <= 1e-3
+        assert np.array_equal(bits(h), bits(r)), f"layer {l} hidden differs"
+    for l in range(spec.n_layer):
+        for which in (0, 1):
+            assert np.array_equal(bits(c.read_kv(l, which, n_prompt)), bits(oc.read_kv(l, which, n_prompt)))
+    assert rel_l2(logits, ref_logits) <= 2e-3
+    assert np.array_equal(bits(logits), bits(ref_logits))
+    assert c.len == n_prompt and oc.len == n_prompt
+
+    # decode: one step at a time through forward_into (n == 1 -> forward_one)
+    lib = oracle.load()
+    tok = lib.orc_argmax(ref_logits.ctypes.data, len(ref_logits))
+    assert c.greedy_next() == tok
+    for i in range(n_gen):
+        lg = c.forward_into(np.array([tok], np.uint32), n_prompt + i)
+        rg = oc.forward_into(np.array([tok], np.uint32), n_prompt + i, oracle.MODE_DEFAULT)
+        assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ (rel {rel_l2(lg, rg):.2e})"
+        tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+        assert c.greedy_next() == tok
+    c.close()
+    oc.close()
+
+
+@pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
+def test_generate_greedy_matches_cpu_tokens(name):
+    spec, tensors, m, om = _get(name)
+    prompt = rlh.synth_tokens(5, 9, spec.vocab)
+    n_gen = 24
+    c = m.new_cache(64)
+    oc = om.new_cache(64)
+    logits = c.forward_into(prompt, 0)
+    first = c.greedy_next()
+    toks = c.generate_greedy(first, n_gen)
+    _, ref_toks, _ = _greedy_ref(oc, prompt, n_gen)
+    assert list(map(int, toks)) == ref_toks
+    assert c.len == len(prompt) + n_gen
+    c.close()
+    oc.close()
+
+
+def test_forward_errors():
+    spec, tensors, m, om = _get("tiny-q4km")
+    c = m.new_cache(16)
+    with pytest.raises(rlh.RlhError) as e:
+        c.forward_into(np.array([spec.vocab], np.uint32), 0)
+    assert e.value.code == rlh.RLH_EINVAL
+    with pytest.raises(rlh.RlhError) as e:
+        c.forward_into(np.array([1], np.uint32), 16)
+    assert e.value.code == rlh.RLH_ECTX
+    # batch truncation to max_ctx - start_pos (model.rs:392)
+    c.forward_into(np.arange(20, dtype=np.uint32), 0)
+    assert c.len == 16
+    with pytest.raises(rlh.RlhError) as e:
+        c.generate_greedy(1, 4)
+    assert e.value.code == rlh.RLH_ECTX
+    c.reset()
+    assert c.len == 0
+    c.close()
+
+
+def test_cache_max_ctx_clamped_to_n_ctx():
+    spec, tensors, m, om = _get("tiny-q4km")
+    c = m.new_cache(10 ** 6)
+    assert c.max_ctx == spec.n_ctx
+    c.close()

@@ -1,0 +1,104 @@
+"""Op-level parity: HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: bit-exact for dequantisation, Q8 activation blocks and integer block
+dots, and bit-exact for the matvec rows too (the kernel
+sums the per-group terms in the reference order).
+"""
+import numpy as np
+import pytest
+
+import oracle
+import rlh
+from helpers import Q4_0, Q4_K, Q6_K, Q8_0, BLOCK, bits, random_activation, random_blocks
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [Q4_K, Q6_K, Q8_0, Q4_0]
+
+
+@pytest.mark.parametrize("kind", ["normal", "ties", "sparse"])
+@pytest.mark.parametrize("n", [32, 256, 4096, 12288])
+def test_quantize_q8_bit_exact(n, kind):
+    print(f"quantize_q8 n={n} kind={kind}", flush=True)
+    rng = np.random.default_rng(n + len(kind))
+    x = random_activation(n, rng, kind)
+    got = rlh.quantize_q8(x)
+    ref = oracle.quantize_q8(x, mode=1)  # AVX2 rounding (ties to even)
+    for g, r, name in zip(got, ref, ["qs", "scales", "sums", "sums16"]):
+        assert np.array_equal(np.asarray(g).view(np.uint8), np.asarray(r).view(np.uint8)), name
+
+
+def test_quantize_q8_zero_block():
+    x = np.zeros(64, np.float32)
+    x[40] = -3.0
+    qs, d, s, s16 = rlh.quantize_q8(x)
+    assert d[0] == 0.0 and not qs[:32].any() and s[0] == 0
+    rq, rd, rs, rs16 = oracle.quantize_q8(x, mode=1)
+    assert np.array_equal(qs, rq) and np.array_equal(bits(d), bits(rd))
+
+
+@pytest.mark.parametrize("ty", TYPES + [0, 1])
+def test_dequant_bit_exact(ty):
+    print(f"dequant ty={ty}", flush=True)
+    rng = np.random.default_rng(ty)
+    bs, ts = BLOCK[ty]
+    n = 4096
+    if ty == 0:
+        data = rng.standard_normal(n).astype(np.float32).view(np.uint8)
+    elif ty == 1:
+        data = rng.standard_normal(n).astype(np.float16).view(np.uint8)
+    else:
+        data = random_blocks(ty, n // bs, rng)
+    got = rlh.dequant(ty, data, n)
+    ref = oracle.dequant_row(ty, data, n)
+    assert np.array_equal(bits(got), bits(ref))
+
+
+@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("rows,cols", [(3, 256), (17, 1024), (64, 4096)])
+def test_block_dots_exact(ty, rows, cols):
+    print(f"block_dots ty={ty} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * cols + ty)
+    bs, ts = BLOCK[ty]
+    w = random_blocks(ty, rows * cols // bs, rng)
+    qs, _, _, _ = oracle.quantize_q8(rng.standard_normal(cols).astype(np.float32), mode=1)
+    got = rlh.block_dots(ty, w, rows, cols, qs)
+    ref = oracle.block_dots(ty, w, rows, cols, qs)
+    assert np.array_equal(got, ref)
+
+
+# Shapes of the Qwen3 matrices (0.6B .. 32B) at reduced row counts plus odd
+# row counts that leave partial row blocks.
+SHAPES = [(1, 256), (5, 512), (16, 1024), (33, 2048), (100, 2560), (64, 3072), (48, 4096), (7, 9728),
+          (20, 12288), (9, 25600)]
+
+
+@pytest.mark.parametrize("ty", TYPES)
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_matvec_bit_exact(ty, rows, cols):
+    print(f"matvec ty={ty} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows + cols + ty)
+    bs, ts = BLOCK[ty]
+    w = random_blocks(ty, rows * cols // bs, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = rlh.matvec(ty, w, rows, cols, x)
+    ref = oracle.matmul(ty, w, rows, cols, x, oracle.MODE_DEFAULT)  # AVX2 integer path
+    assert np.array_equal(bits(got), bits(ref)), f"max diff {np.max(np.abs(got - ref))}"
+
+
+def test_matvec_large_rows():
+    """A full 8B-size ffn_down-like matrix (4096 x 12288, Q6_K)."""
+    rng = np.random.default_rng(5)
+    rows, cols = 4096, 12288
+    w = random_blocks(Q6_K, rows * cols // 256, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = rlh.matvec(Q6_K, w, rows, cols, x)
+    ref = oracle.matmul(Q6_K, w, rows, cols, x, oracle.MODE_DEFAULT)
+    assert np.array_equal(bits(got), bits(ref))
+
+
+def test_matvec_rejects_bad_shape():
+    w = np.zeros(144, np.uint8)
+    with pytest.raises(rlh.RlhError) as e:
+        rlh.matvec(Q4_K, w, 1, 100, np.zeros(100, np.float32))
+    assert e.value.code == rlh.RLH_EINVAL
