@@ -179,10 +179,11 @@ int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t 
 int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
 
 /* ---- measurement ---------------------------------------------------------------------
- * Runs one resident weight matrix's decode matvec `iters` times on the
- * cache's stream and reports the average kernel duration (HIP events on that
- * stream) in microseconds. kind/layer select the tensor. */
-int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int layer, int iters, double* avg_us);
+ * Runs the decode matvec of one weight kind `iters` times on the cache's
+ * stream, rotating over the layers' copies of that matrix (so weights stream
+ * from HBM as in a decode step), and reports the average kernel duration in
+ * microseconds from a HIP event pair around each launch on that stream. */
+int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us);
 /* Average duration of one captured decode step (graph launch) over `iters`
  * steps at the cache's current length, in microseconds; the cache position
  * advances by `iters`. */

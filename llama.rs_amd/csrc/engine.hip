@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <thread>
@@ -18,11 +19,70 @@
 
 #include "../../include/rlh.h"
 #include "kernels.h"
+#include "attention.h"
+#include "matvec.h"
 #include "rlh_format.h"
 
 using namespace rlh;
 
 namespace {
+
+// ---- decode matvec launch plans ----------------------------------------------
+struct MvPlan {
+  MvLaunch L{};
+  uint32_t wgs = 0;
+  uint32_t lds = 0;
+  uint32_t ns = 1;  // row slots per lane, shared by the launch's segments
+};
+
+uint32_t mv_p(const DevMat& w) { return mv_pack(mv_units(w.ty, w.cols)); }
+
+// Row slots per lane for a matrix: the largest NS in {8, 4, 2, 1} that still
+// gives at least 512 blocks (R = 4 * NS * P rows each), so that even the
+// 1024-row K/V projections spread over every CU.
+uint32_t mv_pick_ns(const DevMat& w) {
+  uint32_t P = mv_p(w), ns = 8;
+  while (ns > 1 && (w.rows + 4 * ns * P - 1) / (4 * ns * P) < 512) ns /= 2;
+  while (ns > 1 && 4 * ns * P > 64) ns /= 2;
+  return ns;
+}
+
+void mv_lds(MvPlan& p, uint32_t R, uint32_t ty) {
+  p.lds = std::max(p.lds, 2 * R * (64 * mv_terms_per_unit(ty) + 4) * 4);
+}
+
+void mv_add(MvPlan& p, const DevMat& w, const Q8Buf& act, float* y, float* resid) {
+  MvSeg& g = p.L.seg[p.L.nseg++];
+  g = MvSeg{};
+  g.w = w;
+  g.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
+  g.y = y;
+  g.resid = resid;
+  g.rows_per_wg = 4 * p.ns * mv_p(w);
+  g.wg_begin = p.wgs;
+  p.wgs += (w.rows + g.rows_per_wg - 1) / g.rows_per_wg;
+  mv_lds(p, g.rows_per_wg, w.ty);
+}
+
+// gate/up rows in blocks of 32 with SwiGLU + Q8 of h in the epilogue. The
+// launch's NS must be 8 / P so that R = 32.
+void mv_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Buf& act, const Q8Buf& hq, float* h) {
+  MvSeg& g = p.L.seg[p.L.nseg++];
+  g = MvSeg{};
+  g.w = gate;
+  g.w2 = up;
+  g.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
+  g.y = h;
+  g.hq = hq;
+  g.pair = 1;
+  g.rows_per_wg = 32;
+  g.wg_begin = p.wgs;
+  p.wgs += gate.rows / 32;
+  mv_lds(p, 32, gate.ty);
+  mv_lds(p, 32, up.ty);
+}
+
+void mv_run(hipStream_t st, const MvPlan& p) { launch_mv(st, p.L, p.wgs, p.lds, p.ns); }
 
 thread_local std::string g_err;
 
@@ -216,6 +276,11 @@ int ensure_device() {
   hipError_t e = hipGetDeviceCount(&n);
   if (e != hipSuccess || n == 0)
     return fail(RLH_EDEVICE, "no HIP device available (librlh needs an MI355X / gfx950 GPU)");
+  static bool lds_set = false;
+  if (!lds_set) {
+    if (!mv_set_max_lds(150 * 1024)) return fail(RLH_EDEVICE, "matvec LDS attribute");
+    lds_set = true;
+  }
   return RLH_OK;
 }
 
@@ -239,6 +304,8 @@ struct rlh_cache {
   // workspace for one token
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *g = nullptr, *u = nullptr,
         *logits = nullptr, *scratch = nullptr;
+  float* scores = nullptr;  // attention scores [H][max_ctx]
+  uint32_t vtile = 0;       // V positions per LDS tile of the attention output kernel
   Q8Buf act_e{}, act_q{}, act_f{};
   // step state (device): tok, pos, step, argmax out
   uint32_t* st_dev = nullptr;  // [0]=tok [1]=pos [2]=step [3]=argmax
@@ -249,6 +316,7 @@ struct rlh_cache {
   uint32_t* host_st = nullptr;  // pinned staging for tok/pos
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
   bool debug = false;
+  bool use_graphs = true;  // RLH_GRAPHS=0 launches the same kernels eagerly
   float* dbg = nullptr;  // [L][kDbgTokens][E]
   uint64_t dbg_tokens = 0;
   bool logits_valid = false;
@@ -275,7 +343,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   rlh_model* m = c->m;
   const rlh_config& cfg = m->cfg;
   hipStream_t st = c->st;
-  const uint32_t E = cfg.n_embd, F = cfg.n_ff, H = cfg.n_head, KVH = cfg.n_head_kv, hd = cfg.head_dim;
+  const uint32_t E = cfg.n_embd, H = cfg.n_head, KVH = cfg.n_head_kv, hd = cfg.head_dim;
   const float eps = cfg.rms_eps;
   const float scale = 1.0f / std::sqrt((float)hd);  // model.rs:616
   uint32_t* tok = c->st_dev;
@@ -284,20 +352,60 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   for (uint32_t l = 0; l < cfg.n_layer; l++) {
     Layer& L = m->layers[l];
     launch_rmsnorm_q8(st, c->x, L.attn_norm.p, E, 1, eps, c->act_e, nullptr);
-    launch_matvec(st, L.q.dm, c->act_e, c->q, nullptr);
-    launch_matvec(st, L.k.dm, c->act_e, c->k, nullptr);
-    launch_matvec(st, L.v.dm, c->act_e, c->v, nullptr);
-    launch_qk_norm_rope_kv(st, c->q, c->k, c->v, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
-                           cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
-                           (int)H, (int)KVH, 1, eps);
-    launch_attention(st, c->q, layer_k(c, l), layer_v(c, l), pos, (int)H, (int)KVH, 1, (uint32_t)c->max_ctx, scale,
-                     c->attn, c->act_q);
-    launch_matvec(st, L.o.dm, c->act_q, nullptr, c->x);
+    {
+      MvPlan p;
+      p.ns = mv_pick_ns(L.q.dm);
+      mv_add(p, L.q.dm, c->act_e, c->q, nullptr);
+      mv_add(p, L.k.dm, c->act_e, c->k, nullptr);
+      mv_add(p, L.v.dm, c->act_e, c->v, nullptr);
+      mv_run(st, p);
+    }
+    {
+      AttnArgs a{};
+      a.q = c->q;
+      a.k = c->k;
+      a.v = c->v;
+      a.bq = L.bq.p;
+      a.bk = L.bk.p;
+      a.bv = L.bv.p;
+      a.qn = cfg.has_qk_norm ? L.q_norm.p : nullptr;
+      a.kn = cfg.has_qk_norm ? L.k_norm.p : nullptr;
+      a.rope_cs = m->rope_cs;
+      a.pos0 = pos;
+      a.kcache = layer_k(c, l);
+      a.vcache = layer_v(c, l);
+      a.scores = c->scores;
+      a.t_stride = (uint32_t)c->max_ctx;
+      a.t_max = (uint32_t)c->max_ctx;
+      a.vtile = c->vtile;
+      a.H = (int)H;
+      a.KVH = (int)KVH;
+      a.eps = eps;
+      a.scale = scale;
+      a.out = c->attn;
+      a.out_q8 = c->act_q;
+      launch_attn_scores(st, a, 1, true);
+      launch_attn_out(st, a, 1);
+    }
+    {
+      MvPlan p;
+      p.ns = mv_pick_ns(L.o.dm);
+      mv_add(p, L.o.dm, c->act_q, nullptr, c->x);
+      mv_run(st, p);
+    }
     launch_rmsnorm_q8(st, c->x, L.ffn_norm.p, E, 1, eps, c->act_e, nullptr);
-    launch_matvec(st, L.gate.dm, c->act_e, c->g, nullptr);
-    launch_matvec(st, L.up.dm, c->act_e, c->u, nullptr);
-    launch_swiglu_q8(st, c->g, c->u, F, c->act_f, nullptr);
-    launch_matvec(st, L.down.dm, c->act_f, nullptr, c->x);
+    {
+      MvPlan p;
+      p.ns = 8 / mv_p(L.gate.dm);
+      mv_add_pair(p, L.gate.dm, L.up.dm, c->act_e, c->act_f, nullptr);
+      mv_run(st, p);
+    }
+    {
+      MvPlan p;
+      p.ns = mv_pick_ns(L.down.dm);
+      mv_add(p, L.down.dm, c->act_f, nullptr, c->x);
+      mv_run(st, p);
+    }
     if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
       (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
                            st);
@@ -305,7 +413,12 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   if (kind == STEP_NOLOGITS) return;
   launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
-  launch_matvec(st, ow.dm, c->act_e, c->logits, nullptr);
+  {
+    MvPlan p;
+    p.ns = mv_pick_ns(ow.dm);
+    mv_add(p, ow.dm, c->act_e, c->logits, nullptr);
+    mv_run(st, p);
+  }
   if (kind == STEP_GREEDY)
     launch_argmax(st, c->logits, cfg.vocab_size, c->pv, c->pi, c->nparts, tok, pos, c->st_dev + 2, c->hist);
 }
@@ -322,7 +435,7 @@ int capture(rlh_cache* c, StepKind kind, hipGraphExec_t* out) {
 }
 
 int run_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
-  if (c->debug) {
+  if (c->debug || !c->use_graphs) {
     enqueue_step(c, kind, dbg_slot);
     HIPCHK(hipGetLastError());
     return RLH_OK;
@@ -526,7 +639,7 @@ static void cache_free(rlh_cache* c) {
   if (c->g_logits) (void)hipGraphExecDestroy(c->g_logits);
   if (c->g_nologits) (void)hipGraphExecDestroy(c->g_nologits);
   if (c->g_greedy) (void)hipGraphExecDestroy(c->g_greedy);
-  void* ptrs[] = {c->kc, c->vc, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
+  void* ptrs[] = {c->kc, c->vc, c->scores, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
                   c->act_e.qs, c->act_e.d, c->act_e.s, c->act_e.s16, c->act_q.qs, c->act_q.d, c->act_q.s,
                   c->act_q.s16, c->act_f.qs, c->act_f.d, c->act_f.s, c->act_f.s16, c->st_dev, c->hist, c->pv,
                   c->pi, c->dbg};
@@ -551,16 +664,19 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   const rlh_config& cfg = m->cfg;
   max_ctx = std::min<uint64_t>(max_ctx, cfg.n_ctx);  // model.rs:340
   if (max_ctx == 0) return fail(RLH_EINVAL, "max_ctx is 0");
-  size_t lds = (size_t)max_ctx * 4;
-  if (lds > 150 * 1024) return fail(RLH_EUNSUP, "max_ctx above 38400 is not supported by the attention kernel");
-  if (!attention_set_max_lds(std::max<size_t>(lds, 64 * 1024))) return fail(RLH_EDEVICE, "attention LDS attribute");
+  if (max_ctx > 32768) return fail(RLH_EUNSUP, "max_ctx above 32768 is not supported by the attention kernels");
+  if (cfg.n_head / cfg.n_head_kv > 8) return fail(RLH_EUNSUP, "more than 8 query heads per KV head");
+  uint32_t vtile = attn_vtile((uint32_t)max_ctx);
+  if (!attn_set_max_lds(attn_out_lds((uint32_t)max_ctx, vtile))) return fail(RLH_EDEVICE, "attention LDS attribute");
   rlh_cache* c = new rlh_cache();
   c->m = m;
   c->max_ctx = max_ctx;
+  c->vtile = vtile;
   uint64_t E = cfg.n_embd, F = cfg.n_ff, qd = (uint64_t)cfg.n_head * cfg.head_dim,
            kvd = (uint64_t)cfg.n_head_kv * cfg.head_dim;
   size_t kvbytes = (size_t)cfg.n_layer * max_ctx * kvd * 4;
   bool ok = hipStreamCreate(&c->st) == hipSuccess && hipMalloc((void**)&c->kc, kvbytes) == hipSuccess &&
+            hipMalloc((void**)&c->scores, (size_t)cfg.n_head * max_ctx * 4) == hipSuccess &&
             hipMalloc((void**)&c->vc, kvbytes) == hipSuccess && hipMalloc((void**)&c->x, E * 4) == hipSuccess &&
             hipMalloc((void**)&c->q, qd * 4) == hipSuccess && hipMalloc((void**)&c->k, kvd * 4) == hipSuccess &&
             hipMalloc((void**)&c->v, kvd * 4) == hipSuccess && hipMalloc((void**)&c->attn, qd * 4) == hipSuccess &&
@@ -588,8 +704,11 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
     cache_free(c);
     return fail(RLH_EDEVICE, "cache init");
   }
-  if ((rc = capture(c, STEP_LOGITS, &c->g_logits)) || (rc = capture(c, STEP_NOLOGITS, &c->g_nologits)) ||
-      (rc = capture(c, STEP_GREEDY, &c->g_greedy))) {
+  const char* env = std::getenv("RLH_GRAPHS");
+  c->use_graphs = !(env && std::strcmp(env, "0") == 0);
+  if (c->use_graphs &&
+      ((rc = capture(c, STEP_LOGITS, &c->g_logits)) || (rc = capture(c, STEP_NOLOGITS, &c->g_nologits)) ||
+       (rc = capture(c, STEP_GREEDY, &c->g_greedy)))) {
     std::string msg = g_err;
     cache_free(c);
     return fail(rc, msg);
@@ -806,7 +925,12 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
   Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
   hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
   launch_quantize_q8(st, dx.p, (uint32_t)cols, act);
-  launch_matvec(st, t.dm, act, dy.p, nullptr);
+  {
+    MvPlan p;
+    p.ns = mv_pick_ns(t.dm);
+    mv_add(p, t.dm, act, dy.p, nullptr);
+    mv_run(st, p);
+  }
   if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(y, dy.p, rows * 4, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -867,30 +991,47 @@ static const DevTensor* find_matrix(rlh_model* m, int kind, int layer) {
   }
 }
 
-int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int layer, int iters, double* avg_us) {
+int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us) {
   int rc = check_forward_args(m, c);
   if (rc) return rc;
   if (!avg_us || iters <= 0) return fail(RLH_EINVAL, "bad argument");
-  const DevTensor* t = find_matrix(m, kind, layer);
-  if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
-  const Q8Buf& act = t->cols == m->cfg.n_ff ? c->act_f
-                     : t->cols == (uint64_t)m->cfg.n_head * m->cfg.head_dim ? c->act_q
-                                                                           : c->act_e;
-  if (t->cols != m->cfg.n_embd && t->cols != m->cfg.n_ff && t->cols != (uint64_t)m->cfg.n_head * m->cfg.head_dim)
+  // Rotate over every layer's copy of the matrix so that, as in a decode
+  // step, each launch streams its weights from HBM rather than from the
+  // 256 MB last-level cache a single re-launched matrix would sit in.
+  std::vector<const DevTensor*> mats;
+  bool global = kind == RLH_T_OUTPUT || kind == RLH_T_TOKEN_EMBD;
+  for (uint32_t l = 0; l < (global ? 1u : m->cfg.n_layer); l++) {
+    const DevTensor* t = find_matrix(m, kind, (int)l);
+    if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
+    mats.push_back(t);
+  }
+  uint64_t qd = (uint64_t)m->cfg.n_head * m->cfg.head_dim;
+  uint64_t cols = mats[0]->cols;
+  if (cols != m->cfg.n_embd && cols != m->cfg.n_ff && cols != qd)
     return fail(RLH_EINVAL, "matrix width matches no activation buffer");
-  hipEvent_t e0, e1;
-  HIPCHK(hipEventCreate(&e0));
-  HIPCHK(hipEventCreate(&e1));
-  launch_matvec(c->st, t->dm, act, c->scratch, nullptr);  // warm-up
-  HIPCHK(hipEventRecord(e0, c->st));
-  for (int i = 0; i < iters; i++) launch_matvec(c->st, t->dm, act, c->scratch, nullptr);
-  HIPCHK(hipEventRecord(e1, c->st));
-  HIPCHK(hipEventSynchronize(e1));
-  float ms = 0.f;
-  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
-  (void)hipEventDestroy(e0);
-  (void)hipEventDestroy(e1);
-  *avg_us = (double)ms * 1000.0 / iters;
+  const Q8Buf& act = cols == m->cfg.n_ff ? c->act_f : (cols == qd ? c->act_q : c->act_e);
+  std::vector<hipEvent_t> ev(2 * (size_t)iters);
+  for (auto& e : ev) HIPCHK(hipEventCreate(&e));
+  std::vector<MvPlan> plans(mats.size());
+  for (size_t i = 0; i < mats.size(); i++) {
+    plans[i].ns = mv_pick_ns(mats[i]->dm);
+    mv_add(plans[i], mats[i]->dm, act, c->scratch, nullptr);
+  }
+  mv_run(c->st, plans[0]);  // warm-up
+  for (int i = 0; i < iters; i++) {
+    HIPCHK(hipEventRecord(ev[2 * i], c->st));
+    mv_run(c->st, plans[i % plans.size()]);
+    HIPCHK(hipEventRecord(ev[2 * i + 1], c->st));
+  }
+  HIPCHK(hipStreamSynchronize(c->st));
+  double total = 0.0;
+  for (int i = 0; i < iters; i++) {
+    float ms = 0.f;
+    HIPCHK(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+    total += ms;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  *avg_us = total * 1000.0 / iters;
   return RLH_OK;
 }
 
@@ -909,7 +1050,8 @@ int rlh_profile_decode(rlh_model* m, rlh_cache* c, int iters, double* avg_us) {
   HIPCHK(hipEventCreate(&e0));
   HIPCHK(hipEventCreate(&e1));
   HIPCHK(hipEventRecord(e0, c->st));
-  for (int i = 0; i < iters; i++) HIPCHK(hipGraphLaunch(c->g_greedy, c->st));
+  for (int i = 0; i < iters; i++)
+    if ((rc = run_step(c, STEP_GREEDY, -1))) return rc;
   HIPCHK(hipEventRecord(e1, c->st));
   HIPCHK(hipEventSynchronize(e1));
   float ms = 0.f;

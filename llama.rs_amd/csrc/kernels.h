@@ -7,14 +7,10 @@
 
 namespace rlh {
 
-// Q8 activation rows in device memory (Q8Row, simd.rs:88-101), token-major:
-// qs[n][cols], d[n][cols/32], s[n][cols/32], s16[n][cols/16].
-struct Q8Buf {
-  int8_t* qs;
-  float* d;
-  int32_t* s;
-  int32_t* s16;
-};
+using Q8Buf = Q8Mut;
+
+// Largest hidden size the single-block row kernels (rmsnorm) stage in LDS.
+constexpr int kMaxEmbd = 7168;
 
 bool matvec_supported(uint32_t ty);
 
@@ -22,7 +18,6 @@ void launch_embed(hipStream_t st, const DevMat& w, const uint32_t* tok, uint32_t
 void launch_rmsnorm_q8(hipStream_t st, const float* x, const float* w, uint32_t n, uint32_t n_tok, float eps,
                        const Q8Buf& out, float* xb);
 void launch_quantize_q8(hipStream_t st, const float* x, uint32_t n, const Q8Buf& out);
-void launch_matvec(hipStream_t st, const DevMat& w, const Q8Buf& act, float* y, float* resid);
 void launch_block_dots(hipStream_t st, const DevMat& w, const int8_t* a, int32_t* out, uint32_t per_row);
 void launch_dequant(hipStream_t st, const DevMat& w, float* out);
 void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, const float* bq, const float* bk,

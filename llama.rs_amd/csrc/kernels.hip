@@ -31,24 +31,57 @@ __global__ void __launch_bounds__(256) k_embed(DevMat w, const uint32_t* tok, fl
 __global__ void __launch_bounds__(256) k_rmsnorm_q8(const float* x, const float* w, int n, float eps, Q8Out out,
                                                     float* xb) {
   __shared__ float s_scale;
+  __shared__ __attribute__((aligned(16))) float xs_generic[kMaxEmbd];
+  RLH_LDS float* xs = (RLH_LDS float*)xs_generic;
+  constexpr int kV = kMaxEmbd / 4 / 256;  // float4 of the row per thread
   const float* xt = x + (size_t)blockIdx.x * n;
+  const int n4 = n / 4;
+  // Every global load is issued up front (registers), then the row is staged
+  // in LDS for the 32 sequential FMA chains of the sum of squares.
+  float4 xr[kV], wr[kV];
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < n4) {
+      xr[k] = ld_gf4(xt + 4 * i);
+      wr[k] = ld_gf4(w + 4 * i);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < n4) {
+      xs[4 * i] = xr[k].x;
+      xs[4 * i + 1] = xr[k].y;
+      xs[4 * i + 2] = xr[k].z;
+      xs[4 * i + 3] = xr[k].w;
+    }
+  }
+  __syncthreads();
   if (threadIdx.x < 64) {
-    float ss = rms_sumsq_wave(xt, n);
+    float ss = rms_sumsq_lds(xs, n);
     if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
   __syncthreads();
-  float s = s_scale;
-  uint32_t nb = (uint32_t)n / 32;
+  const float s = s_scale;
+  const uint32_t nb = (uint32_t)n / 32;
   Q8Out o{out.qs + (size_t)blockIdx.x * n, out.d + (size_t)blockIdx.x * nb, out.s + (size_t)blockIdx.x * nb,
           out.s16 + (size_t)blockIdx.x * nb * 2};
-  // 8 blocks of 32 per pass (two per wave).
-  for (uint32_t base = 0; base < (uint32_t)n; base += 256) {
-    uint32_t i = base + threadIdx.x;
-    // Waves whose 32-lane halves are past the end skip the pass as a whole half.
-    if (base + (threadIdx.x & ~31u) < (uint32_t)n) {
-      float v = (xt[i] * s) * w[i];
-      if (xb) xb[(size_t)blockIdx.x * n + i] = v;
-      q8_quant_block32(v, o, i / 32);
+  // xb = (x * s) * w; 8 consecutive threads hold one Q8 block (4 values each).
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const int i = threadIdx.x + 256 * k;
+    if (i < n4) {  // n4 is a multiple of 8: whole 8-lane groups
+      const float v0 = (xr[k].x * s) * wr[k].x, v1 = (xr[k].y * s) * wr[k].y;
+      const float v2 = (xr[k].z * s) * wr[k].z, v3 = (xr[k].w * s) * wr[k].w;
+      if (xb) {
+        float* xo = xb + (size_t)blockIdx.x * n + 4 * i;
+        xo[0] = v0;
+        xo[1] = v1;
+        xo[2] = v2;
+        xo[3] = v3;
+      }
+      q8_quant_block8x4(v0, v1, v2, v3, o, (uint32_t)i / 8);
     }
   }
 }
@@ -58,185 +91,6 @@ __global__ void __launch_bounds__(256) k_quantize_q8(const float* x, uint32_t n,
   uint32_t i = blockIdx.x * 256 + threadIdx.x;
   if (blockIdx.x * 256 + (threadIdx.x & ~31u) >= n) return;  // whole 32-lane halves
   q8_quant_block32(x[i], out, i / 32);
-}
-
-// ---------------------------------------------------------------------------
-// Decode matvec y = W x (ops.rs:67-141, integer path), exact in the reference
-// order: each row's f32 total is the sequential sum, in index order, of the
-// per-group terms of dot_q4k_q8_avx2 (simd.rs:581), dot_q6k_q8_avx2
-// (simd.rs:663), dot_q80_q8_avx2 (simd.rs:891) or dot_q40_q8_avx2
-// (simd.rs:863). Threads compute terms (coalesced over the row's blocks),
-// stage them in LDS, and lane r of the block chains row r's terms in order.
-// ---------------------------------------------------------------------------
-struct Q8In {
-  const int8_t* qs;
-  const float* d;
-  const int32_t* s;
-  const int32_t* s16;
-};
-
-template <uint32_t TY>
-struct Unit;
-
-// Q4_K: unit = group g of super-block bi -> 1 term (64 weights).
-template <>
-struct Unit<RLH_TYPE_Q4_K> {
-  static constexpr int kTerms = 1;
-  __device__ static uint32_t units(uint32_t cols) { return cols / 64; }
-  __device__ static void run(const DevMat& w, const Q8In& act, uint32_t row, uint32_t u, float* t) {
-    uint32_t bi = u >> 2, g = u & 3;
-    const uint8_t* sb = w.a + (size_t)row * w.row_bytes + (size_t)bi * 144;
-    uint4 hdr = *(const uint4*)sb;
-    uint4 q0 = *(const uint4*)(sb + 16 + 32 * g);
-    uint4 q1 = *(const uint4*)(sb + 32 + 32 * g);
-    uint32_t ab = bi * 8 + 2 * g;
-    const uint4* ap = (const uint4*)(act.qs + (size_t)ab * 32);
-    uint4 a0 = ap[0], a1 = ap[1], b0 = ap[2], b1 = ap[3];
-    const uint32_t m = 0x0F0F0F0Fu;
-    int i1 = 0, i2 = 0;
-    i1 = sdot4(q0.x & m, a0.x, i1); i1 = sdot4(q0.y & m, a0.y, i1);
-    i1 = sdot4(q0.z & m, a0.z, i1); i1 = sdot4(q0.w & m, a0.w, i1);
-    i1 = sdot4(q1.x & m, a1.x, i1); i1 = sdot4(q1.y & m, a1.y, i1);
-    i1 = sdot4(q1.z & m, a1.z, i1); i1 = sdot4(q1.w & m, a1.w, i1);
-    i2 = sdot4((q0.x >> 4) & m, b0.x, i2); i2 = sdot4((q0.y >> 4) & m, b0.y, i2);
-    i2 = sdot4((q0.z >> 4) & m, b0.z, i2); i2 = sdot4((q0.w >> 4) & m, b0.w, i2);
-    i2 = sdot4((q1.x >> 4) & m, b1.x, i2); i2 = sdot4((q1.y >> 4) & m, b1.y, i2);
-    i2 = sdot4((q1.z >> 4) & m, b1.z, i2); i2 = sdot4((q1.w >> 4) & m, b1.w, i2);
-    float d = f16_to_f32(hdr.x & 0xffff);
-    float dmin = f16_to_f32(hdr.x >> 16);
-    uint8_t sc12[12];
-    *(uint32_t*)(sc12) = hdr.y;
-    *(uint32_t*)(sc12 + 4) = hdr.z;
-    *(uint32_t*)(sc12 + 8) = hdr.w;
-    uint32_t sc1, m1, sc2, m2;
-    scale_min_k4((int)(2 * g), sc12, sc1, m1);
-    scale_min_k4((int)(2 * g + 1), sc12, sc2, m2);
-    float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
-    float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
-    float sa = (float)act.s[ab], sb2 = (float)act.s[ab + 1];
-    float da = act.d[ab], db = act.d[ab + 1];
-    t[0] = da * (d1 * (float)i1 - mm1 * sa) + db * (d2 * (float)i2 - mm2 * sb2);
-  }
-};
-
-// Q6_K: unit = (bi, half, sub) -> 4 terms c = 0..3 (16 weights each), in the
-// reference's loop order half { sub { c } } (simd.rs:617-665).
-template <>
-struct Unit<RLH_TYPE_Q6_K> {
-  static constexpr int kTerms = 4;
-  __device__ static uint32_t units(uint32_t cols) { return cols / 64; }
-  __device__ static void run(const DevMat& w, const Q8In& act, uint32_t row, uint32_t u, float* t) {
-    uint32_t nsb = w.cols >> 8;
-    uint32_t bi = u >> 2, half = (u >> 1) & 1, sub = u & 1;
-    size_t sbi = (size_t)row * nsb + bi;
-    const uint8_t* ql = w.a + sbi * 128 + half * 64 + sub * 16;
-    uint4 ql0 = *(const uint4*)ql;
-    uint4 ql1 = *(const uint4*)(ql + 32);
-    uint4 qh = *(const uint4*)(w.b + sbi * 64 + half * 32 + sub * 16);
-    const int8_t* sc = (const int8_t*)(w.c + sbi * 16 + half * 8 + sub);
-    const uint8_t* dp = w.d + sbi * 2;
-    float d = f16_to_f32(dp[0] | (dp[1] << 8));
-    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
-    uint32_t l0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
-    uint32_t l1[4] = {ql1.x, ql1.y, ql1.z, ql1.w};
-    uint32_t h[4] = {qh.x, qh.y, qh.z, qh.w};
-    uint32_t ab = bi * 8 + half * 4;
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const uint4 a = *(const uint4*)(act.qs + (size_t)(ab + c) * 32 + sub * 16);
-      uint32_t av[4] = {a.x, a.y, a.z, a.w};
-      int ss = 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        uint32_t lo = (c & 1) ? l1[k] : l0[k];
-        uint32_t nib = (c < 2) ? (lo & m4) : ((lo >> 4) & m4);
-        uint32_t uu = nib | (((h[k] >> (2 * c)) & m2) << 4);
-        ss = sdot4(uu, av[k], ss);
-      }
-      float scf = (float)sc[2 * c];
-      float sa = (float)act.s16[(size_t)(ab + c) * 2 + sub];
-      float da = act.d[ab + c];
-      t[c] = d * scf * ((float)ss - 32.0f * sa) * da;
-    }
-  }
-};
-
-// Q8_0: unit = one 32-block -> 1 term (simd.rs:874-894).
-template <>
-struct Unit<RLH_TYPE_Q8_0> {
-  static constexpr int kTerms = 1;
-  __device__ static uint32_t units(uint32_t cols) { return cols / 32; }
-  __device__ static void run(const DevMat& w, const Q8In& act, uint32_t row, uint32_t u, float* t) {
-    uint32_t nb = w.cols >> 5;
-    size_t b = (size_t)row * nb + u;
-    const uint4* qp = (const uint4*)(w.a + b * 32);
-    uint4 q0 = qp[0], q1 = qp[1];
-    const uint4* ap = (const uint4*)(act.qs + (size_t)u * 32);
-    uint4 a0 = ap[0], a1 = ap[1];
-    int i = 0;
-    i = sdot4(q0.x, a0.x, i); i = sdot4(q0.y, a0.y, i); i = sdot4(q0.z, a0.z, i); i = sdot4(q0.w, a0.w, i);
-    i = sdot4(q1.x, a1.x, i); i = sdot4(q1.y, a1.y, i); i = sdot4(q1.z, a1.z, i); i = sdot4(q1.w, a1.w, i);
-    float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
-    t[0] = d * (float)i * act.d[u];
-  }
-};
-
-// Q4_0: unit = one 32-block -> 1 term (simd.rs:844-866).
-template <>
-struct Unit<RLH_TYPE_Q4_0> {
-  static constexpr int kTerms = 1;
-  __device__ static uint32_t units(uint32_t cols) { return cols / 32; }
-  __device__ static void run(const DevMat& w, const Q8In& act, uint32_t row, uint32_t u, float* t) {
-    uint32_t nb = w.cols >> 5;
-    size_t b = (size_t)row * nb + u;
-    uint4 q = *(const uint4*)(w.a + b * 16);
-    const uint4* ap = (const uint4*)(act.qs + (size_t)u * 32);
-    uint4 a0 = ap[0], a1 = ap[1];
-    const uint32_t m = 0x0F0F0F0Fu;
-    int i0 = 0, i1 = 0;
-    i0 = sdot4(q.x & m, a0.x, i0); i0 = sdot4(q.y & m, a0.y, i0);
-    i0 = sdot4(q.z & m, a0.z, i0); i0 = sdot4(q.w & m, a0.w, i0);
-    i1 = sdot4((q.x >> 4) & m, a1.x, i1); i1 = sdot4((q.y >> 4) & m, a1.y, i1);
-    i1 = sdot4((q.z >> 4) & m, a1.z, i1); i1 = sdot4((q.w >> 4) & m, a1.w, i1);
-    float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
-    t[0] = d * (float)(i0 + i1 - 8 * act.s[u]) * act.d[u];
-  }
-};
-
-constexpr int kMvRows = 16;   // rows per block
-constexpr int kMvUnits = 64;  // units per LDS chunk
-
-// y[r] = sum of terms (or resid[r] = resid[r] + sum when resid != nullptr).
-template <uint32_t TY>
-__global__ void __launch_bounds__(256) k_matvec(DevMat w, Q8In act, float* y, float* resid) {
-  constexpr int T = Unit<TY>::kTerms;
-  __shared__ float terms[kMvRows][kMvUnits * T + 1];
-  const uint32_t r0 = blockIdx.x * kMvRows;
-  const uint32_t U = Unit<TY>::units(w.cols);
-  float acc = 0.0f;
-  for (uint32_t c0 = 0; c0 < U; c0 += kMvUnits) {
-    uint32_t cn = U - c0 < (uint32_t)kMvUnits ? U - c0 : (uint32_t)kMvUnits;
-    for (uint32_t idx = threadIdx.x; idx < (uint32_t)(kMvRows * kMvUnits); idx += 256) {
-      uint32_t rl = idx / kMvUnits, uu = idx % kMvUnits;
-      uint32_t r = r0 + rl;
-      if (r < w.rows && uu < cn) Unit<TY>::run(w, act, r, c0 + uu, &terms[rl][uu * T]);
-    }
-    __syncthreads();
-    if (threadIdx.x < (uint32_t)kMvRows) {
-      const float* tr = terms[threadIdx.x];
-      for (uint32_t k = 0; k < cn * T; k++) acc = acc + tr[k];
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x < (uint32_t)kMvRows) {
-    uint32_t r = r0 + threadIdx.x;
-    if (r < w.rows) {
-      if (resid)
-        resid[r] = resid[r] + acc;
-      else
-        y[r] = acc;
-    }
-  }
 }
 
 // Exact integer partial dots for the op-level parity entry (one thread per
@@ -538,7 +392,6 @@ __global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const uin
 // ---------------------------------------------------------------------------
 // Launch wrappers
 // ---------------------------------------------------------------------------
-static inline Q8In q8in(const Q8Buf& b) { return Q8In{b.qs, b.d, b.s, b.s16}; }
 static inline Q8Out q8out(const Q8Buf& b) { return Q8Out{b.qs, b.d, b.s, b.s16}; }
 
 void launch_embed(hipStream_t st, const DevMat& w, const uint32_t* tok, uint32_t n_tok, float* x) {
@@ -557,17 +410,6 @@ void launch_quantize_q8(hipStream_t st, const float* x, uint32_t n, const Q8Buf&
 
 bool matvec_supported(uint32_t ty) {
   return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
-}
-
-void launch_matvec(hipStream_t st, const DevMat& w, const Q8Buf& act, float* y, float* resid) {
-  dim3 grid((w.rows + kMvRows - 1) / kMvRows);
-  switch (w.ty) {
-    case RLH_TYPE_Q4_K: hipLaunchKernelGGL(k_matvec<RLH_TYPE_Q4_K>, grid, dim3(256), 0, st, w, q8in(act), y, resid); break;
-    case RLH_TYPE_Q6_K: hipLaunchKernelGGL(k_matvec<RLH_TYPE_Q6_K>, grid, dim3(256), 0, st, w, q8in(act), y, resid); break;
-    case RLH_TYPE_Q8_0: hipLaunchKernelGGL(k_matvec<RLH_TYPE_Q8_0>, grid, dim3(256), 0, st, w, q8in(act), y, resid); break;
-    case RLH_TYPE_Q4_0: hipLaunchKernelGGL(k_matvec<RLH_TYPE_Q4_0>, grid, dim3(256), 0, st, w, q8in(act), y, resid); break;
-    default: break;
-  }
 }
 
 void launch_block_dots(hipStream_t st, const DevMat& w, const int8_t* a, int32_t* out, uint32_t per_row) {

@@ -10,6 +10,12 @@
 
 #include "rlh_format.h"
 
+// Explicit address spaces: pointers reaching a kernel inside a by-value
+// struct are generic, and generic (flat) loads share the LDS wait counter,
+// which would make every LDS access wait for all outstanding HBM loads.
+#define RLH_GLOBAL __attribute__((address_space(1)))
+#define RLH_LDS __attribute__((address_space(3)))
+
 namespace rlh {
 
 // ---------------------------------------------------------------------------
@@ -114,12 +120,7 @@ __device__ __forceinline__ int cvtps_packs_i8(float r) {
   return v > 127 ? 127 : (v < -128 ? -128 : v);
 }
 
-struct Q8Out {
-  int8_t* qs;      // [n]
-  float* d;        // [n/32]
-  int32_t* s;      // [n/32]
-  int32_t* s16;    // [n/16]
-};
+using Q8Out = Q8Mut;
 
 __device__ __forceinline__ void q8_quant_block32(float v, Q8Out o, uint32_t blk) {
   int l = threadIdx.x & 31;
@@ -143,6 +144,64 @@ __device__ __forceinline__ void q8_quant_block32(float v, Q8Out o, uint32_t blk)
   }
 }
 
+// quantize_q8 of one 32-value block held as 4 consecutive values per lane in
+// 8 consecutive lanes (lane & 7 = which 4 values). Same arithmetic as
+// q8_quant_block32; stores 4 packed bytes per lane.
+__device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, float v3, Q8Out o, uint32_t blk) {
+  const int l = threadIdx.x & 7;
+  float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+  a = fmaxf(a, __shfl_xor(a, 1, 8));
+  a = fmaxf(a, __shfl_xor(a, 2, 8));
+  a = fmaxf(a, __shfl_xor(a, 4, 8));
+  const float d = a / 127.0f;
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  const int q0 = cvtps_packs_i8(__builtin_rintf(v0 * inv));
+  const int q1 = cvtps_packs_i8(__builtin_rintf(v1 * inv));
+  const int q2 = cvtps_packs_i8(__builtin_rintf(v2 * inv));
+  const int q3 = cvtps_packs_i8(__builtin_rintf(v3 * inv));
+  int s = q0 + q1 + q2 + q3;
+  s = s + __shfl_xor(s, 1, 8);
+  s = s + __shfl_xor(s, 2, 8);  // sum of the 16-value half (lanes 0-3 / 4-7)
+  const int tot = s + __shfl_xor(s, 4, 8);
+  const uint32_t packed =
+      (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
+  *(RLH_GLOBAL uint32_t*)(o.qs + (size_t)blk * 32 + 4 * l) = packed;
+  if (l == 0) {
+    ((RLH_GLOBAL float*)o.d)[blk] = d;
+    ((RLH_GLOBAL int32_t*)o.s)[blk] = tot;
+    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2] = s;
+  } else if (l == 4) {
+    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2 + 1] = s;
+  }
+}
+
+// Sum of squares of rmsnorm_core (simd.rs:285-313) over a row staged in LDS,
+// computed by one wave: lanes 0..31 run the 32 FMA chains (8 independent
+// loads in flight per step), remainder loop into slots 0..7, then the AVX2
+// tree and the in-order scalar tail. Returns ss in every lane.
+__device__ __forceinline__ float rms_sumsq_lds(const RLH_LDS float* x, int n) {
+  const int lane = threadIdx.x & 63;
+  const int n32 = (n / 32) * 32;
+  const int n8 = n32 + ((n - n32) / 8) * 8;
+  float acc = 0.0f;
+  if (lane < 32) {
+    int i = lane;
+    for (; i + 32 * 7 < n32; i += 32 * 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = x[i + 32 * k];
+#pragma unroll
+      for (int k = 0; k < 8; k++) acc = __builtin_fmaf(v[k], v[k], acc);
+    }
+    for (; i < n32; i += 32) acc = __builtin_fmaf(x[i], x[i], acc);
+    if (lane < 8)
+      for (int j = n32 + lane; j < n8; j += 8) acc = __builtin_fmaf(x[j], x[j], acc);
+  }
+  float ss = avx2_tree32(acc);
+  for (int i = n8; i < n; i++) ss = ss + x[i] * x[i];
+  return ss;
+}
+
 // get_scale_min_k4 (quant.rs:176-185) on the 12 scale bytes.
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
   if (j < 4) {
@@ -157,6 +216,33 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint32_t& 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
+
+// Load helpers that force global_load_* instructions.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 ld_g16(const void* p) {
+  u32x4_t v = *(const RLH_GLOBAL u32x4_t*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+// 16-byte streaming load (weights are read once per token).
+__device__ __forceinline__ uint4 ld_nt16(const void* p) {
+  u32x4_t v = __builtin_nontemporal_load((const RLH_GLOBAL u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld_g8(const void* p) {
+  u32x2_t v = *(const RLH_GLOBAL u32x2_t*)p;
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld_g4(const void* p) { return *(const RLH_GLOBAL uint32_t*)p; }
+__device__ __forceinline__ uint32_t ld_g2(const void* p) { return *(const RLH_GLOBAL uint16_t*)p; }
+__device__ __forceinline__ float ld_gf(const float* p) { return *(const RLH_GLOBAL float*)p; }
+typedef float f32x4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_gf4(const float* p) {
+  f32x4v_t v = *(const RLH_GLOBAL f32x4v_t*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ int ld_gi(const int32_t* p) { return *(const RLH_GLOBAL int32_t*)p; }
 
 // ---------------------------------------------------------------------------
 // Element dequantisation in the device layouts (quant.rs:191-385).

@@ -32,4 +32,13 @@ struct DevMat {
   const uint8_t* d;
 };
 
+// Q8 activation rows in device memory (Q8Row, simd.rs:88-101), token-major:
+// qs[n][cols], d[n][cols/32], s[n][cols/32], s16[n][cols/16].
+struct Q8Mut {
+  int8_t* qs;
+  float* d;
+  int32_t* s;
+  int32_t* s16;
+};
+
 }  // namespace rlh

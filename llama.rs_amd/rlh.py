@@ -209,7 +209,7 @@ def load():
         "rlh_matvec": (I32, [U32, P, U64, U64, P, P]),
         "rlh_matmul_batch": (I32, [U32, P, U64, U64, P, U64, P]),
         "rlh_block_dots": (I32, [U32, P, U64, U64, P, P]),
-        "rlh_profile_matvec": (I32, [P, P, I32, I32, I32, ctypes.POINTER(ctypes.c_double)]),
+        "rlh_profile_matvec": (I32, [P, P, I32, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_quantize_row": (I32, [U32, P, U64, P]),
         "rlh_synth_normal": (None, [U64, U64, U64, U64, F, F, P]),
@@ -314,6 +314,16 @@ class Cache:
         out = np.empty((n_tokens, self.model.spec.n_embd), dtype=np.float32)
         check(self.lib.rlh_debug_layer_hidden(self.h, layer, out.ctypes.data, n_tokens))
         return out
+
+    def profile_matvec(self, kind, iters):
+        v = ctypes.c_double()
+        check(self.lib.rlh_profile_matvec(self.model.h, self.h, kind, iters, ctypes.byref(v)))
+        return v.value
+
+    def profile_decode(self, iters):
+        v = ctypes.c_double()
+        check(self.lib.rlh_profile_decode(self.model.h, self.h, iters, ctypes.byref(v)))
+        return v.value
 
     def read_kv(self, layer, which_v, n_pos):
         s = self.model.spec
