@@ -179,10 +179,11 @@ int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t 
 int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
 
 /* ---- measurement ---------------------------------------------------------------------
- * Runs the decode matvec of one weight kind `iters` times on the cache's
- * stream, rotating over the layers' copies of that matrix (so weights stream
- * from HBM as in a decode step), and reports the average kernel duration in
- * microseconds from a HIP event pair around each launch on that stream. */
+ * Runs the decode matvec of one weight kind `iters` times back to back on the
+ * cache's stream, rotating over the layers' copies of that matrix (so weights
+ * stream from HBM as in a decode step), and reports the average time per
+ * launch in microseconds from one HIP event pair around all launches on that
+ * stream (launch-to-launch gaps included, as inside a captured step). */
 int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us);
 /* Average duration of one captured decode step (graph launch) over `iters`
  * steps at the cache's current length, in microseconds; the cache position

@@ -27,63 +27,6 @@ using namespace rlh;
 
 namespace {
 
-// ---- decode matvec launch plans ----------------------------------------------
-struct MvPlan {
-  MvLaunch L{};
-  uint32_t wgs = 0;
-  uint32_t lds = 0;
-  uint32_t ns = 1;  // row slots per lane, shared by the launch's segments
-};
-
-uint32_t mv_p(const DevMat& w) { return mv_pack(mv_units(w.ty, w.cols)); }
-
-// Row slots per lane for a matrix: the largest NS in {8, 4, 2, 1} that still
-// gives at least 512 blocks (R = 4 * NS * P rows each), so that even the
-// 1024-row K/V projections spread over every CU.
-uint32_t mv_pick_ns(const DevMat& w) {
-  uint32_t P = mv_p(w), ns = 8;
-  while (ns > 1 && (w.rows + 4 * ns * P - 1) / (4 * ns * P) < 512) ns /= 2;
-  while (ns > 1 && 4 * ns * P > 64) ns /= 2;
-  return ns;
-}
-
-void mv_lds(MvPlan& p, uint32_t R, uint32_t ty) {
-  p.lds = std::max(p.lds, 2 * R * (64 * mv_terms_per_unit(ty) + 4) * 4);
-}
-
-void mv_add(MvPlan& p, const DevMat& w, const Q8Buf& act, float* y, float* resid) {
-  MvSeg& g = p.L.seg[p.L.nseg++];
-  g = MvSeg{};
-  g.w = w;
-  g.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
-  g.y = y;
-  g.resid = resid;
-  g.rows_per_wg = 4 * p.ns * mv_p(w);
-  g.wg_begin = p.wgs;
-  p.wgs += (w.rows + g.rows_per_wg - 1) / g.rows_per_wg;
-  mv_lds(p, g.rows_per_wg, w.ty);
-}
-
-// gate/up rows in blocks of 32 with SwiGLU + Q8 of h in the epilogue. The
-// launch's NS must be 8 / P so that R = 32.
-void mv_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Buf& act, const Q8Buf& hq, float* h) {
-  MvSeg& g = p.L.seg[p.L.nseg++];
-  g = MvSeg{};
-  g.w = gate;
-  g.w2 = up;
-  g.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
-  g.y = h;
-  g.hq = hq;
-  g.pair = 1;
-  g.rows_per_wg = 32;
-  g.wg_begin = p.wgs;
-  p.wgs += gate.rows / 32;
-  mv_lds(p, 32, gate.ty);
-  mv_lds(p, 32, up.ty);
-}
-
-void mv_run(hipStream_t st, const MvPlan& p) { launch_mv(st, p.L, p.wgs, p.lds, p.ns); }
-
 thread_local std::string g_err;
 
 int fail(int code, const std::string& msg) {
@@ -174,39 +117,62 @@ struct Layer {
   DevVec attn_norm, ffn_norm, q_norm, k_norm, bq, bk, bv;
 };
 
-// Builds the device layout of rows x cols ggml bytes; returns the blob and
-// fills the plane pointers relative to `base`.
-std::vector<uint8_t> to_device_layout(uint32_t ty, const uint8_t* src, uint64_t rows, uint64_t cols, size_t off[4]) {
-  size_t rb = (size_t)type_size(ty) * (cols / block_size(ty));
-  off[0] = off[1] = off[2] = off[3] = 0;
-  if (ty == RLH_TYPE_Q6_K) {
-    size_t nsb = cols / 256, ns = rows * nsb;
-    off[1] = align256(ns * 128);
-    off[2] = off[1] + align256(ns * 64);
-    off[3] = off[2] + align256(ns * 16);
-    std::vector<uint8_t> out(off[3] + align256(ns * 2));
-    for (size_t s = 0; s < ns; s++) {
-      const uint8_t* b = src + s * 210;  // super-blocks are contiguous across rows
-      std::memcpy(&out[s * 128], b, 128);
-      std::memcpy(&out[off[1] + s * 64], b + 128, 64);
-      std::memcpy(&out[off[2] + s * 16], b + 192, 16);
-      std::memcpy(&out[off[3] + s * 2], b + 208, 2);
-    }
+// Item bytes (see rlh_format.h) of item j of a ggml row: super-blocks are
+// taken as they are; for Q8_0/Q4_0 the quants of 8 blocks come first, then
+// their 8 f16 scales.
+void gather_item(uint32_t ty, const uint8_t* row, uint32_t j, uint8_t* item) {
+  if (ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K) {
+    const uint32_t ib = item_bytes(ty);
+    std::memcpy(item, row + (size_t)j * ib, ib);
+    return;
+  }
+  const uint32_t bs = (uint32_t)type_size(ty), qb = bs - 2;  // 34/32 or 18/16
+  for (uint32_t k = 0; k < 8; k++) {
+    const uint8_t* blk = row + ((size_t)j * 8 + k) * bs;
+    std::memcpy(item + k * qb, blk + 2, qb);
+    item[8 * qb + 2 * k] = blk[0];
+    item[8 * qb + 2 * k + 1] = blk[1];
+  }
+}
+
+// Fills the DevMat layout fields and returns the device bytes of a rows x
+// cols matrix of type ty.
+size_t device_layout(DevMat& dm, uint32_t ty, uint64_t rows, uint64_t cols) {
+  dm.ty = ty;
+  dm.rows = (uint32_t)rows;
+  dm.cols = (uint32_t)cols;
+  dm.row_bytes = (uint32_t)((size_t)type_size(ty) * (cols / block_size(ty)));
+  if (!is_tiled(ty)) {
+    dm.tr = dm.tj = dm.ntj = dm.ib = 0;
+    return (size_t)rows * dm.row_bytes;
+  }
+  const uint32_t nitems = (uint32_t)(cols / 256);
+  dm.ib = item_bytes(ty);
+  dm.tj = tile_width(nitems);
+  dm.tr = 64 / dm.tj;
+  dm.ntj = nitems / dm.tj;
+  const size_t nrt = (rows + dm.tr - 1) / dm.tr;
+  return nrt * dm.ntj * 64 * dm.ib;
+}
+
+std::vector<uint8_t> to_device_layout(const DevMat& dm, const uint8_t* src, size_t bytes) {
+  std::vector<uint8_t> out(bytes, 0);
+  if (!is_tiled(dm.ty)) {
+    std::memcpy(out.data(), src, bytes);
     return out;
   }
-  if (ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0) {
-    size_t nb = rows * (cols / 32), qb = ty == RLH_TYPE_Q8_0 ? 32 : 16, bs = (size_t)type_size(ty);
-    off[1] = align256(nb * qb);
-    std::vector<uint8_t> out(off[1] + align256(nb * 2));
-    for (size_t b = 0; b < nb; b++) {
-      const uint8_t* p = src + b * bs;
-      out[off[1] + 2 * b] = p[0];
-      out[off[1] + 2 * b + 1] = p[1];
-      std::memcpy(&out[b * qb], p + 2, qb);
+  const uint32_t nitems = dm.cols / 256;
+  uint8_t item[272];
+  for (uint32_t r = 0; r < dm.rows; r++) {
+    const uint8_t* row = src + (size_t)r * dm.row_bytes;
+    for (uint32_t j = 0; j < nitems; j++) {
+      gather_item(dm.ty, row, j, item);
+      const uint32_t ch = dm.ib / 16;
+      for (uint32_t k = 0; k < ch; k++) std::memcpy(&out[item_offset(dm, r, j, 16 * k)], item + 16 * k, 16);
+      if (dm.ib % 16) std::memcpy(&out[item_offset(dm, r, j, ch * 16)], item + ch * 16, dm.ib % 16);
     }
-    return out;
   }
-  return std::vector<uint8_t>(src, src + rows * rb);
+  return out;
 }
 
 int upload_matrix(DevTensor& t, uint32_t ty, const void* bytes, uint64_t cols, uint64_t rows) {
@@ -214,8 +180,12 @@ int upload_matrix(DevTensor& t, uint32_t ty, const void* bytes, uint64_t cols, u
     return fail(RLH_EUNSUP, "ggml type " + std::to_string(ty) + " has no device layout on this path");
   if (cols == 0 || rows == 0 || cols % (uint64_t)block_size(ty) != 0)
     return fail(RLH_EINVAL, "row length " + std::to_string(cols) + " is not a multiple of the block size");
-  size_t off[4];
-  std::vector<uint8_t> blob = to_device_layout(ty, (const uint8_t*)bytes, rows, cols, off);
+  if (is_tiled(ty) && cols % 256 != 0)
+    return fail(RLH_EUNSUP, "quantized rows must hold a multiple of 256 values");
+  if (rows > 0xffffffffull || cols > 0xffffffffull) return fail(RLH_EINVAL, "matrix too large");
+  DevMat dm{};
+  const size_t bytes_dev = device_layout(dm, ty, rows, cols);
+  std::vector<uint8_t> blob = to_device_layout(dm, (const uint8_t*)bytes, bytes_dev);
   if (t.mem) (void)hipFree(t.mem);
   t.mem = nullptr;
   hipError_t e = hipMalloc((void**)&t.mem, blob.size());
@@ -226,14 +196,8 @@ int upload_matrix(DevTensor& t, uint32_t ty, const void* bytes, uint64_t cols, u
   t.rows = rows;
   t.cols = cols;
   t.bytes = blob.size();
-  t.dm.ty = ty;
-  t.dm.rows = (uint32_t)rows;
-  t.dm.cols = (uint32_t)cols;
-  t.dm.row_bytes = (uint32_t)((size_t)type_size(ty) * (cols / block_size(ty)));
-  t.dm.a = t.mem + off[0];
-  t.dm.b = t.mem + off[1];
-  t.dm.c = t.mem + off[2];
-  t.dm.d = t.mem + off[3];
+  t.dm = dm;
+  t.dm.a = t.mem;
   return RLH_OK;
 }
 
@@ -312,7 +276,8 @@ struct rlh_cache {
   uint32_t* hist = nullptr;    // greedy history [max_ctx + 1]
   float* pv = nullptr;
   uint32_t* pi = nullptr;
-  uint32_t nparts = 256;
+  uint32_t nparts = 256;        // partials of the standalone argmax (rlh_greedy_next)
+  uint32_t* am_counter = nullptr;  // block counter of the fused logits argmax
   uint32_t* host_st = nullptr;  // pinned staging for tok/pos
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
   bool debug = false;
@@ -349,16 +314,18 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   uint32_t* tok = c->st_dev;
   uint32_t* pos = c->st_dev + 1;
   launch_embed(st, m->token_embd.dm, tok, 1, c->x);
+  const uint32_t qd = H * hd, F = cfg.n_ff;
   for (uint32_t l = 0; l < cfg.n_layer; l++) {
     Layer& L = m->layers[l];
-    launch_rmsnorm_q8(st, c->x, L.attn_norm.p, E, 1, eps, c->act_e, nullptr);
-    {
+    {  // rmsnorm + Q8 (block prologue), then q, k, v (model.rs:621-624)
       MvPlan p;
-      p.ns = mv_pick_ns(L.q.dm);
-      mv_add(p, L.q.dm, c->act_e, c->q, nullptr);
-      mv_add(p, L.k.dm, c->act_e, c->k, nullptr);
-      mv_add(p, L.v.dm, c->act_e, c->v, nullptr);
-      mv_run(st, p);
+      mv_plan_init(p, E, c->x);
+      mv_plan_norm(p, L.attn_norm.p, eps);
+      mv_plan_add(p, L.q.dm, c->q, nullptr);
+      mv_plan_add(p, L.k.dm, c->k, nullptr);
+      mv_plan_add(p, L.v.dm, c->v, nullptr);
+      mv_plan_finish(p);
+      mv_launch(st, p);
     }
     {
       AttnArgs a{};
@@ -387,40 +354,44 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       launch_attn_scores(st, a, 1, true);
       launch_attn_out(st, a, 1);
     }
-    {
+    {  // attn_output, x += (model.rs:713-716)
       MvPlan p;
-      p.ns = mv_pick_ns(L.o.dm);
-      mv_add(p, L.o.dm, c->act_q, nullptr, c->x);
-      mv_run(st, p);
+      mv_plan_init(p, qd, c->attn);
+      mv_plan_add(p, L.o.dm, nullptr, c->x);
+      mv_plan_finish(p);
+      mv_launch(st, p);
     }
-    launch_rmsnorm_q8(st, c->x, L.ffn_norm.p, E, 1, eps, c->act_e, nullptr);
-    {
+    {  // rmsnorm + Q8, gate/up, silu(g)*u, Q8 of h (model.rs:719-724)
       MvPlan p;
-      p.ns = 8 / mv_p(L.gate.dm);
-      mv_add_pair(p, L.gate.dm, L.up.dm, c->act_e, c->act_f, nullptr);
-      mv_run(st, p);
+      mv_plan_init(p, E, c->x);
+      mv_plan_norm(p, L.ffn_norm.p, eps);
+      mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->g);
+      mv_plan_finish(p);
+      mv_launch(st, p);
     }
-    {
+    {  // ffn_down, x += (model.rs:725-728)
       MvPlan p;
-      p.ns = mv_pick_ns(L.down.dm);
-      mv_add(p, L.down.dm, c->act_f, nullptr, c->x);
-      mv_run(st, p);
+      mv_plan_init(p, F, c->g);
+      mv_plan_add(p, L.down.dm, nullptr, c->x);
+      mv_plan_finish(p);
+      mv_launch(st, p);
     }
     if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
       (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
                            st);
   }
   if (kind == STEP_NOLOGITS) return;
-  launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
-  {
+  {  // output_norm + logits (model.rs:733-737), greedy argmax fused
     MvPlan p;
-    p.ns = mv_pick_ns(ow.dm);
-    mv_add(p, ow.dm, c->act_e, c->logits, nullptr);
-    mv_run(st, p);
+    mv_plan_init(p, E, c->x);
+    mv_plan_norm(p, m->output_norm.p, eps);
+    mv_plan_add(p, ow.dm, c->logits, nullptr);
+    if (kind == STEP_GREEDY)
+      mv_plan_argmax(p, MvArgmax{c->pv, c->pi, c->am_counter, tok, pos, c->st_dev + 2, c->hist});
+    mv_plan_finish(p);
+    mv_launch(st, p);
   }
-  if (kind == STEP_GREEDY)
-    launch_argmax(st, c->logits, cfg.vocab_size, c->pv, c->pi, c->nparts, tok, pos, c->st_dev + 2, c->hist);
 }
 
 int capture(rlh_cache* c, StepKind kind, hipGraphExec_t* out) {
@@ -587,6 +558,31 @@ int rlh_model_finalize(rlh_model* m) {
     if ((rc = check_vec(L.bk, "attn_k.bias", li, kvd, false))) return rc;
     if ((rc = check_vec(L.bv, "attn_v.bias", li, kvd, false))) return rc;
   }
+  // every decode matvec launch must fit the kernel's LDS budget
+  for (uint32_t l = 0; l < c.n_layer; l++) {
+    Layer& L = m->layers[l];
+    if (L.gate.ty != L.up.ty)
+      return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": ffn_gate and ffn_up must share a ggml type");
+    const float* dummy = (const float*)m;  // plans are only sized here, never launched
+    MvPlan p;
+    mv_plan_init(p, (uint32_t)E, dummy);
+    mv_plan_norm(p, dummy, 0.0f);
+    mv_plan_add(p, L.q.dm, nullptr, nullptr);
+    mv_plan_add(p, L.k.dm, nullptr, nullptr);
+    mv_plan_add(p, L.v.dm, nullptr, nullptr);
+    bool ok = mv_plan_finish(p);
+    mv_plan_init(p, (uint32_t)qd, dummy);
+    mv_plan_add(p, L.o.dm, nullptr, nullptr);
+    ok = ok && mv_plan_finish(p);
+    mv_plan_init(p, (uint32_t)E, dummy);
+    mv_plan_norm(p, dummy, 0.0f);
+    mv_plan_add_pair(p, L.gate.dm, L.up.dm, nullptr);
+    ok = ok && mv_plan_finish(p);
+    mv_plan_init(p, (uint32_t)F, dummy);
+    mv_plan_add(p, L.down.dm, nullptr, nullptr);
+    ok = ok && mv_plan_finish(p);
+    if (!ok) return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": matrix shapes exceed the matvec LDS budget");
+  }
   // RoPE table with the host libm, as the reference computes it:
   // inv_freq = theta^(-2i/hd) (model.rs:221-227), angle = pos * inv_freq,
   // (sin, cos) = f32::sin_cos (ops.rs:439).
@@ -642,7 +638,7 @@ static void cache_free(rlh_cache* c) {
   void* ptrs[] = {c->kc, c->vc, c->scores, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
                   c->act_e.qs, c->act_e.d, c->act_e.s, c->act_e.s16, c->act_q.qs, c->act_q.d, c->act_q.s,
                   c->act_q.s16, c->act_f.qs, c->act_f.d, c->act_f.s, c->act_f.s16, c->st_dev, c->hist, c->pv,
-                  c->pi, c->dbg};
+                  c->pi, c->dbg, c->am_counter};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   if (c->host_st) (void)hipHostFree(c->host_st);
@@ -671,6 +667,8 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   rlh_cache* c = new rlh_cache();
   c->m = m;
   c->max_ctx = max_ctx;
+  const DevTensor& ow = m->output.set ? m->output : m->token_embd;
+  const uint32_t npv = std::max(c->nparts, mv_blocks_for(ow.ty, cfg.vocab_size, cfg.n_embd));
   c->vtile = vtile;
   uint64_t E = cfg.n_embd, F = cfg.n_ff, qd = (uint64_t)cfg.n_head * cfg.head_dim,
            kvd = (uint64_t)cfg.n_head_kv * cfg.head_dim;
@@ -685,8 +683,9 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
             hipMalloc((void**)&c->scratch, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) == hipSuccess &&
             hipMalloc((void**)&c->st_dev, 64) == hipSuccess &&
             hipMalloc((void**)&c->hist, (max_ctx + 2) * 4) == hipSuccess &&
-            hipMalloc((void**)&c->pv, c->nparts * 4) == hipSuccess &&
-            hipMalloc((void**)&c->pi, c->nparts * 4) == hipSuccess &&
+            hipMalloc((void**)&c->pv, (size_t)npv * 4) == hipSuccess &&
+            hipMalloc((void**)&c->pi, (size_t)npv * 4) == hipSuccess &&
+            hipMalloc((void**)&c->am_counter, 64) == hipSuccess &&
             hipHostMalloc((void**)&c->host_st, 64) == hipSuccess;
   if (!ok) {
     cache_free(c);
@@ -700,7 +699,9 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
     return rc;
   }
   if (hipMemset(c->st_dev, 0, 64) != hipSuccess || hipMemset(c->kc, 0, kvbytes) != hipSuccess ||
-      hipMemset(c->vc, 0, kvbytes) != hipSuccess) {
+      hipMemset(c->vc, 0, kvbytes) != hipSuccess || hipMemset(c->am_counter, 0, 64) != hipSuccess || hipMemset(c->scratch, 0, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) != hipSuccess ||
+      hipMemset(c->act_e.qs, 0, E) != hipSuccess || hipMemset(c->act_e.d, 0, E / 32 * 4) != hipSuccess ||
+      hipMemset(c->act_e.s, 0, E / 32 * 4) != hipSuccess || hipMemset(c->act_e.s16, 0, E / 16 * 4) != hipSuccess) {
     cache_free(c);
     return fail(RLH_EDEVICE, "cache init");
   }
@@ -907,30 +908,26 @@ int rlh_dequant(uint32_t ty, const void* bytes, uint64_t n, float* out) {
 int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const float* x, float* y) {
   if (!x || !y) return fail(RLH_EINVAL, "null argument");
   if (!matvec_supported(ty)) return fail(RLH_EUNSUP, "no matvec kernel for ggml type " + std::to_string(ty));
-  if (cols % 256 && !(ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0))
-    return fail(RLH_EINVAL, "cols must be a multiple of 256");
-  if (cols % 32) return fail(RLH_EINVAL, "cols must be a multiple of 32");
+  if (cols == 0 || cols % 256) return fail(RLH_EINVAL, "cols must be a positive multiple of 256");
+  if (rows == 0 || rows > 0xffffffffull) return fail(RLH_EINVAL, "rows out of range");
   DevTensor t;
   int rc = op_upload(t, ty, w, rows, cols);
   if (rc) return rc;
   hipStream_t st = op_stream();
-  DevBuf<float> dx, dy, dd;
-  DevBuf<int8_t> dq;
-  DevBuf<int32_t> ds, ds16;
-  if (dx.alloc(cols) || dy.alloc(rows) || dq.alloc(cols) || dd.alloc(cols / 32) || ds.alloc(cols / 32) ||
-      ds16.alloc(cols / 16)) {
+  DevBuf<float> dx, dy;
+  if (dx.alloc(cols) || dy.alloc(rows)) {
     free_tensor(t);
     return fail(RLH_ENOMEM, "hipMalloc");
   }
-  Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
   hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
-  launch_quantize_q8(st, dx.p, (uint32_t)cols, act);
-  {
-    MvPlan p;
-    p.ns = mv_pick_ns(t.dm);
-    mv_add(p, t.dm, act, dy.p, nullptr);
-    mv_run(st, p);
+  MvPlan p;
+  mv_plan_init(p, (uint32_t)cols, dx.p);
+  mv_plan_add(p, t.dm, dy.p, nullptr);
+  if (!mv_plan_finish(p)) {
+    free_tensor(t);
+    return fail(RLH_EUNSUP, "row length " + std::to_string(cols) + " exceeds the matvec LDS budget");
   }
+  mv_launch(st, p);
   if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(y, dy.p, rows * 4, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -1009,29 +1006,27 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   uint64_t cols = mats[0]->cols;
   if (cols != m->cfg.n_embd && cols != m->cfg.n_ff && cols != qd)
     return fail(RLH_EINVAL, "matrix width matches no activation buffer");
-  const Q8Buf& act = cols == m->cfg.n_ff ? c->act_f : (cols == qd ? c->act_q : c->act_e);
-  std::vector<hipEvent_t> ev(2 * (size_t)iters);
-  for (auto& e : ev) HIPCHK(hipEventCreate(&e));
   std::vector<MvPlan> plans(mats.size());
   for (size_t i = 0; i < mats.size(); i++) {
-    plans[i].ns = mv_pick_ns(mats[i]->dm);
-    mv_add(plans[i], mats[i]->dm, act, c->scratch, nullptr);
+    mv_plan_init(plans[i], (uint32_t)cols, c->scratch);
+    mv_plan_add(plans[i], mats[i]->dm, c->logits, nullptr);
+    if (!mv_plan_finish(plans[i])) return fail(RLH_EUNSUP, "matvec shape");
   }
-  mv_run(c->st, plans[0]);  // warm-up
-  for (int i = 0; i < iters; i++) {
-    HIPCHK(hipEventRecord(ev[2 * i], c->st));
-    mv_run(c->st, plans[i % plans.size()]);
-    HIPCHK(hipEventRecord(ev[2 * i + 1], c->st));
-  }
-  HIPCHK(hipStreamSynchronize(c->st));
-  double total = 0.0;
-  for (int i = 0; i < iters; i++) {
-    float ms = 0.f;
-    HIPCHK(hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
-    total += ms;
-  }
-  for (auto& e : ev) (void)hipEventDestroy(e);
-  *avg_us = total * 1000.0 / iters;
+  // back-to-back launches between one event pair, as in a captured decode
+  // step; the average therefore includes the launch-to-launch gap
+  hipEvent_t e0, e1;
+  HIPCHK(hipEventCreate(&e0));
+  HIPCHK(hipEventCreate(&e1));
+  mv_launch(c->st, plans[0]);  // warm-up
+  HIPCHK(hipEventRecord(e0, c->st));
+  for (int i = 0; i < iters; i++) mv_launch(c->st, plans[i % plans.size()]);
+  HIPCHK(hipEventRecord(e1, c->st));
+  HIPCHK(hipEventSynchronize(e1));
+  float ms = 0.f;
+  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *avg_us = (double)ms * 1000.0 / iters;
   return RLH_OK;
 }
 

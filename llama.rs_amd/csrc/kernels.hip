@@ -102,33 +102,33 @@ __global__ void __launch_bounds__(256) k_block_dots(DevMat w, const int8_t* a, i
   int s = 0;
   switch (w.ty) {
     case RLH_TYPE_Q4_K: {  // k = 32-block index: bi*8 + 2g + hi
-      uint32_t bi = k >> 3, g = (k >> 1) & 3, hi = k & 1;
-      const uint8_t* qs = w.a + (size_t)row * w.row_bytes + (size_t)bi * 144 + 16 + 32 * g;
-      for (int l = 0; l < 32; l++) s += (int)((qs[l] >> (4 * hi)) & 0xF) * a[(size_t)k * 32 + l];
+      const uint32_t bi = k >> 3, g = (k >> 1) & 3, hi = k & 1;
+      for (uint32_t l = 0; l < 32; l++)
+        s += (int)((item_u8(w, row, bi, 16 + 32 * g + l) >> (4 * hi)) & 0xF) * a[(size_t)k * 32 + l];
       break;
     }
     case RLH_TYPE_Q6_K: {  // k = 16-half index: (bi*8 + half*4 + c)*2 + sub
-      uint32_t blk = k >> 1, sub = k & 1, bi = blk >> 3, half = (blk >> 2) & 1, c = blk & 3;
-      size_t sbi = (size_t)row * (w.cols >> 8) + bi;
-      const uint8_t* ql = w.a + sbi * 128 + half * 64 + (c & 1) * 32 + sub * 16;
-      const uint8_t* qh = w.b + sbi * 64 + half * 32 + sub * 16;
-      for (int l = 0; l < 16; l++) {
-        uint32_t nib = c < 2 ? (ql[l] & 0xF) : (ql[l] >> 4);
-        uint32_t uu = nib | (((qh[l] >> (2 * c)) & 3) << 4);
+      const uint32_t blk = k >> 1, sub = k & 1, bi = blk >> 3, half = (blk >> 2) & 1, c = blk & 3;
+      for (uint32_t l = 0; l < 16; l++) {
+        const uint32_t qlb = item_u8(w, row, bi, half * 64 + (c & 1) * 32 + sub * 16 + l);
+        const uint32_t qhb = item_u8(w, row, bi, 128 + half * 32 + sub * 16 + l);
+        const uint32_t nib = c < 2 ? (qlb & 0xF) : (qlb >> 4);
+        const uint32_t uu = nib | (((qhb >> (2 * c)) & 3) << 4);
         s += (int)uu * a[(size_t)blk * 32 + sub * 16 + l];
       }
       break;
     }
     case RLH_TYPE_Q8_0: {
-      const int8_t* q = (const int8_t*)(w.a + ((size_t)row * (w.cols >> 5) + k) * 32);
-      for (int l = 0; l < 32; l++) s += (int)q[l] * a[(size_t)k * 32 + l];
+      const uint32_t j = k >> 3, kk = k & 7;
+      for (uint32_t l = 0; l < 32; l++) s += (int)(int8_t)item_u8(w, row, j, kk * 32 + l) * a[(size_t)k * 32 + l];
       break;
     }
     case RLH_TYPE_Q4_0: {
-      const uint8_t* q = w.a + ((size_t)row * (w.cols >> 5) + k) * 16;
-      for (int l = 0; l < 16; l++) {
-        s += (int)(q[l] & 0xF) * a[(size_t)k * 32 + l];
-        s += (int)(q[l] >> 4) * a[(size_t)k * 32 + 16 + l];
+      const uint32_t j = k >> 3, kk = k & 7;
+      for (uint32_t l = 0; l < 16; l++) {
+        const uint32_t q = item_u8(w, row, j, kk * 16 + l);
+        s += (int)(q & 0xF) * a[(size_t)k * 32 + l];
+        s += (int)(q >> 4) * a[(size_t)k * 32 + 16 + l];
       }
       break;
     }

@@ -1,4 +1,4 @@
-// matvec.h — launch descriptors of the multi-segment decode matvec.
+// matvec.h — launch descriptors of the decode matvec (ops.rs:67-141).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -7,40 +7,76 @@
 
 namespace rlh {
 
-struct Q8Ptr {
-  const int8_t* qs;
-  const float* d;
-  const int32_t* s;
-  const int32_t* s16;
+// One matrix (or a gate/up pair) of a launch. Every segment of a launch
+// multiplies the same activation row (cols wide).
+struct MvSeg {
+  DevMat w;            // rows summed into y / resid (gate in PAIR mode)
+  DevMat w2;           // PAIR mode: up
+  float* y;            // single: y[r] = total (nullable); PAIR: h[r] = silu(g)*u
+  float* resid;        // single: resid[r] = resid[r] + total (nullable)
+  uint32_t blk_begin;  // first block of this segment
+  uint32_t pair;
 };
 
-// One matrix (or a gate/up pair) of a launch.
-struct MvSeg {
-  DevMat w;          // rows summed into y / resid (gate in PAIR mode)
-  DevMat w2;         // PAIR mode: up
-  Q8Ptr act;         // Q8 activation row (cols of w)
-  float* y;          // single: y[r] = total (nullable); PAIR: h[r] (nullable)
-  float* resid;      // single: resid[r] = resid[r] + total (nullable)
-  Q8Mut hq;          // PAIR: Q8 blocks of h = silu(gate) * up
-  uint32_t wg_begin;     // first block index of this segment
-  uint32_t rows_per_wg;  // R = 4 * NS * P (NS of the launch; 32 in PAIR mode)
-  uint32_t pair;
+// Greedy argmax fused into the logits launch (main.rs:453-463 semantics):
+// every block leaves its (max, lowest index) in pv/pi[block]; the last
+// block to finish reduces them, writes *tok and, when `step` is set,
+// advances the greedy loop state (pos += 1, hist[++step] = token).
+struct MvArgmax {
+  float* pv;
+  uint32_t* pi;
+  uint32_t* counter;  // zero between launches (the last block resets it)
+  uint32_t* tok;
+  uint32_t* pos;
+  uint32_t* step;
+  uint32_t* hist;
 };
 
 struct MvLaunch {
   MvSeg seg[3];
   uint32_t nseg;
+  uint32_t cols;
+  uint32_t rows_per_blk;  // R: rows of one block (all segments)
+  const float* x;         // f32 activation row; the block quantises it to Q8
+  const float* nw;        // rmsnorm weights: when set, the block first computes
+  float eps;              //   rmsnorm(x) * nw (simd.rs:282-326)
+  uint32_t region_off;    // byte offset of the staging / term-tile region in LDS
+  uint32_t tile_stride;   // floats per term-tile row
+  uint32_t has_argmax;
+  MvArgmax am;
 };
 
-// Rows packed per wave instruction for a row of `units` units.
-inline uint32_t mv_pack(uint32_t units) { return units <= 16 ? 4u : (units <= 32 ? 2u : 1u); }
-inline uint32_t mv_units(uint32_t ty, uint32_t cols) {
-  return (ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0) ? cols / 32 : cols / 64;
-}
-inline uint32_t mv_terms_per_unit(uint32_t ty) { return ty == RLH_TYPE_Q6_K ? 4u : 1u; }
+// Host-side plan: segments are appended, then launched once.
+struct MvPlan {
+  MvLaunch L{};
+  uint32_t blocks = 0;
+  uint32_t lds = 0;
+  uint32_t waves = 0;  // waves per block
+  uint32_t max_terms = 0;
+  uint32_t rows = 0;   // rows over all segments
+};
 
-// ns: row slots per lane (1, 2, 4 or 8), shared by all segments of L.
-void launch_mv(hipStream_t st, const MvLaunch& L, uint32_t total_wgs, uint32_t lds_bytes, uint32_t ns);
+// Terms (float summands of the reference's per-row chain) per 256-value
+// super-block: one per 64 values for Q4_K, per 16 for Q6_K, per 32 for
+// Q8_0/Q4_0.
+__host__ __device__ inline uint32_t mv_terms_per_sb(uint32_t ty) {
+  return ty == RLH_TYPE_Q6_K ? 16u : (ty == RLH_TYPE_Q4_K ? 4u : 8u);
+}
+
+// Plan construction: x is the f32 activation (cols values, cols a multiple
+// of 256); mv_plan_norm adds the rmsnorm prologue. Every segment must have
+// `cols` columns; PAIR plans hold exactly one segment. mv_plan_finish fixes
+// the block shape (returns false when no shape fits the LDS).
+void mv_plan_init(MvPlan& p, uint32_t cols, const float* x);
+void mv_plan_norm(MvPlan& p, const float* w, float eps);
+void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
+void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, float* h);
+void mv_plan_argmax(MvPlan& p, const MvArgmax& am);
+bool mv_plan_finish(MvPlan& p);
+void mv_launch(hipStream_t st, const MvPlan& p);
+// Blocks of a single-matrix plan over `rows` rows of `cols` columns (the
+// argmax partial buffers of the logits launch hold one entry per block).
+uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols);
 bool mv_set_max_lds(size_t bytes);
 
 }  // namespace rlh

@@ -6,21 +6,30 @@
 // dot_q40_q8_avx2 (simd.rs:863), each term evaluated with the reference's
 // expression and rounding.
 //
-// Structure (HBM-bound): a block of 256 threads owns R = 4 * NS * P rows of
-// one matrix. The row is walked in chunks of 64/P "units" per lane group (a
-// unit = the weights behind one term, or four consecutive terms for Q6_K).
-// Per chunk every lane first issues the loads of its unit for all NS of its
-// rows (memory-level parallelism), then computes the terms into an LDS tile
-// [row][term]. The in-order per-row sum (one lane per row) of chunk k-1 runs
-// while chunk k's loads are in flight, from a double-buffered tile. Rows
-// narrower than 64 units pack P rows per wave instruction.
-//
-// One launch covers up to three matrices (the q/k/v projections) of mixed
-// ggml types; a segment in PAIR mode computes the same rows of two matrices
-// (ffn_gate, ffn_up) and fuses SwiGLU + Q8 quantisation of the 32-row block
-// (model.rs:720-724, ops.rs:393-395, simd.rs:116-203).
+// Structure (HBM-bound, one pass over the weights):
+//  * A block owns R rows (whole row-tiles of the tiled weight layout, see
+//    rlh_format.h); wave w takes the block's tiles w, w + waves, ... A lane
+//    owns one item (a 256-value super-block of one row) of the tile and
+//    loads it with 16-byte loads that are contiguous across the wave, so
+//    every load instruction reads 1 KB of HBM while the scale unpacking and
+//    address arithmetic are paid once per 256 weights.
+//  * The activation enters as f32. The block quantises it to Q8 blocks in LDS
+//    (quantize_q8, simd.rs:116-203), optionally after rmsnorm with the layer's
+//    norm weights (simd.rs:282-326), which removes the separate normalisation
+//    launch. x and the norm weights reach LDS with global_load_lds while the
+//    first weights are already in flight. Q8 super-blocks are stored with a
+//    16-byte pad so that lanes on different super-blocks hit different banks.
+//  * Every item writes its terms into the block's LDS tile [row][term]; after
+//    one barrier, lane r of wave 0 adds row r's terms in order (the
+//    reference's `total +=` chain) and runs the epilogue.
+//  * PAIR mode multiplies the same rows of ffn_gate and ffn_up and writes
+//    h = silu(gate) * up (ops.rs:393-395, model.rs:722-724). Single mode can
+//    add into the residual (model.rs:714-716, 726-728) and fuse the greedy
+//    argmax of the logits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 
 #include "kernels.h"
 #include "matvec.h"
@@ -30,370 +39,579 @@ namespace rlh {
 
 namespace {
 
-constexpr int kThreads = 256;
 typedef RLH_LDS float lfloat;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef RLH_LDS f32x4_t lf32x4;
+typedef RLH_LDS u32x4_t lu32x4;
 
-// ---- per-type unit loaders and term evaluators ------------------------------
-template <uint32_t TY>
-struct MU;
+constexpr uint32_t kSbStride = 272;  // LDS bytes per 256 Q8 values (16-byte pad)
 
-template <>
-struct MU<RLH_TYPE_Q4_K> {
-  static constexpr int kT = 1;
-  struct W {
-    uint4 hdr, q0, q1;
-  };
-  struct A {
-    uint4 a0, a1, b0, b1;
-    float da, db, sa, sb;
-  };
-  __device__ __forceinline__ static uint32_t units(uint32_t cols) { return cols >> 6; }
-  __device__ __forceinline__ static A act(const Q8Ptr& q, uint32_t u) {
-    uint32_t ab = (u >> 2) * 8 + 2 * (u & 3);
-    const int8_t* p = q.qs + (size_t)ab * 32;
-    A a;
-    a.a0 = ld_g16(p);
-    a.a1 = ld_g16(p + 16);
-    a.b0 = ld_g16(p + 32);
-    a.b1 = ld_g16(p + 48);
-    a.da = ld_gf(q.d + ab);
-    a.db = ld_gf(q.d + ab + 1);
-    a.sa = (float)ld_gi(q.s + ab);
-    a.sb = (float)ld_gi(q.s + ab + 1);
-    return a;
-  }
-  __device__ __forceinline__ static W load(const DevMat& w, uint32_t row, uint32_t u) {
-    const uint8_t* sb = w.a + (size_t)row * w.row_bytes + (size_t)(u >> 2) * 144;
-    uint32_t g = u & 3;
-    W r;
-    r.hdr = ld_nt16(sb);
-    r.q0 = ld_nt16(sb + 16 + 32 * g);
-    r.q1 = ld_nt16(sb + 32 + 32 * g);
-    return r;
-  }
-  __device__ __forceinline__ static void terms(const W r, const A& a, uint32_t u, lfloat* t) {
-    const uint32_t m = 0x0F0F0F0Fu;
-    uint32_t g = u & 3;
-    int i1 = 0, i2 = 0;
-    i1 = sdot4(r.q0.x & m, a.a0.x, i1); i1 = sdot4(r.q0.y & m, a.a0.y, i1);
-    i1 = sdot4(r.q0.z & m, a.a0.z, i1); i1 = sdot4(r.q0.w & m, a.a0.w, i1);
-    i1 = sdot4(r.q1.x & m, a.a1.x, i1); i1 = sdot4(r.q1.y & m, a.a1.y, i1);
-    i1 = sdot4(r.q1.z & m, a.a1.z, i1); i1 = sdot4(r.q1.w & m, a.a1.w, i1);
-    i2 = sdot4((r.q0.x >> 4) & m, a.b0.x, i2); i2 = sdot4((r.q0.y >> 4) & m, a.b0.y, i2);
-    i2 = sdot4((r.q0.z >> 4) & m, a.b0.z, i2); i2 = sdot4((r.q0.w >> 4) & m, a.b0.w, i2);
-    i2 = sdot4((r.q1.x >> 4) & m, a.b1.x, i2); i2 = sdot4((r.q1.y >> 4) & m, a.b1.y, i2);
-    i2 = sdot4((r.q1.z >> 4) & m, a.b1.z, i2); i2 = sdot4((r.q1.w >> 4) & m, a.b1.w, i2);
-    float d = f16_to_f32(r.hdr.x & 0xffff);
-    float dmin = f16_to_f32(r.hdr.x >> 16);
-    // get_scale_min_k4 (quant.rs:176-185) for j = 2g and 2g+1 on the 12
-    // scale bytes held in hdr.y, hdr.z, hdr.w
-    const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-    uint32_t sc1, m1, sc2, m2;
-    if (g < 2) {  // j = 2g, 2g+1 < 4: low 6 bits of bytes j (scale) and j+4 (min)
-      uint32_t sh1 = 16 * g, sh2 = 16 * g + 8;
-      sc1 = (s0 >> sh1) & 63;
-      m1 = (s1 >> sh1) & 63;
-      sc2 = (s0 >> sh2) & 63;
-      m2 = (s1 >> sh2) & 63;
-    } else {  // j >= 4: nibbles of byte j+4, top bits of bytes j-4 and j
-      uint32_t sh1 = 16 * (g - 2), sh2 = sh1 + 8;
-      sc1 = ((s2 >> sh1) & 0xF) | (((s0 >> sh1) >> 6 & 3) << 4);
-      m1 = ((s2 >> sh1) >> 4 & 0xF) | (((s1 >> sh1) >> 6 & 3) << 4);
-      sc2 = ((s2 >> sh2) & 0xF) | (((s0 >> sh2) >> 6 & 3) << 4);
-      m2 = ((s2 >> sh2) >> 4 & 0xF) | (((s1 >> sh2) >> 6 & 3) << 4);
-    }
-    float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
-    float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
-    t[0] = a.da * (d1 * (float)i1 - mm1 * a.sa) + a.db * (d2 * (float)i2 - mm2 * a.sb);
-  }
+// Q8 activation row in LDS (Q8Row, simd.rs:88-101).
+struct LAct {
+  RLH_LDS int8_t* qs;  // padded: value i at (i / 256) * kSbStride + i % 256
+  RLH_LDS float* d;
+  RLH_LDS int32_t* s;
+  RLH_LDS float* s16x32;  // 32.0f * (float)sums16 (the Q6_K correction, exact in f32)
 };
 
+__device__ __forceinline__ const RLH_LDS int8_t* qblk(const LAct& a, uint32_t b) {
+  return a.qs + (b >> 3) * kSbStride + (b & 7) * 32;
+}
+__device__ __forceinline__ u32x4_t lds_u4(const RLH_LDS int8_t* p) { return *(const lu32x4*)p; }
+__device__ __forceinline__ u32x4_t gl_u4(const void* p) { return *(const RLH_GLOBAL u32x4_t*)p; }
+
+// Cross-lane moves inside groups of 8 lanes with DPP (no LDS round trip):
+// lane ^ 1 and lane ^ 2 within a quad, and the mirror 7 - i of the 8-lane
+// half-row, which pairs every lane of one quad with a lane of the other.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
+
+__device__ __forceinline__ int dot16(u32x4_t w, u32x4_t a, int acc) {
+  acc = sdot4(w.x, a.x, acc);
+  acc = sdot4(w.y, a.y, acc);
+  acc = sdot4(w.z, a.z, acc);
+  return sdot4(w.w, a.w, acc);
+}
+
+// ---- work items: one super-block of one row ---------------------------------
+template <uint32_t TY>
+struct MI;
+
 template <>
-struct MU<RLH_TYPE_Q6_K> {
-  static constexpr int kT = 4;
+struct MI<RLH_TYPE_Q4_K> {
+  static constexpr uint32_t kT = 4;
   struct W {
-    uint4 ql0, ql1, qh;
-    uint2 sc;
-    uint32_t d;
+    u32x4_t hdr, q[8];
   };
-  struct A {
-    uint4 a[4];
-    float da[4], sa[4];
-  };
-  __device__ __forceinline__ static uint32_t units(uint32_t cols) { return cols >> 6; }
-  __device__ __forceinline__ static A act(const Q8Ptr& q, uint32_t u) {
-    uint32_t bi = u >> 2, half = (u >> 1) & 1, sub = u & 1;
-    uint32_t ab = bi * 8 + half * 4;
-    A a;
+  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+    r.hdr = gl_u4(tile + lane * 16);
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      a.a[c] = ld_g16(q.qs + (size_t)(ab + c) * 32 + sub * 16);
-      a.da[c] = ld_gf(q.d + ab + c);
-      a.sa[c] = (float)ld_gi(q.s16 + (size_t)(ab + c) * 2 + sub);
-    }
-    return a;
+    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + (k + 1) * 1024 + lane * 16);
   }
-  __device__ __forceinline__ static W load(const DevMat& w, uint32_t row, uint32_t u) {
-    uint32_t nsb = w.cols >> 8;
-    uint32_t bi = u >> 2, half = (u >> 1) & 1, sub = u & 1;
-    size_t sbi = (size_t)row * nsb + bi;
-    const uint8_t* ql = w.a + sbi * 128 + half * 64 + sub * 16;
-    W r;
-    r.ql0 = ld_nt16(ql);
-    r.ql1 = ld_nt16(ql + 32);
-    r.qh = ld_nt16(w.b + sbi * 64 + half * 32 + sub * 16);
-    r.sc = ld_g8(w.c + sbi * 16 + half * 8);
-    r.d = ld_g2(w.d + sbi * 2);
-    return r;
-  }
-  __device__ __forceinline__ static void terms(const W r, const A& a, uint32_t u, lfloat* t) {
-    uint32_t sub = u & 1;
-    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
-    const uint32_t l0[4] = {r.ql0.x, r.ql0.y, r.ql0.z, r.ql0.w};
-    const uint32_t l1[4] = {r.ql1.x, r.ql1.y, r.ql1.z, r.ql1.w};
-    const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    float d = f16_to_f32(r.d);
+  // Group g: low nibbles of q[2g], q[2g+1] = sub-block 2g, high = 2g+1.
+  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    const float d = f16_to_f32(r.hdr.x & 0xffff);
+    const float dmin = f16_to_f32(r.hdr.x >> 16);
+    const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;  // the 12 scale bytes
     float out[4];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const uint32_t av[4] = {a.a[c].x, a.a[c].y, a.a[c].z, a.a[c].w};
-      int ss = 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        uint32_t lo = (c & 1) ? l1[k] : l0[k];
-        uint32_t nib = (c < 2) ? (lo & m4) : ((lo >> 4) & m4);
-        uint32_t uu = nib | (((h[k] >> (2 * c)) & m2) << 4);
-        ss = sdot4(uu, av[k], ss);
+    for (int g = 0; g < 4; g++) {
+      // get_scale_min_k4 (quant.rs:176-185) for sub-blocks 2g and 2g+1
+      uint32_t sc1, m1, sc2, m2;
+      if (g < 2) {
+        const uint32_t sh1 = 16 * g, sh2 = 16 * g + 8;
+        sc1 = (s0 >> sh1) & 63;
+        m1 = (s1 >> sh1) & 63;
+        sc2 = (s0 >> sh2) & 63;
+        m2 = (s1 >> sh2) & 63;
+      } else {
+        const uint32_t sh1 = 16 * (g - 2), sh2 = sh1 + 8;
+        sc1 = ((s2 >> sh1) & 0xF) | (((s0 >> sh1) >> 6 & 3) << 4);
+        m1 = ((s2 >> sh1) >> 4 & 0xF) | (((s1 >> sh1) >> 6 & 3) << 4);
+        sc2 = ((s2 >> sh2) & 0xF) | (((s0 >> sh2) >> 6 & 3) << 4);
+        m2 = ((s2 >> sh2) >> 4 & 0xF) | (((s1 >> sh2) >> 6 & 3) << 4);
       }
-      // sc[sub + 2c] of the half's 8 scale bytes (simd.rs:626-629)
-      uint32_t word = (c < 2) ? r.sc.x : r.sc.y;
-      uint32_t shift = 8 * ((sub + 2 * c) & 3);
-      float scf = (float)(int8_t)((word >> shift) & 0xff);
-      out[c] = d * scf * ((float)ss - 32.0f * a.sa[c]) * a.da[c];
+      const uint32_t ab = j * 8 + 2 * g;
+      const RLH_LDS int8_t* pa = qblk(act, ab);
+      const u32x4_t a0 = lds_u4(pa), a1 = lds_u4(pa + 16), b0 = lds_u4(pa + 32), b1 = lds_u4(pa + 48);
+      const u32x4_t q0 = r.q[2 * g], q1 = r.q[2 * g + 1];
+      int i1 = dot16(q0 & m4, a0, 0);
+      i1 = dot16(q1 & m4, a1, i1);
+      int i2 = dot16((q0 >> 4) & m4, b0, 0);
+      i2 = dot16((q1 >> 4) & m4, b1, i2);
+      const float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+      const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+      const float da = act.d[ab], db = act.d[ab + 1];
+      const float sa = (float)act.s[ab], sb = (float)act.s[ab + 1];
+      out[g] = da * (d1 * (float)i1 - mm1 * sa) + db * (d2 * (float)i2 - mm2 * sb);
     }
-    f32x4_t v = {out[0], out[1], out[2], out[3]};
-    *(lf32x4*)t = v;
+    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
   }
 };
 
+// Q6_K terms in the reference order: for half { for sub { for c } }
+// (simd.rs:611-666), 16 per super-block.
 template <>
-struct MU<RLH_TYPE_Q8_0> {
-  static constexpr int kT = 1;
+struct MI<RLH_TYPE_Q6_K> {
+  static constexpr uint32_t kT = 16;
   struct W {
-    uint4 q0, q1;
+    u32x4_t ql[8], qh[4], sc;
     uint32_t d;
   };
-  struct A {
-    uint4 a0, a1;
-    float da;
-  };
-  __device__ __forceinline__ static uint32_t units(uint32_t cols) { return cols >> 5; }
-  __device__ __forceinline__ static A act(const Q8Ptr& q, uint32_t u) {
-    const int8_t* p = q.qs + (size_t)u * 32;
-    A a;
-    a.a0 = ld_g16(p);
-    a.a1 = ld_g16(p + 16);
-    a.da = ld_gf(q.d + u);
-    return a;
+  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.ql[k] = gl_u4(tile + k * 1024 + lane * 16);
+#pragma unroll
+    for (int k = 0; k < 4; k++) r.qh[k] = gl_u4(tile + (8 + k) * 1024 + lane * 16);
+    r.sc = gl_u4(tile + 12 * 1024 + lane * 16);
+    r.d = ld_g2(tile + 13 * 1024 + lane * 2);
   }
-  __device__ __forceinline__ static W load(const DevMat& w, uint32_t row, uint32_t u) {
-    size_t b = (size_t)row * (w.cols >> 5) + u;
-    const uint8_t* qp = w.a + b * 32;
-    W r;
-    r.q0 = ld_nt16(qp);
-    r.q1 = ld_nt16(qp + 16);
-    r.d = ld_g2(w.b + b * 2);
-    return r;
-  }
-  __device__ __forceinline__ static void terms(const W r, const A& a, uint32_t, lfloat* t) {
-    int i = 0;
-    i = sdot4(r.q0.x, a.a0.x, i); i = sdot4(r.q0.y, a.a0.y, i); i = sdot4(r.q0.z, a.a0.z, i);
-    i = sdot4(r.q0.w, a.a0.w, i); i = sdot4(r.q1.x, a.a1.x, i); i = sdot4(r.q1.y, a.a1.y, i);
-    i = sdot4(r.q1.z, a.a1.z, i); i = sdot4(r.q1.w, a.a1.w, i);
-    t[0] = f16_to_f32(r.d) * (float)i * a.da;
+  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
+    const float d = f16_to_f32(r.d);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const uint32_t wlo = h ? r.sc.z : r.sc.x, whi = h ? r.sc.w : r.sc.y;  // the half's 8 scale bytes
+      const uint32_t ab = j * 8 + 4 * h;
+      // the half's 128 activation bytes, scales and 16-value sums, read in
+      // one batch so the LDS latency is paid once per half
+      u32x4_t av[4][2];
+      float da[4], sa[4][2];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        av[c][0] = lds_u4(qblk(act, ab + c));
+        av[c][1] = lds_u4(qblk(act, ab + c) + 16);
+        da[c] = act.d[ab + c];
+        sa[c][0] = act.s16x32[(ab + c) * 2];
+        sa[c][1] = act.s16x32[(ab + c) * 2 + 1];
+      }
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const u32x4_t ql0 = r.ql[4 * h + s], ql1 = r.ql[4 * h + 2 + s], qh = r.qh[2 * h + s];
+        float out[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const u32x4_t lo = (c & 1) ? ql1 : ql0;
+          const u32x4_t nib = (c < 2) ? (lo & m4) : ((lo >> 4) & m4);
+          const u32x4_t uu = nib | (((qh >> (2 * c)) & m2) << 4);
+          const int ss = dot16(uu, av[c][s], 0);
+          const uint32_t bi = s + 2 * c;  // sc[sub + 2c] (simd.rs:626-629)
+          const float scf = (float)(int8_t)(((bi < 4 ? wlo : whi) >> (8 * (bi & 3))) & 0xff);
+          out[c] = d * scf * ((float)ss - sa[c][s]) * da[c];
+        }
+        *(lf32x4*)(t + 8 * h + 4 * s) = f32x4_t{out[0], out[1], out[2], out[3]};
+      }
+    }
   }
 };
 
+// Q8_0: item = 8 consecutive 32-value blocks (256 values).
 template <>
-struct MU<RLH_TYPE_Q4_0> {
-  static constexpr int kT = 1;
+struct MI<RLH_TYPE_Q8_0> {
+  static constexpr uint32_t kT = 8;
   struct W {
-    uint4 q;
-    uint32_t d;
+    u32x4_t q[16], dv;
   };
-  struct A {
-    uint4 a0, a1;
-    float da;
-    int s;
-  };
-  __device__ __forceinline__ static uint32_t units(uint32_t cols) { return cols >> 5; }
-  __device__ __forceinline__ static A act(const Q8Ptr& q, uint32_t u) {
-    const int8_t* p = q.qs + (size_t)u * 32;
-    A a;
-    a.a0 = ld_g16(p);
-    a.a1 = ld_g16(p + 16);
-    a.da = ld_gf(q.d + u);
-    a.s = ld_gi(q.s + u);
-    return a;
+  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+#pragma unroll
+    for (int k = 0; k < 16; k++) r.q[k] = gl_u4(tile + k * 1024 + lane * 16);
+    r.dv = gl_u4(tile + 16 * 1024 + lane * 16);
   }
-  __device__ __forceinline__ static W load(const DevMat& w, uint32_t row, uint32_t u) {
-    size_t b = (size_t)row * (w.cols >> 5) + u;
-    W r;
-    r.q = ld_nt16(w.a + b * 16);
-    r.d = ld_g2(w.b + b * 2);
-    return r;
-  }
-  __device__ __forceinline__ static void terms(const W r, const A& a, uint32_t, lfloat* t) {
-    const uint32_t m = 0x0F0F0F0Fu;
-    int i0 = 0, i1 = 0;
-    i0 = sdot4(r.q.x & m, a.a0.x, i0); i0 = sdot4(r.q.y & m, a.a0.y, i0);
-    i0 = sdot4(r.q.z & m, a.a0.z, i0); i0 = sdot4(r.q.w & m, a.a0.w, i0);
-    i1 = sdot4((r.q.x >> 4) & m, a.a1.x, i1); i1 = sdot4((r.q.y >> 4) & m, a.a1.y, i1);
-    i1 = sdot4((r.q.z >> 4) & m, a.a1.z, i1); i1 = sdot4((r.q.w >> 4) & m, a.a1.w, i1);
-    t[0] = f16_to_f32(r.d) * (float)(i0 + i1 - 8 * a.s) * a.da;
+  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+    const uint32_t dw[4] = {r.dv.x, r.dv.y, r.dv.z, r.dv.w};
+    float out[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t b = j * 8 + k;
+      const RLH_LDS int8_t* pa = qblk(act, b);
+      const int i = dot16(r.q[2 * k + 1], lds_u4(pa + 16), dot16(r.q[2 * k], lds_u4(pa), 0));
+      const float dk = f16_to_f32((dw[k >> 1] >> (16 * (k & 1))) & 0xffff);
+      out[k] = dk * (float)i * act.d[b];  // simd.rs:891
+    }
+    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
+    *(lf32x4*)(t + 4) = f32x4_t{out[4], out[5], out[6], out[7]};
   }
 };
 
-// In-order sum of n terms (the per-row f32 chain).
-__device__ __forceinline__ float chain(float acc, const lfloat* t, uint32_t n) {
+// Q4_0: item = 8 consecutive 32-value blocks.
+template <>
+struct MI<RLH_TYPE_Q4_0> {
+  static constexpr uint32_t kT = 8;
+  struct W {
+    u32x4_t q[8], dv;
+  };
+  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + k * 1024 + lane * 16);
+    r.dv = gl_u4(tile + 8 * 1024 + lane * 16);
+  }
+  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    const uint32_t dw[4] = {r.dv.x, r.dv.y, r.dv.z, r.dv.w};
+    float out[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t b = j * 8 + k;
+      const RLH_LDS int8_t* pa = qblk(act, b);
+      const int i0 = dot16(r.q[k] & m4, lds_u4(pa), 0);
+      const int i1 = dot16((r.q[k] >> 4) & m4, lds_u4(pa + 16), 0);
+      const float dk = f16_to_f32((dw[k >> 1] >> (16 * (k & 1))) & 0xffff);
+      out[k] = dk * (float)(i0 + i1 - 8 * act.s[b]) * act.d[b];  // simd.rs:863
+    }
+    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
+    *(lf32x4*)(t + 4) = f32x4_t{out[4], out[5], out[6], out[7]};
+  }
+};
+
+// In-order sum of n terms (the per-row f32 chain); 32 terms per batch of
+// LDS reads so that the reads overlap the dependent adds.
+__device__ __forceinline__ float chain(const lfloat* t, uint32_t n) {
+  float acc = 0.0f;
   uint32_t k = 0;
-  for (; k + 4 <= n; k += 4) {
-    f32x4_t v = *(const lf32x4*)(t + k);
-    acc = acc + v.x;
-    acc = acc + v.y;
-    acc = acc + v.z;
-    acc = acc + v.w;
+  for (; k + 32 <= n; k += 32) {
+    f32x4_t v[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) v[q] = *(const lf32x4*)(t + k + 4 * q);
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      acc = acc + v[q].x;
+      acc = acc + v[q].y;
+      acc = acc + v[q].z;
+      acc = acc + v[q].w;
+    }
   }
   for (; k < n; k++) acc = acc + t[k];
   return acc;
 }
 
-// Rows [row0, row0 + nrows) of matrix `w` (nrows <= 4 * NS * P). Row r is
-// summed by block thread chain_lane0 + r, which gets the total as result.
-// Lane layout in P-packed groups: lane -> (sub = lane / (64/P), unit
-// offset = lane % (64/P)); wave w owns rows [w*NS*P, (w+1)*NS*P).
-template <uint32_t TY, int P, int NS>
-__device__ __forceinline__ float mv_rows(const DevMat& w, const Q8Ptr& act, uint32_t row0, uint32_t nrows, uint32_t chain_lane0,
-                         lfloat* tile) {
-  using U = MU<TY>;
-  constexpr int kT = U::kT;
-  constexpr uint32_t kUnits = 64 / P;      // units of one row per wave instruction
-  constexpr uint32_t kStride = 64 * kT + 4;  // floats per tile row
-  constexpr uint32_t R = 4 * NS * P;
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t sub = lane / kUnits, ul = lane % kUnits;
-  const uint32_t nunits = U::units(w.cols);
-  float acc = 0.0f;
-  const bool chain_lane = threadIdx.x >= chain_lane0 && threadIdx.x < chain_lane0 + nrows;
-  const uint32_t my_row = threadIdx.x - chain_lane0;
-  uint32_t prev_cn = 0;
-  uint32_t buf = 0;
-  for (uint32_t c0 = 0; c0 < nunits; c0 += kUnits) {
-    const uint32_t cn = nunits - c0 < kUnits ? nunits - c0 : kUnits;
-    const uint32_t u = c0 + ul;
-    const bool uok = ul < cn;
-    typename U::W raw[NS];
-#pragma unroll
-    for (int i = 0; i < NS; i++) {
-      uint32_t r = wave * NS * P + (uint32_t)i * P + sub;
-      if (uok && r < nrows) raw[i] = U::load(w, row0 + r, u);
-    }
-    // chain of the previous chunk while this chunk's loads are in flight
-    if (prev_cn && chain_lane) acc = chain(acc, tile + ((buf ^ 1) * R + my_row) * kStride, prev_cn * kT);
-    if (uok) {
-      const typename U::A a = U::act(act, u);
-#pragma unroll
-      for (int i = 0; i < NS; i++) {
-        uint32_t r = wave * NS * P + (uint32_t)i * P + sub;
-        if (r < nrows) U::terms(raw[i], a, u, tile + (buf * R + r) * kStride + ul * kT);
-      }
+// Asynchronous copy of n bytes (a multiple of 16) from HBM into LDS with
+// global_load_lds_dwordx4: wave `wave` of `nw` copies 1 KB pieces wave,
+// wave + nw, ...; lanes past the end are masked off. No registers are
+// involved, so the copy overlaps the weight loads already in flight.
+__device__ __forceinline__ void lds_dma(RLH_LDS void* dst, const void* src, uint32_t n, uint32_t wave, uint32_t nw) {
+  const uint32_t lane = threadIdx.x & 63;
+  for (uint32_t off = wave * 1024; off < n; off += nw * 1024) {
+    if (off + lane * 16 < n)
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)src + off + lane * 16),
+                                       (RLH_LDS void*)((RLH_LDS uint8_t*)dst + off), 16, 0, 0);
+  }
+}
+
+// Builds the Q8 activation row in LDS from the f32 row x: optionally
+// rmsnorm(x) * w first (rmsnorm_core, simd.rs:282-326: 32 FMA chains, AVX2
+// reduction tree, s = 1/sqrt(ss/n + eps), out = (x*s)*w), then
+// quantize_q8 (simd.rs:116-203). xs and ws (cols floats each) are only used
+// here, so they may alias the term tiles.
+__device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* ws,
+                                                 lfloat* misc) {
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6, nthreads = blockDim.x;
+  const uint32_t cols = L.cols, nb = cols / 32;
+  lds_dma(xs, L.x, cols * 4, wave, nw);
+  if (L.nw) lds_dma(ws, L.nw, cols * 4, wave, nw);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and first weights) have landed
+  __syncthreads();
+  float s = 1.0f;
+  if (L.nw) {
+    if (tid < 64) {
+      const float ss = rms_sumsq_lds(xs, (int)cols);
+      if (tid == 0) misc[0] = 1.0f / sqrtf(ss / (float)cols + L.eps);  // simd.rs:315
     }
     __syncthreads();
-    prev_cn = cn;
-    buf ^= 1;
+    s = misc[0];
   }
-  if (prev_cn && chain_lane) acc = chain(acc, tile + ((buf ^ 1) * R + my_row) * kStride, prev_cn * kT);
+  // 8 lanes per 32-value block, 4 values per lane (groups of 8 lanes stay
+  // together through the loop, so the width-8 shuffles see whole groups)
+  for (uint32_t b = tid / 8; b < nb; b += nthreads / 8) {
+    const uint32_t l = tid & 7, i = b * 32 + 4 * l;
+    const f32x4_t xv = *(const lf32x4*)(xs + i);
+    float v0 = xv.x, v1 = xv.y, v2 = xv.z, v3 = xv.w;
+    if (L.nw) {
+      const f32x4_t wv = *(const lf32x4*)(ws + i);
+      v0 = (v0 * s) * wv.x;
+      v1 = (v1 * s) * wv.y;
+      v2 = (v2 * s) * wv.z;
+      v3 = (v3 * s) * wv.w;
+    }
+    // amax over the block (max is order-free), then exact integer sums
+    const float a0 = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+    float a = fmaxf(a0, dpp_f<kDppXor1>(a0));
+    a = fmaxf(a, dpp_f<kDppXor2>(a));
+    a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
+    const float d = a / 127.0f;
+    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = cvtps_packs_i8(__builtin_rintf(v0 * inv));
+    const int q1 = cvtps_packs_i8(__builtin_rintf(v1 * inv));
+    const int q2 = cvtps_packs_i8(__builtin_rintf(v2 * inv));
+    const int q3 = cvtps_packs_i8(__builtin_rintf(v3 * inv));
+    int sm = q0 + q1 + q2 + q3;
+    sm = sm + dpp_i<kDppXor1>(sm);
+    sm = sm + dpp_i<kDppXor2>(sm);  // sum of the 16-value half (lanes 0-3 / 4-7)
+    const int tot = sm + dpp_i<kDppHalfMirror>(sm);
+    *(RLH_LDS uint32_t*)(la.qs + (i >> 8) * kSbStride + (i & 255)) =
+        (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
+    if (l == 0) {
+      la.d[b] = d;
+      la.s[b] = tot;
+      la.s16x32[2 * b] = 32.0f * (float)sm;
+    } else if (l == 4) {
+      la.s16x32[2 * b + 1] = 32.0f * (float)sm;
+    }
+  }
   __syncthreads();
-  return acc;
 }
 
-template <uint32_t TY, int NS>
-__device__ __forceinline__ float mv_rows_p(const DevMat& w, const Q8Ptr& act, uint32_t row0, uint32_t nrows, uint32_t chain_lane0,
-                           lfloat* tile) {
-  uint32_t units = MU<TY>::units(w.cols);
-  if (units <= 16) return mv_rows<TY, 4, NS>(w, act, row0, nrows, chain_lane0, tile);
-  if (units <= 32) return mv_rows<TY, 2, NS>(w, act, row0, nrows, chain_lane0, tile);
-  return mv_rows<TY, 1, NS>(w, act, row0, nrows, chain_lane0, tile);
-}
-
-template <int NS>
-__device__ __forceinline__ float mv_dispatch(const DevMat& w, const Q8Ptr& act, uint32_t row0, uint32_t nrows, uint32_t chain_lane0,
-                             lfloat* tile) {
-  switch (w.ty) {
-    case RLH_TYPE_Q4_K: return mv_rows_p<RLH_TYPE_Q4_K, NS>(w, act, row0, nrows, chain_lane0, tile);
-    case RLH_TYPE_Q6_K: return mv_rows_p<RLH_TYPE_Q6_K, NS>(w, act, row0, nrows, chain_lane0, tile);
-    case RLH_TYPE_Q8_0: return mv_rows_p<RLH_TYPE_Q8_0, NS>(w, act, row0, nrows, chain_lane0, tile);
-    case RLH_TYPE_Q4_0: return mv_rows_p<RLH_TYPE_Q4_0, NS>(w, act, row0, nrows, chain_lane0, tile);
-    default: return 0.0f;
+__device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
   }
 }
 
-// All segments of one launch use the same NS; a segment's rows per block is
-// R = 4 * NS * P with P from its row width (host computes the same).
-template <int NS>
-__global__ void __launch_bounds__(kThreads) k_mv(MvLaunch L) {
-  extern __shared__ float tile_generic[];
-  lfloat* tile = (lfloat*)tile_generic;
-  uint32_t s = 0;
-  if (L.nseg > 1 && blockIdx.x >= L.seg[1].wg_begin) s = 1;
-  if (L.nseg > 2 && blockIdx.x >= L.seg[2].wg_begin) s = 2;
-  const MvSeg& g = L.seg[s];
-  const uint32_t wg = blockIdx.x - g.wg_begin;
-  const uint32_t R = g.rows_per_wg;
-  const uint32_t row0 = wg * R;
-  const uint32_t nrows = g.w.rows - row0 < R ? g.w.rows - row0 : R;
-  if (!g.pair) {
-    float acc = mv_dispatch<NS>(g.w, g.act, row0, nrows, 0, tile);
-    if (threadIdx.x < nrows) {
-      uint32_t r = row0 + threadIdx.x;
-      if (g.resid) {  // x += xb (model.rs:714-716, 726-728)
-        RLH_GLOBAL float* x = (RLH_GLOBAL float*)g.resid;
-        x[r] = x[r] + acc;
-      }
-      if (g.y) ((RLH_GLOBAL float*)g.y)[r] = acc;
+__device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const uint32_t oi = __shfl_xor(bi, m);
+    argmax_merge(bv, bi, ov, oi);
+  }
+}
+
+// The body of one block for weight type TY; NM = 2 in PAIR mode (gate and
+// up share type and tiling).
+template <uint32_t TY, int NM>
+__device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc) {
+  using I = MI<TY>;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
+  const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
+  const uint32_t TR = g.w.tr, TJ = g.w.tj, ntj = g.w.ntj, RB = R / TR;
+  const uint32_t rows = g.w.rows, row0 = blk * R;
+  const uint32_t nrows = rows - row0 < R ? rows - row0 : R;
+  const uint32_t rt0 = blk * RB, nrt = (rows + TR - 1) / TR;
+  const uint32_t ntiles = (nrt - rt0 < RB ? nrt - rt0 : RB) * ntj;
+  const size_t tile_bytes = (size_t)64 * g.w.ib;
+  const uint32_t stride = L.tile_stride;
+
+  LAct la;
+  la.qs = (RLH_LDS int8_t*)lds;
+  la.d = (RLH_LDS float*)((RLH_LDS int8_t*)lds + nsb * kSbStride);
+  la.s = (RLH_LDS int32_t*)(la.d + nb);
+  la.s16x32 = (RLH_LDS float*)(la.s + nb);
+  lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
+
+  // first tile: its weights are in flight while the activation is built
+  typename I::W wr[NM];
+  uint32_t t = wave;
+  if (t < ntiles) {
+    const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
+    I::load(wr[0], g.w.a + off, lane);
+    if (NM == 2) I::load(wr[NM - 1], g.w2.a + off, lane);
+  }
+  stage_activation(L, la, region, region + cols, misc);
+  while (t < ntiles) {
+    const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
+    I::terms(wr[0], la, j, region + rl * stride + j * I::kT);
+    if (NM == 2) I::terms(wr[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
+    t += nwaves;
+    if (t < ntiles) {
+      const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
+      I::load(wr[0], g.w.a + off, lane);
+      if (NM == 2) I::load(wr[NM - 1], g.w2.a + off, lane);
+    }
+  }
+  __syncthreads();
+
+  // wave m < NM: lane r adds row r's terms of matrix m in order; lanes past
+  // the valid rows chain a copy of row 0 so that the wave stays converged
+  float acc = 0.0f;
+  if (wave < (uint32_t)NM) acc = chain(region + (wave * R + (lane < nrows ? lane : 0)) * stride, nsb * I::kT);
+  if (NM == 2) {
+    if (wave == 1) misc[4 + lane] = acc;
+    __syncthreads();
+  }
+  if (wave != 0) return;  // wave 0 runs the epilogue
+
+  if (NM == 2) {
+    if (lane < nrows) {
+      const float x = acc, up = misc[4 + lane];
+      ((RLH_GLOBAL float*)g.y)[row0 + lane] = (x / (1.0f + expf_glibc(-x))) * up;  // silu(g) * u
     }
     return;
   }
-  // PAIR (R == 32): gate rows summed in lanes [0, 32), up rows in [32, 64).
-  float ag = mv_dispatch<NS>(g.w, g.act, row0, nrows, 0, tile);
-  float au = mv_dispatch<NS>(g.w2, g.act, row0, nrows, 32, tile);
-  float acc = threadIdx.x < 32 ? ag : au;
-  if (threadIdx.x < 64) {
-    float up = __shfl(acc, (int)(threadIdx.x + 32) & 63);
-    if (threadIdx.x < 32) {
-      float x = acc;
-      float h = (x / (1.0f + expf_glibc(-x))) * up;  // silu(g) * u (ops.rs:393-395)
-      if (g.y) ((RLH_GLOBAL float*)g.y)[row0 + threadIdx.x] = h;
-      q8_quant_block32(h, g.hq, row0 / 32);
+  const bool mine = lane < nrows;
+  const uint32_t row = row0 + lane;
+  if (mine) {
+    if (g.resid) {
+      RLH_GLOBAL float* x = (RLH_GLOBAL float*)g.resid;
+      x[row] = x[row] + acc;
     }
+    if (g.y) ((RLH_GLOBAL float*)g.y)[row] = acc;
   }
+  if (!L.has_argmax) return;
+  float bv = mine ? acc : -__int_as_float(0x7f800000);
+  uint32_t bi = mine ? row : 0xffffffffu;
+  wave_argmax(bv, bi);
+  uint32_t last = 0;
+  if (lane == 0) {
+    ((RLH_GLOBAL float*)L.am.pv)[blockIdx.x] = bv;
+    ((RLH_GLOBAL uint32_t*)L.am.pi)[blockIdx.x] = bi;
+    __threadfence();
+    last = atomicAdd(L.am.counter, 1u) == gridDim.x - 1 ? 1u : 0u;
+  }
+  last = __shfl(last, 0);
+  if (!last) return;
+  // the last block to finish reduces every block's candidate
+  __threadfence();
+  float b2 = -__int_as_float(0x7f800000);
+  uint32_t j2 = 0xffffffffu;
+  for (uint32_t k = lane; k < gridDim.x; k += 64)
+    argmax_merge(b2, j2, __hip_atomic_load(L.am.pv + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                 __hip_atomic_load(L.am.pi + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  wave_argmax(b2, j2);
+  if (lane == 0) {
+    const uint32_t best = j2 == 0xffffffffu ? 0u : j2;  // all NaN -> 0 (main.rs:453-463)
+    L.am.tok[0] = best;
+    if (L.am.step) {
+      const uint32_t s = L.am.step[0] + 1;
+      L.am.hist[s] = best;
+      L.am.step[0] = s;
+      L.am.pos[0] = L.am.pos[0] + 1;
+    }
+    atomicExch(L.am.counter, 0u);
+  }
+}
+
+template <int NM, int MAXT>
+__global__ void __launch_bounds__(MAXT) k_mv(MvLaunch L) {
+  extern __shared__ __attribute__((aligned(16))) float lds_generic[];
+  __shared__ float misc_generic[4 + 64];
+  lfloat* lds = (lfloat*)lds_generic;
+  lfloat* misc = (lfloat*)misc_generic;
+  // segment of this block, selected without indexing the argument array
+  // (a dynamic index would copy the kernel argument to private memory)
+  MvSeg g = L.seg[0];
+  if (L.nseg > 1 && blockIdx.x >= L.seg[1].blk_begin) g = L.seg[1];
+  if (L.nseg > 2 && blockIdx.x >= L.seg[2].blk_begin) g = L.seg[2];
+  const uint32_t blk = blockIdx.x - g.blk_begin;
+  switch (g.w.ty) {
+    case RLH_TYPE_Q4_K: mv_block<RLH_TYPE_Q4_K, NM>(L, g, blk, lds, misc); break;
+    case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM>(L, g, blk, lds, misc); break;
+    case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc); break;
+    case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc); break;
+    default: break;
+  }
+}
+
+constexpr uint32_t kMaxLds = 150u * 1024u;
+
+// LDS bytes of a plan with R rows per block.
+uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
+  const uint32_t cols = p.L.cols, nsb = cols / 256, nb = cols / 32;
+  const uint32_t act = (nsb * kSbStride + nb * 16 + 15) & ~15u;
+  const uint32_t stride = nsb * p.max_terms + 4;
+  const uint32_t tile = nm * R * stride * 4;
+  const uint32_t staging = (p.L.nw ? 2u : 1u) * cols * 4;
+  return act + std::max(tile, staging);
+}
+
+uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
+  uint32_t b = 0;
+  for (uint32_t s = 0; s < p.L.nseg; s++) b += (p.L.seg[s].w.rows + R - 1) / R;
+  return b;
 }
 
 }  // namespace
 
-void launch_mv(hipStream_t st, const MvLaunch& L, uint32_t total_wgs, uint32_t lds_bytes, uint32_t ns) {
-  switch (ns) {
-    case 1: hipLaunchKernelGGL(k_mv<1>, dim3(total_wgs), dim3(kThreads), lds_bytes, st, L); break;
-    case 2: hipLaunchKernelGGL(k_mv<2>, dim3(total_wgs), dim3(kThreads), lds_bytes, st, L); break;
-    case 4: hipLaunchKernelGGL(k_mv<4>, dim3(total_wgs), dim3(kThreads), lds_bytes, st, L); break;
-    default: hipLaunchKernelGGL(k_mv<8>, dim3(total_wgs), dim3(kThreads), lds_bytes, st, L); break;
+void mv_plan_init(MvPlan& p, uint32_t cols, const float* x) {
+  p = MvPlan{};
+  p.L.cols = cols;
+  p.L.x = x;
+}
+
+void mv_plan_norm(MvPlan& p, const float* w, float eps) {
+  p.L.nw = w;
+  p.L.eps = eps;
+}
+
+void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
+  MvSeg& g = p.L.seg[p.L.nseg++];
+  g = MvSeg{};
+  g.w = w;
+  g.y = y;
+  g.resid = resid;
+  p.rows += w.rows;
+  p.max_terms = std::max(p.max_terms, mv_terms_per_sb(w.ty));
+}
+
+void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, float* h) {
+  MvSeg& g = p.L.seg[p.L.nseg++];
+  g = MvSeg{};
+  g.w = gate;
+  g.w2 = up;
+  g.y = h;
+  g.pair = 1;
+  p.rows += gate.rows;
+  p.max_terms = std::max(p.max_terms, std::max(mv_terms_per_sb(gate.ty), mv_terms_per_sb(up.ty)));
+}
+
+void mv_plan_argmax(MvPlan& p, const MvArgmax& am) {
+  p.L.has_argmax = 1;
+  p.L.am = am;
+}
+
+// Block shape: R rows = whole row-tiles, at most 64; the largest R that
+// gives at least one block per CU (256) and fits the LDS, else the smallest
+// that fits. One wave per tile of the block (at most 16 waves).
+bool mv_plan_finish(MvPlan& p) {
+  const uint32_t nm = (p.L.nseg == 1 && p.L.seg[0].pair) ? 2u : 1u;
+  const uint32_t nsb = p.L.cols / 256;
+  if (p.L.nseg == 0 || nsb == 0) return false;
+  const uint32_t tr = p.L.seg[0].w.tr, ntj = p.L.seg[0].w.ntj;
+  for (uint32_t s = 0; s < p.L.nseg; s++)
+    if (p.L.seg[s].w.tr != tr || p.L.seg[s].w.cols != p.L.cols) return false;
+  if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows)) return false;
+  uint32_t best = 0;
+  for (uint32_t R = 64; R >= tr; R /= 2) {
+    if (plan_lds(p, R, nm) > kMaxLds) continue;
+    best = R;
+    if (plan_blocks(p, R) >= 256) break;
+  }
+  if (!best) return false;
+  const uint32_t R = best;
+  p.L.rows_per_blk = R;
+  p.L.tile_stride = nsb * p.max_terms + 4;
+  const uint32_t act = nsb * kSbStride + (p.L.cols / 32) * 16;
+  p.L.region_off = (act + 15) & ~15u;
+  p.lds = plan_lds(p, R, nm);
+  p.waves = std::min<uint32_t>(16, (R / tr) * ntj);
+  if (p.waves < nm) p.waves = nm;
+  p.blocks = 0;
+  for (uint32_t s = 0; s < p.L.nseg; s++) {
+    p.L.seg[s].blk_begin = p.blocks;
+    p.blocks += (p.L.seg[s].w.rows + R - 1) / R;
+  }
+  return true;
+}
+
+uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
+  MvPlan p;
+  mv_plan_init(p, cols, nullptr);
+  DevMat w{};
+  w.ty = ty;
+  w.rows = rows;
+  w.cols = cols;
+  w.ib = item_bytes(ty);
+  w.tj = tile_width(cols / 256);
+  w.tr = 64 / w.tj;
+  w.ntj = cols / 256 / w.tj;
+  mv_plan_add(p, w, nullptr, nullptr);
+  p.L.nw = (const float*)&p;  // the logits plan has the norm prologue (only its LDS size matters here)
+  if (!mv_plan_finish(p)) return 0;
+  return p.blocks;
+}
+
+void mv_launch(hipStream_t st, const MvPlan& p) {
+  const bool pair = p.L.nseg == 1 && p.L.seg[0].pair;
+  const dim3 grid(p.blocks), blk(64 * p.waves);
+  if (pair) {
+    if (p.waves <= 8) hipLaunchKernelGGL((k_mv<2, 512>), grid, blk, p.lds, st, p.L);
+    else hipLaunchKernelGGL((k_mv<2, 1024>), grid, blk, p.lds, st, p.L);
+  } else {
+    if (p.waves <= 8) hipLaunchKernelGGL((k_mv<1, 512>), grid, blk, p.lds, st, p.L);
+    else hipLaunchKernelGGL((k_mv<1, 1024>), grid, blk, p.lds, st, p.L);
   }
 }
 
 bool mv_set_max_lds(size_t bytes) {
-  const void* fns[] = {(const void*)k_mv<1>, (const void*)k_mv<2>, (const void*)k_mv<4>, (const void*)k_mv<8>};
+  const void* fns[] = {(const void*)k_mv<1, 512>, (const void*)k_mv<1, 1024>, (const void*)k_mv<2, 512>,
+                       (const void*)k_mv<2, 1024>};
   for (const void* f : fns)
     if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) return false;
   return true;

@@ -245,61 +245,62 @@ __device__ __forceinline__ float4 ld_gf4(const float* p) {
 __device__ __forceinline__ int ld_gi(const int32_t* p) { return *(const RLH_GLOBAL int32_t*)p; }
 
 // ---------------------------------------------------------------------------
-// Element dequantisation in the device layouts (quant.rs:191-385).
+// Element dequantisation in the device layout (quant.rs:191-385).
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t item_u8(const DevMat& w, uint32_t row, uint32_t j, uint32_t o) {
+  return w.a[item_offset(w, row, j, o)];
+}
+__device__ __forceinline__ uint32_t item_u16(const DevMat& w, uint32_t row, uint32_t j, uint32_t o) {
+  return item_u8(w, row, j, o) | (item_u8(w, row, j, o + 1) << 8);
+}
+
 __device__ __forceinline__ float dq_elem(const DevMat& w, uint32_t row, uint32_t i) {
+  const uint32_t j = i >> 8, p = i & 255;
   switch (w.ty) {
     case RLH_TYPE_Q4_K: {
-      uint32_t bi = i >> 8, p = i & 255, g = p >> 6, hi = (p >> 5) & 1, l = p & 31;
-      const uint8_t* sb = w.a + (size_t)row * w.row_bytes + (size_t)bi * 144;
-      float d = f16_to_f32(sb[0] | (sb[1] << 8));
-      float dmin = f16_to_f32(sb[2] | (sb[3] << 8));
+      const uint32_t g = p >> 6, hi = (p >> 5) & 1, l = p & 31;
+      const float d = f16_to_f32(item_u16(w, row, j, 0));
+      const float dmin = f16_to_f32(item_u16(w, row, j, 2));
+      uint8_t sb[12];
+      for (int k = 0; k < 12; k++) sb[k] = (uint8_t)item_u8(w, row, j, 4 + k);
       uint32_t sc, m;
-      scale_min_k4((int)(2 * g + hi), sb + 4, sc, m);
-      float d1 = d * (float)sc;
-      float mm1 = dmin * (float)m;
-      uint32_t q = (sb[16 + 32 * g + l] >> (4 * hi)) & 0xF;
+      scale_min_k4((int)(2 * g + hi), sb, sc, m);
+      const float d1 = d * (float)sc;
+      const float mm1 = dmin * (float)m;
+      const uint32_t q = (item_u8(w, row, j, 16 + 32 * g + l) >> (4 * hi)) & 0xF;
       return d1 * (float)q - mm1;
     }
     case RLH_TYPE_Q6_K: {
-      uint32_t nsb = w.cols >> 8;
-      uint32_t bi = i >> 8, p = i & 255, half = p >> 7, pp = p & 127, quarter = pp >> 5, l = pp & 31;
-      size_t sbi = (size_t)row * nsb + bi;
-      const uint8_t* ql = w.a + sbi * 128 + half * 64;
-      const uint8_t* qh = w.b + sbi * 64 + half * 32;
-      const int8_t* sc = (const int8_t*)(w.c + sbi * 16 + half * 8);
-      const uint8_t* dd = w.d + sbi * 2;
-      float d = f16_to_f32(dd[0] | (dd[1] << 8));
-      uint32_t byte = ql[(quarter & 1) * 32 + l];
-      uint32_t nib = quarter < 2 ? (byte & 0xF) : (byte >> 4);
-      uint32_t h2 = (qh[l] >> (2 * quarter)) & 3;
-      int q = (int)(nib | (h2 << 4)) - 32;
-      return d * (float)sc[(l >> 4) + 2 * quarter] * (float)q;
+      const uint32_t half = p >> 7, pp = p & 127, quarter = pp >> 5, l = pp & 31;
+      const float d = f16_to_f32(item_u16(w, row, j, 208));
+      const uint32_t byte = item_u8(w, row, j, half * 64 + (quarter & 1) * 32 + l);
+      const uint32_t nib = quarter < 2 ? (byte & 0xF) : (byte >> 4);
+      const uint32_t h2 = (item_u8(w, row, j, 128 + half * 32 + l) >> (2 * quarter)) & 3;
+      const int q = (int)(nib | (h2 << 4)) - 32;
+      const float sc = (float)(int8_t)item_u8(w, row, j, 192 + half * 8 + (l >> 4) + 2 * quarter);
+      return d * sc * (float)q;
     }
     case RLH_TYPE_Q8_0: {
-      uint32_t nb = w.cols >> 5;
-      size_t b = (size_t)row * nb + (i >> 5);
-      float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
-      return (float)(int8_t)w.a[b * 32 + (i & 31)] * d;
+      const uint32_t k = p >> 5;
+      const float d = f16_to_f32(item_u16(w, row, j, 256 + 2 * k));
+      return (float)(int8_t)item_u8(w, row, j, p) * d;
     }
     case RLH_TYPE_Q4_0: {
-      uint32_t nb = w.cols >> 5;
-      size_t b = (size_t)row * nb + (i >> 5);
-      float d = f16_to_f32(w.b[2 * b] | (w.b[2 * b + 1] << 8));
-      uint32_t j = i & 31;
-      uint32_t byte = w.a[b * 16 + (j & 15)];
-      float x = (float)((int)(j < 16 ? (byte & 0xF) : (byte >> 4)) - 8);
+      const uint32_t k = p >> 5, t = p & 31;
+      const float d = f16_to_f32(item_u16(w, row, j, 128 + 2 * k));
+      const uint32_t byte = item_u8(w, row, j, k * 16 + (t & 15));
+      const float x = (float)((int)(t < 16 ? (byte & 0xF) : (byte >> 4)) - 8);
       return x * d;
     }
     case RLH_TYPE_F32:
       return ((const float*)(w.a + (size_t)row * w.row_bytes))[i];
     case RLH_TYPE_F16: {
-      const uint8_t* p = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
-      return f16_to_f32(p[0] | (p[1] << 8));
+      const uint8_t* q = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
+      return f16_to_f32(q[0] | (q[1] << 8));
     }
     case RLH_TYPE_BF16: {
-      const uint8_t* p = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
-      return __uint_as_float((uint32_t)(p[0] | (p[1] << 8)) << 16);
+      const uint8_t* q = w.a + (size_t)row * w.row_bytes + 2 * (size_t)i;
+      return __uint_as_float((uint32_t)(q[0] | (q[1] << 8)) << 16);
     }
     default:
       return 0.0f;
