@@ -277,7 +277,6 @@ struct rlh_cache {
   float* pv = nullptr;
   uint32_t* pi = nullptr;
   uint32_t nparts = 256;        // partials of the standalone argmax (rlh_greedy_next)
-  uint32_t* am_counter = nullptr;  // block counter of the fused logits argmax
   uint32_t* host_st = nullptr;  // pinned staging for tok/pos
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
   bool debug = false;
@@ -313,14 +312,15 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   const float scale = 1.0f / std::sqrt((float)hd);  // model.rs:616
   uint32_t* tok = c->st_dev;
   uint32_t* pos = c->st_dev + 1;
+  // x = embedding row; Q8 of rmsnorm(x) for the first layer (model.rs:612-621)
   launch_embed(st, m->token_embd.dm, tok, 1, c->x);
+  launch_rmsnorm_q8(st, c->x, m->layers[0].attn_norm.p, E, 1, eps, c->act_e, nullptr);
   const uint32_t qd = H * hd, F = cfg.n_ff;
   for (uint32_t l = 0; l < cfg.n_layer; l++) {
     Layer& L = m->layers[l];
-    {  // rmsnorm + Q8 (block prologue), then q, k, v (model.rs:621-624)
+    {  // q, k, v (model.rs:622-624)
       MvPlan p;
-      mv_plan_init(p, E, c->x);
-      mv_plan_norm(p, L.attn_norm.p, eps);
+      mv_plan_init(p, E, c->act_e);
       mv_plan_add(p, L.q.dm, c->q, nullptr);
       mv_plan_add(p, L.k.dm, c->k, nullptr);
       mv_plan_add(p, L.v.dm, c->v, nullptr);
@@ -354,27 +354,29 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       launch_attn_scores(st, a, 1, true);
       launch_attn_out(st, a, 1);
     }
-    {  // attn_output, x += (model.rs:713-716)
+    {  // attn_output, x += (model.rs:713-716); Q8 of rmsnorm(x, ffn_norm) (719)
       MvPlan p;
-      mv_plan_init(p, qd, c->attn);
+      mv_plan_init(p, qd, c->act_q);
       mv_plan_add(p, L.o.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
+      launch_rmsnorm_q8(st, c->x, L.ffn_norm.p, E, 1, eps, c->act_e, nullptr);
     }
-    {  // rmsnorm + Q8, gate/up, silu(g)*u, Q8 of h (model.rs:719-724)
+    {  // gate, up, silu(g)*u and its Q8 blocks (model.rs:720-724)
       MvPlan p;
-      mv_plan_init(p, E, c->x);
-      mv_plan_norm(p, L.ffn_norm.p, eps);
-      mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->g);
+      mv_plan_init(p, E, c->act_e);
+      mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
       mv_plan_finish(p);
       mv_launch(st, p);
     }
-    {  // ffn_down, x += (model.rs:725-728)
+    {  // ffn_down, x += (model.rs:725-728); Q8 of the next rmsnorm(x)
+      const float* next_norm = l + 1 < cfg.n_layer ? m->layers[l + 1].attn_norm.p : m->output_norm.p;
       MvPlan p;
-      mv_plan_init(p, F, c->g);
+      mv_plan_init(p, F, c->act_f);
       mv_plan_add(p, L.down.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
+      launch_rmsnorm_q8(st, c->x, next_norm, E, 1, eps, c->act_e, nullptr);
     }
     if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
       (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
@@ -382,15 +384,14 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   }
   if (kind == STEP_NOLOGITS) return;
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
-  {  // output_norm + logits (model.rs:733-737), greedy argmax fused
+  {  // logits of rmsnorm(x, output_norm) (model.rs:733-737), greedy argmax fused
     MvPlan p;
-    mv_plan_init(p, E, c->x);
-    mv_plan_norm(p, m->output_norm.p, eps);
+    mv_plan_init(p, E, c->act_e);
     mv_plan_add(p, ow.dm, c->logits, nullptr);
-    if (kind == STEP_GREEDY)
-      mv_plan_argmax(p, MvArgmax{c->pv, c->pi, c->am_counter, tok, pos, c->st_dev + 2, c->hist});
+    if (kind == STEP_GREEDY) mv_plan_argmax(p, MvArgmax{c->pv, c->pi});
     mv_plan_finish(p);
     mv_launch(st, p);
+    if (kind == STEP_GREEDY) launch_argmax_final(st, c->pv, c->pi, p.blocks, tok, pos, c->st_dev + 2, c->hist);
   }
 }
 
@@ -563,25 +564,30 @@ int rlh_model_finalize(rlh_model* m) {
     Layer& L = m->layers[l];
     if (L.gate.ty != L.up.ty)
       return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": ffn_gate and ffn_up must share a ggml type");
-    const float* dummy = (const float*)m;  // plans are only sized here, never launched
+    const Q8Mut none{};
     MvPlan p;
-    mv_plan_init(p, (uint32_t)E, dummy);
-    mv_plan_norm(p, dummy, 0.0f);
+    mv_plan_init(p, (uint32_t)E, none);
     mv_plan_add(p, L.q.dm, nullptr, nullptr);
     mv_plan_add(p, L.k.dm, nullptr, nullptr);
     mv_plan_add(p, L.v.dm, nullptr, nullptr);
     bool ok = mv_plan_finish(p);
-    mv_plan_init(p, (uint32_t)qd, dummy);
+    mv_plan_init(p, (uint32_t)qd, none);
     mv_plan_add(p, L.o.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
-    mv_plan_init(p, (uint32_t)E, dummy);
-    mv_plan_norm(p, dummy, 0.0f);
-    mv_plan_add_pair(p, L.gate.dm, L.up.dm, nullptr);
+    mv_plan_init(p, (uint32_t)E, none);
+    mv_plan_add_pair(p, L.gate.dm, L.up.dm, none, nullptr);
     ok = ok && mv_plan_finish(p);
-    mv_plan_init(p, (uint32_t)F, dummy);
+    mv_plan_init(p, (uint32_t)F, none);
     mv_plan_add(p, L.down.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
-    if (!ok) return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": matrix shapes exceed the matvec LDS budget");
+    if (!ok) return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": matrix shapes or types are not supported by the matvec");
+  }
+  {
+    const DevTensor& ow = m->output.set ? m->output : m->token_embd;
+    MvPlan p;
+    mv_plan_init(p, (uint32_t)E, Q8Mut{});
+    mv_plan_add(p, ow.dm, nullptr, nullptr);
+    if (!mv_plan_finish(p)) return fail(RLH_EUNSUP, "logits matrix shape or type is not supported by the matvec");
   }
   // RoPE table with the host libm, as the reference computes it:
   // inv_freq = theta^(-2i/hd) (model.rs:221-227), angle = pos * inv_freq,
@@ -638,7 +644,7 @@ static void cache_free(rlh_cache* c) {
   void* ptrs[] = {c->kc, c->vc, c->scores, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
                   c->act_e.qs, c->act_e.d, c->act_e.s, c->act_e.s16, c->act_q.qs, c->act_q.d, c->act_q.s,
                   c->act_q.s16, c->act_f.qs, c->act_f.d, c->act_f.s, c->act_f.s16, c->st_dev, c->hist, c->pv,
-                  c->pi, c->dbg, c->am_counter};
+                  c->pi, c->dbg};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   if (c->host_st) (void)hipHostFree(c->host_st);
@@ -685,7 +691,6 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
             hipMalloc((void**)&c->hist, (max_ctx + 2) * 4) == hipSuccess &&
             hipMalloc((void**)&c->pv, (size_t)npv * 4) == hipSuccess &&
             hipMalloc((void**)&c->pi, (size_t)npv * 4) == hipSuccess &&
-            hipMalloc((void**)&c->am_counter, 64) == hipSuccess &&
             hipHostMalloc((void**)&c->host_st, 64) == hipSuccess;
   if (!ok) {
     cache_free(c);
@@ -699,7 +704,7 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
     return rc;
   }
   if (hipMemset(c->st_dev, 0, 64) != hipSuccess || hipMemset(c->kc, 0, kvbytes) != hipSuccess ||
-      hipMemset(c->vc, 0, kvbytes) != hipSuccess || hipMemset(c->am_counter, 0, 64) != hipSuccess || hipMemset(c->scratch, 0, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) != hipSuccess ||
+      hipMemset(c->vc, 0, kvbytes) != hipSuccess || hipMemset(c->scratch, 0, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) != hipSuccess ||
       hipMemset(c->act_e.qs, 0, E) != hipSuccess || hipMemset(c->act_e.d, 0, E / 32 * 4) != hipSuccess ||
       hipMemset(c->act_e.s, 0, E / 32 * 4) != hipSuccess || hipMemset(c->act_e.s16, 0, E / 16 * 4) != hipSuccess) {
     cache_free(c);
@@ -914,19 +919,24 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
   int rc = op_upload(t, ty, w, rows, cols);
   if (rc) return rc;
   hipStream_t st = op_stream();
-  DevBuf<float> dx, dy;
-  if (dx.alloc(cols) || dy.alloc(rows)) {
+  DevBuf<float> dx, dy, dd;
+  DevBuf<int8_t> dq;
+  DevBuf<int32_t> ds, ds16;
+  if (dx.alloc(cols) || dy.alloc(rows) || dq.alloc(cols) || dd.alloc(cols / 32) || ds.alloc(cols / 32) ||
+      ds16.alloc(cols / 16)) {
     free_tensor(t);
     return fail(RLH_ENOMEM, "hipMalloc");
   }
-  hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
+  const Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
   MvPlan p;
-  mv_plan_init(p, (uint32_t)cols, dx.p);
+  mv_plan_init(p, (uint32_t)cols, act);
   mv_plan_add(p, t.dm, dy.p, nullptr);
   if (!mv_plan_finish(p)) {
     free_tensor(t);
     return fail(RLH_EUNSUP, "row length " + std::to_string(cols) + " exceeds the matvec LDS budget");
   }
+  hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
+  launch_quantize_q8(st, dx.p, (uint32_t)cols, act);  // quantize_q8 once (ops.rs:104)
   mv_launch(st, p);
   if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(y, dy.p, rows * 4, hipMemcpyDeviceToHost, st);
@@ -1006,9 +1016,10 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   uint64_t cols = mats[0]->cols;
   if (cols != m->cfg.n_embd && cols != m->cfg.n_ff && cols != qd)
     return fail(RLH_EINVAL, "matrix width matches no activation buffer");
+  const Q8Buf& act = cols == m->cfg.n_ff ? c->act_f : (cols == qd ? c->act_q : c->act_e);
   std::vector<MvPlan> plans(mats.size());
   for (size_t i = 0; i < mats.size(); i++) {
-    mv_plan_init(plans[i], (uint32_t)cols, c->scratch);
+    mv_plan_init(plans[i], (uint32_t)cols, act);
     mv_plan_add(plans[i], mats[i]->dm, c->logits, nullptr);
     if (!mv_plan_finish(plans[i])) return fail(RLH_EUNSUP, "matvec shape");
   }

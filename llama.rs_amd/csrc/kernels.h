@@ -28,6 +28,10 @@ void launch_attention(hipStream_t st, const float* q, const float* kcache, const
                       int H, int KVH, uint32_t n_tok, uint32_t t_max, float scale, float* out, const Q8Buf& out_q8);
 void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
                       float* h_out);
+// Final reduction of per-block (max, lowest index) candidates; with `step`
+// set it also advances the greedy loop state (pos += 1, hist[++step] = tok).
+void launch_argmax_final(hipStream_t st, const float* pv, const uint32_t* pi, uint32_t nparts, uint32_t* tok_out,
+                         uint32_t* pos, uint32_t* step, uint32_t* hist);
 void launch_argmax(hipStream_t st, const float* x, uint32_t n, float* pv, uint32_t* pi, uint32_t nparts,
                    uint32_t* tok_out, uint32_t* pos, uint32_t* step, uint32_t* hist);
 // Raises the dynamic-LDS limit of the attention kernel (returns false on error).

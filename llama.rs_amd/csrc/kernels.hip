@@ -355,33 +355,46 @@ __global__ void __launch_bounds__(256) k_argmax_partial(const float* x, uint32_t
 }
 
 // step: when non-null, greedy-loop state: tok_out <- argmax, pos += 1,
-// hist[++step] <- argmax.
-__global__ void __launch_bounds__(256) k_argmax_final(const float* pv, const uint32_t* pi, uint32_t np,
-                                                      uint32_t* tok_out, uint32_t* pos, uint32_t* step,
-                                                      uint32_t* hist) {
-  __shared__ float sv[256];
-  __shared__ uint32_t si[256];
+// hist[++step] <- argmax. 1024 threads; every thread first issues the loads
+// of its partials (up to 16 in flight), then merges them.
+__global__ void __launch_bounds__(1024) k_argmax_final(const float* pv, const uint32_t* pi, uint32_t np,
+                                                       uint32_t* tok_out, uint32_t* pos, uint32_t* step,
+                                                       uint32_t* hist) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
   float bv = -__int_as_float(0x7f800000);
   uint32_t bi = 0xffffffffu;
-  for (uint32_t i = threadIdx.x; i < np; i += 256) argmax_merge(bv, bi, pv[i], pi[i]);
-  sv[threadIdx.x] = bv;
-  si[threadIdx.x] = bi;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if ((int)threadIdx.x < st) {
-      float b = sv[threadIdx.x];
-      uint32_t j = si[threadIdx.x];
-      argmax_merge(b, j, sv[threadIdx.x + st], si[threadIdx.x + st]);
-      sv[threadIdx.x] = b;
-      si[threadIdx.x] = j;
+  for (uint32_t i0 = threadIdx.x; i0 < np; i0 += 1024 * 16) {
+    float v[16];
+    uint32_t ix[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const uint32_t i = i0 + 1024u * k;
+      v[k] = i < np ? pv[i] : -__int_as_float(0x7f800000);
+      ix[k] = i < np ? pi[i] : 0xffffffffu;
     }
-    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) argmax_merge(bv, bi, v[k], ix[k]);
   }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m);
+    const uint32_t oi = __shfl_xor(bi, m);
+    argmax_merge(bv, bi, ov, oi);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = bv;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t best = si[0] == 0xffffffffu ? 0u : si[0];  // all NaN -> 0, as main.rs argmax
+    float b = sv[0];
+    uint32_t j = si[0];
+    for (int k = 1; k < 16; k++) argmax_merge(b, j, sv[k], si[k]);
+    const uint32_t best = j == 0xffffffffu ? 0u : j;  // all NaN -> 0, as main.rs argmax
     tok_out[0] = best;
     if (step) {
-      uint32_t s = step[0] + 1;
+      const uint32_t s = step[0] + 1;
       hist[s] = best;
       step[0] = s;
       pos[0] = pos[0] + 1;
@@ -442,10 +455,15 @@ void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n
   hipLaunchKernelGGL(k_swiglu_q8, dim3((n_total + 255) / 256), dim3(256), 0, st, g, u, n_total, q8out(out), h_out);
 }
 
+void launch_argmax_final(hipStream_t st, const float* pv, const uint32_t* pi, uint32_t nparts, uint32_t* tok_out,
+                         uint32_t* pos, uint32_t* step, uint32_t* hist) {
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, pv, pi, nparts, tok_out, pos, step, hist);
+}
+
 void launch_argmax(hipStream_t st, const float* x, uint32_t n, float* pv, uint32_t* pi, uint32_t nparts,
                    uint32_t* tok_out, uint32_t* pos, uint32_t* step, uint32_t* hist) {
   hipLaunchKernelGGL(k_argmax_partial, dim3(nparts), dim3(256), 0, st, x, n, pv, pi);
-  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, st, pv, pi, nparts, tok_out, pos, step, hist);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(1024), 0, st, pv, pi, nparts, tok_out, pos, step, hist);
 }
 
 }  // namespace rlh

@@ -7,29 +7,31 @@
 
 namespace rlh {
 
+struct Q8Ptr {
+  const int8_t* qs;
+  const float* d;
+  const int32_t* s;
+  const int32_t* s16;
+};
+
 // One matrix (or a gate/up pair) of a launch. Every segment of a launch
-// multiplies the same activation row (cols wide).
+// multiplies the same Q8 activation row (cols wide).
 struct MvSeg {
   DevMat w;            // rows summed into y / resid (gate in PAIR mode)
   DevMat w2;           // PAIR mode: up
-  float* y;            // single: y[r] = total (nullable); PAIR: h[r] = silu(g)*u
+  float* y;            // single: y[r] = total (nullable); PAIR: h[r] = silu(g)*u (nullable)
   float* resid;        // single: resid[r] = resid[r] + total (nullable)
+  Q8Mut hq;            // PAIR: Q8 blocks of h (the next matvec's activation)
   uint32_t blk_begin;  // first block of this segment
   uint32_t pair;
 };
 
-// Greedy argmax fused into the logits launch (main.rs:453-463 semantics):
-// every block leaves its (max, lowest index) in pv/pi[block]; the last
-// block to finish reduces them, writes *tok and, when `step` is set,
-// advances the greedy loop state (pos += 1, hist[++step] = token).
+// Greedy argmax candidates of the logits launch: every block leaves its
+// (max, lowest index) in pv/pi[block]; launch_argmax_final reduces them
+// (main.rs:453-463 semantics).
 struct MvArgmax {
   float* pv;
   uint32_t* pi;
-  uint32_t* counter;  // zero between launches (the last block resets it)
-  uint32_t* tok;
-  uint32_t* pos;
-  uint32_t* step;
-  uint32_t* hist;
 };
 
 struct MvLaunch {
@@ -37,10 +39,8 @@ struct MvLaunch {
   uint32_t nseg;
   uint32_t cols;
   uint32_t rows_per_blk;  // R: rows of one block (all segments)
-  const float* x;         // f32 activation row; the block quantises it to Q8
-  const float* nw;        // rmsnorm weights: when set, the block first computes
-  float eps;              //   rmsnorm(x) * nw (simd.rs:282-326)
-  uint32_t region_off;    // byte offset of the staging / term-tile region in LDS
+  Q8Ptr act;              // Q8 activation row in HBM, staged into LDS by each block
+  uint32_t region_off;    // byte offset of the term tiles in LDS
   uint32_t tile_stride;   // floats per term-tile row
   uint32_t has_argmax;
   MvArgmax am;
@@ -63,14 +63,13 @@ __host__ __device__ inline uint32_t mv_terms_per_sb(uint32_t ty) {
   return ty == RLH_TYPE_Q6_K ? 16u : (ty == RLH_TYPE_Q4_K ? 4u : 8u);
 }
 
-// Plan construction: x is the f32 activation (cols values, cols a multiple
-// of 256); mv_plan_norm adds the rmsnorm prologue. Every segment must have
-// `cols` columns; PAIR plans hold exactly one segment. mv_plan_finish fixes
-// the block shape (returns false when no shape fits the LDS).
-void mv_plan_init(MvPlan& p, uint32_t cols, const float* x);
-void mv_plan_norm(MvPlan& p, const float* w, float eps);
+// Plan construction: act is the Q8 activation row (cols values, cols a
+// multiple of 256). Every segment must have `cols` columns; PAIR plans hold
+// exactly one segment. mv_plan_finish fixes the block shape (returns false
+// when no shape fits the LDS).
+void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act);
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
-void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, float* h);
+void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h);
 void mv_plan_argmax(MvPlan& p, const MvArgmax& am);
 bool mv_plan_finish(MvPlan& p);
 void mv_launch(hipStream_t st, const MvPlan& p);

@@ -13,19 +13,17 @@
 //    loads it with 16-byte loads that are contiguous across the wave, so
 //    every load instruction reads 1 KB of HBM while the scale unpacking and
 //    address arithmetic are paid once per 256 weights.
-//  * The activation enters as f32. The block quantises it to Q8 blocks in LDS
-//    (quantize_q8, simd.rs:116-203), optionally after rmsnorm with the layer's
-//    norm weights (simd.rs:282-326), which removes the separate normalisation
-//    launch. x and the norm weights reach LDS with global_load_lds while the
-//    first weights are already in flight. Q8 super-blocks are stored with a
-//    16-byte pad so that lanes on different super-blocks hit different banks.
+//  * The activation is a Q8 row in HBM (Q8Row, simd.rs:88-101), staged into
+//    LDS with global_load_lds while the first weights are already in flight.
+//    Q8 super-blocks are stored in LDS with a 16-byte pad so that lanes on
+//    different super-blocks hit different banks.
 //  * Every item writes its terms into the block's LDS tile [row][term]; after
 //    one barrier, lane r of wave 0 adds row r's terms in order (the
 //    reference's `total +=` chain) and runs the epilogue.
 //  * PAIR mode multiplies the same rows of ffn_gate and ffn_up and writes
-//    h = silu(gate) * up (ops.rs:393-395, model.rs:722-724). Single mode can
-//    add into the residual (model.rs:714-716, 726-728) and fuse the greedy
-//    argmax of the logits.
+//    h = silu(gate) * up (ops.rs:393-395, model.rs:722-724) with its Q8
+//    blocks. Single mode can add into the residual (model.rs:714-716,
+//    726-728) or leave each block's greedy-argmax candidate of the logits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -59,19 +57,6 @@ __device__ __forceinline__ const RLH_LDS int8_t* qblk(const LAct& a, uint32_t b)
 }
 __device__ __forceinline__ u32x4_t lds_u4(const RLH_LDS int8_t* p) { return *(const lu32x4*)p; }
 __device__ __forceinline__ u32x4_t gl_u4(const void* p) { return *(const RLH_GLOBAL u32x4_t*)p; }
-
-// Cross-lane moves inside groups of 8 lanes with DPP (no LDS round trip):
-// lane ^ 1 and lane ^ 2 within a quad, and the mirror 7 - i of the 8-lane
-// half-row, which pairs every lane of one quad with a lane of the other.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
-}
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
 
 __device__ __forceinline__ int dot16(u32x4_t w, u32x4_t a, int acc) {
   acc = sdot4(w.x, a.x, acc);
@@ -272,78 +257,40 @@ __device__ __forceinline__ float chain(const lfloat* t, uint32_t n) {
   return acc;
 }
 
-// Asynchronous copy of n bytes (a multiple of 16) from HBM into LDS with
-// global_load_lds_dwordx4: wave `wave` of `nw` copies 1 KB pieces wave,
-// wave + nw, ...; lanes past the end are masked off. No registers are
-// involved, so the copy overlaps the weight loads already in flight.
-__device__ __forceinline__ void lds_dma(RLH_LDS void* dst, const void* src, uint32_t n, uint32_t wave, uint32_t nw) {
+// Asynchronous copies HBM -> LDS with global_load_lds (no registers
+// involved, so they overlap the weight loads already in flight). lds_dma4:
+// n bytes (a multiple of 4) in 256-byte pieces, wave `wave` of `nw` taking
+// pieces wave, wave + nw, ...; lanes past the end are masked off.
+__device__ __forceinline__ void lds_dma4(RLH_LDS void* dst, const void* src, uint32_t n, uint32_t wave, uint32_t nw) {
   const uint32_t lane = threadIdx.x & 63;
-  for (uint32_t off = wave * 1024; off < n; off += nw * 1024) {
-    if (off + lane * 16 < n)
-      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)src + off + lane * 16),
-                                       (RLH_LDS void*)((RLH_LDS uint8_t*)dst + off), 16, 0, 0);
+  for (uint32_t off = wave * 256; off < n; off += nw * 256) {
+    if (off + lane * 4 < n)
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)src + off + lane * 4),
+                                       (RLH_LDS void*)((RLH_LDS uint8_t*)dst + off), 4, 0, 0);
   }
 }
 
-// Builds the Q8 activation row in LDS from the f32 row x: optionally
-// rmsnorm(x) * w first (rmsnorm_core, simd.rs:282-326: 32 FMA chains, AVX2
-// reduction tree, s = 1/sqrt(ss/n + eps), out = (x*s)*w), then
-// quantize_q8 (simd.rs:116-203). xs and ws (cols floats each) are only used
-// here, so they may alias the term tiles.
-__device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* ws,
-                                                 lfloat* misc) {
-  const uint32_t tid = threadIdx.x, wave = tid >> 6, nw = blockDim.x >> 6, nthreads = blockDim.x;
-  const uint32_t cols = L.cols, nb = cols / 32;
-  lds_dma(xs, L.x, cols * 4, wave, nw);
-  if (L.nw) lds_dma(ws, L.nw, cols * 4, wave, nw);
+// Stages the Q8 activation row (HBM, Q8Row layout) into LDS. The quants go
+// to the padded layout (17 slots of 16 bytes per 256 values, the 17th empty):
+// lane i of a copy fills slot s0 + i, so its source is chosen per slot and
+// the pad slots are simply masked off.
+__device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& la) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const uint32_t cols = L.cols, nsb = cols >> 8, nb = cols >> 5, nslots = nsb * 17;
+  for (uint32_t s0 = wave * 64; s0 < nslots; s0 += nw * 64) {
+    const uint32_t p = s0 + lane, sb = p / 17, ch = p - sb * 17;
+    if (p < nslots && ch < 16)
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.act.qs + sb * 256 + ch * 16),
+                                       (RLH_LDS void*)(la.qs + s0 * 16), 16, 0, 0);
+  }
+  lds_dma4(la.d, L.act.d, nb * 4, wave, nw);
+  lds_dma4(la.s, L.act.s, nb * 4, wave, nw);
+  lds_dma4(la.s16x32, L.act.s16, nb * 8, wave, nw);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and first weights) have landed
   __syncthreads();
-  float s = 1.0f;
-  if (L.nw) {
-    if (tid < 64) {
-      const float ss = rms_sumsq_lds(xs, (int)cols);
-      if (tid == 0) misc[0] = 1.0f / sqrtf(ss / (float)cols + L.eps);  // simd.rs:315
-    }
-    __syncthreads();
-    s = misc[0];
-  }
-  // 8 lanes per 32-value block, 4 values per lane (groups of 8 lanes stay
-  // together through the loop, so the width-8 shuffles see whole groups)
-  for (uint32_t b = tid / 8; b < nb; b += nthreads / 8) {
-    const uint32_t l = tid & 7, i = b * 32 + 4 * l;
-    const f32x4_t xv = *(const lf32x4*)(xs + i);
-    float v0 = xv.x, v1 = xv.y, v2 = xv.z, v3 = xv.w;
-    if (L.nw) {
-      const f32x4_t wv = *(const lf32x4*)(ws + i);
-      v0 = (v0 * s) * wv.x;
-      v1 = (v1 * s) * wv.y;
-      v2 = (v2 * s) * wv.z;
-      v3 = (v3 * s) * wv.w;
-    }
-    // amax over the block (max is order-free), then exact integer sums
-    const float a0 = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-    float a = fmaxf(a0, dpp_f<kDppXor1>(a0));
-    a = fmaxf(a, dpp_f<kDppXor2>(a));
-    a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
-    const float d = a / 127.0f;
-    const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-    const int q0 = cvtps_packs_i8(__builtin_rintf(v0 * inv));
-    const int q1 = cvtps_packs_i8(__builtin_rintf(v1 * inv));
-    const int q2 = cvtps_packs_i8(__builtin_rintf(v2 * inv));
-    const int q3 = cvtps_packs_i8(__builtin_rintf(v3 * inv));
-    int sm = q0 + q1 + q2 + q3;
-    sm = sm + dpp_i<kDppXor1>(sm);
-    sm = sm + dpp_i<kDppXor2>(sm);  // sum of the 16-value half (lanes 0-3 / 4-7)
-    const int tot = sm + dpp_i<kDppHalfMirror>(sm);
-    *(RLH_LDS uint32_t*)(la.qs + (i >> 8) * kSbStride + (i & 255)) =
-        (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
-    if (l == 0) {
-      la.d[b] = d;
-      la.s[b] = tot;
-      la.s16x32[2 * b] = 32.0f * (float)sm;
-    } else if (l == 4) {
-      la.s16x32[2 * b + 1] = 32.0f * (float)sm;
-    }
+  for (uint32_t i = tid; i < 2 * nb; i += blockDim.x) {
+    const int v = ((RLH_LDS int32_t*)la.s16x32)[i];
+    la.s16x32[i] = 32.0f * (float)v;
   }
   __syncthreads();
 }
@@ -386,7 +333,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   la.s16x32 = (RLH_LDS float*)(la.s + nb);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
 
-  // first tile: its weights are in flight while the activation is built
+  // first tile: its weights are in flight while the activation is staged
   typename I::W wr[NM];
   uint32_t t = wave;
   if (t < ntiles) {
@@ -394,7 +341,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     I::load(wr[0], g.w.a + off, lane);
     if (NM == 2) I::load(wr[NM - 1], g.w2.a + off, lane);
   }
-  stage_activation(L, la, region, region + cols, misc);
+  stage_activation(L, la);
   while (t < ntiles) {
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
     I::terms(wr[0], la, j, region + rl * stride + j * I::kT);
@@ -412,20 +359,23 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   // the valid rows chain a copy of row 0 so that the wave stays converged
   float acc = 0.0f;
   if (wave < (uint32_t)NM) acc = chain(region + (wave * R + (lane < nrows ? lane : 0)) * stride, nsb * I::kT);
+
   if (NM == 2) {
     if (wave == 1) misc[4 + lane] = acc;
     __syncthreads();
-  }
-  if (wave != 0) return;  // wave 0 runs the epilogue
-
-  if (NM == 2) {
+    if (wave != 0) return;
+    // h = silu(gate) * up for the block's rows (R is a multiple of 32 and
+    // divides the rows, so the lanes form whole Q8 blocks)
+    const float x = acc, up = misc[4 + lane];
+    const float h = (x / (1.0f + expf_glibc(-x))) * up;  // ops.rs:393-395
     if (lane < nrows) {
-      const float x = acc, up = misc[4 + lane];
-      ((RLH_GLOBAL float*)g.y)[row0 + lane] = (x / (1.0f + expf_glibc(-x))) * up;  // silu(g) * u
+      if (g.y) ((RLH_GLOBAL float*)g.y)[row0 + lane] = h;
+      q8_quant_block32(h, g.hq, (row0 + lane) / 32);
     }
     return;
   }
-  const bool mine = lane < nrows;
+
+  const bool mine = wave == 0 && lane < nrows;
   const uint32_t row = row0 + lane;
   if (mine) {
     if (g.resid) {
@@ -434,37 +384,15 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     }
     if (g.y) ((RLH_GLOBAL float*)g.y)[row] = acc;
   }
-  if (!L.has_argmax) return;
+  if (wave != 0 || !L.has_argmax) return;
+  // the block's greedy candidate (max, lowest index); a second launch
+  // reduces the candidates of all blocks (main.rs:453-463 semantics)
   float bv = mine ? acc : -__int_as_float(0x7f800000);
   uint32_t bi = mine ? row : 0xffffffffu;
   wave_argmax(bv, bi);
-  uint32_t last = 0;
   if (lane == 0) {
     ((RLH_GLOBAL float*)L.am.pv)[blockIdx.x] = bv;
     ((RLH_GLOBAL uint32_t*)L.am.pi)[blockIdx.x] = bi;
-    __threadfence();
-    last = atomicAdd(L.am.counter, 1u) == gridDim.x - 1 ? 1u : 0u;
-  }
-  last = __shfl(last, 0);
-  if (!last) return;
-  // the last block to finish reduces every block's candidate
-  __threadfence();
-  float b2 = -__int_as_float(0x7f800000);
-  uint32_t j2 = 0xffffffffu;
-  for (uint32_t k = lane; k < gridDim.x; k += 64)
-    argmax_merge(b2, j2, __hip_atomic_load(L.am.pv + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                 __hip_atomic_load(L.am.pi + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  wave_argmax(b2, j2);
-  if (lane == 0) {
-    const uint32_t best = j2 == 0xffffffffu ? 0u : j2;  // all NaN -> 0 (main.rs:453-463)
-    L.am.tok[0] = best;
-    if (L.am.step) {
-      const uint32_t s = L.am.step[0] + 1;
-      L.am.hist[s] = best;
-      L.am.step[0] = s;
-      L.am.pos[0] = L.am.pos[0] + 1;
-    }
-    atomicExch(L.am.counter, 0u);
   }
 }
 
@@ -491,14 +419,14 @@ __global__ void __launch_bounds__(MAXT) k_mv(MvLaunch L) {
 
 constexpr uint32_t kMaxLds = 150u * 1024u;
 
-// LDS bytes of a plan with R rows per block.
+// LDS bytes of a plan with R rows per block: the padded Q8 activation row,
+// then the term tiles.
 uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   const uint32_t cols = p.L.cols, nsb = cols / 256, nb = cols / 32;
   const uint32_t act = (nsb * kSbStride + nb * 16 + 15) & ~15u;
   const uint32_t stride = nsb * p.max_terms + 4;
   const uint32_t tile = nm * R * stride * 4;
-  const uint32_t staging = (p.L.nw ? 2u : 1u) * cols * 4;
-  return act + std::max(tile, staging);
+  return act + tile;
 }
 
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
@@ -509,15 +437,10 @@ uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
 
 }  // namespace
 
-void mv_plan_init(MvPlan& p, uint32_t cols, const float* x) {
+void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act) {
   p = MvPlan{};
   p.L.cols = cols;
-  p.L.x = x;
-}
-
-void mv_plan_norm(MvPlan& p, const float* w, float eps) {
-  p.L.nw = w;
-  p.L.eps = eps;
+  p.L.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
 }
 
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
@@ -530,12 +453,13 @@ void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
   p.max_terms = std::max(p.max_terms, mv_terms_per_sb(w.ty));
 }
 
-void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, float* h) {
+void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h) {
   MvSeg& g = p.L.seg[p.L.nseg++];
   g = MvSeg{};
   g.w = gate;
   g.w2 = up;
   g.y = h;
+  g.hq = hq;
   g.pair = 1;
   p.rows += gate.rows;
   p.max_terms = std::max(p.max_terms, std::max(mv_terms_per_sb(gate.ty), mv_terms_per_sb(up.ty)));
@@ -546,32 +470,28 @@ void mv_plan_argmax(MvPlan& p, const MvArgmax& am) {
   p.L.am = am;
 }
 
-// Block shape: R rows = whole row-tiles, at most 64; the largest R that
-// gives at least one block per CU (256) and fits the LDS, else the smallest
-// that fits. One wave per tile of the block (at most 16 waves).
+// Block shape: R rows = whole row-tiles. Small blocks spread the rows over
+// every CU with high occupancy (R = one row-tile); a PAIR launch needs R to
+// be a multiple of 32 (its epilogue emits whole Q8 blocks of h). One wave
+// per tile of the block, at most 16.
 bool mv_plan_finish(MvPlan& p) {
   const uint32_t nm = (p.L.nseg == 1 && p.L.seg[0].pair) ? 2u : 1u;
   const uint32_t nsb = p.L.cols / 256;
   if (p.L.nseg == 0 || nsb == 0) return false;
   const uint32_t tr = p.L.seg[0].w.tr, ntj = p.L.seg[0].w.ntj;
   for (uint32_t s = 0; s < p.L.nseg; s++)
-    if (p.L.seg[s].w.tr != tr || p.L.seg[s].w.cols != p.L.cols) return false;
-  if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows)) return false;
-  uint32_t best = 0;
-  for (uint32_t R = 64; R >= tr; R /= 2) {
-    if (plan_lds(p, R, nm) > kMaxLds) continue;
-    best = R;
-    if (plan_blocks(p, R) >= 256) break;
-  }
-  if (!best) return false;
-  const uint32_t R = best;
+    if (p.L.seg[s].w.tr != tr || p.L.seg[s].w.cols != p.L.cols || !is_tiled(p.L.seg[s].w.ty)) return false;
+  if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows ||
+                  p.L.seg[0].w.rows % 32 != 0))
+    return false;
+  const uint32_t R = nm == 2 ? std::max<uint32_t>(tr, 32) : tr;
+  if (plan_lds(p, R, nm) > kMaxLds) return false;
   p.L.rows_per_blk = R;
   p.L.tile_stride = nsb * p.max_terms + 4;
   const uint32_t act = nsb * kSbStride + (p.L.cols / 32) * 16;
   p.L.region_off = (act + 15) & ~15u;
   p.lds = plan_lds(p, R, nm);
-  p.waves = std::min<uint32_t>(16, (R / tr) * ntj);
-  if (p.waves < nm) p.waves = nm;
+  p.waves = std::max<uint32_t>(nm, std::min<uint32_t>(16, (R / tr) * ntj));
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;
@@ -582,7 +502,7 @@ bool mv_plan_finish(MvPlan& p) {
 
 uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
   MvPlan p;
-  mv_plan_init(p, cols, nullptr);
+  mv_plan_init(p, cols, Q8Mut{});
   DevMat w{};
   w.ty = ty;
   w.rows = rows;
@@ -592,7 +512,6 @@ uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
   w.tr = 64 / w.tj;
   w.ntj = cols / 256 / w.tj;
   mv_plan_add(p, w, nullptr, nullptr);
-  p.L.nw = (const float*)&p;  // the logits plan has the norm prologue (only its LDS size matters here)
   if (!mv_plan_finish(p)) return 0;
   return p.blocks;
 }

@@ -81,12 +81,15 @@ __device__ __forceinline__ float expf_glibc(float x) {
 // Every lane returns the result.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float avx2_tree32(float a) {
-  float b = a + __shfl_down(a, 8);
-  float A = b + __shfl_down(b, 16);
-  float s = A + __shfl_down(A, 4);
-  float t = s + __shfl_down(s, 2);
-  float r = t + __shfl_down(t, 1);
-  return __shfl(r, 0);
+  // the partner lanes read below (l + 8, l + 16, l + 4, l + 2, l + 1 for the
+  // lanes whose sums are used) stay inside the groups the DPP row shift and
+  // the 32-lane swizzle address, so the operands match the shuffle-down tree
+  const float b = a + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x108, 0xf, 0xf, false));
+  const float A = b + __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(b), 0x401F));  // lane ^ 16
+  const float s = A + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(A), 0x104, 0xf, 0xf, false));
+  const float t = s + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x102, 0xf, 0xf, false));
+  const float r = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x101, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
 }
 
 // Sum of squares of rmsnorm_core (simd.rs:285-313) for one wave: lanes 0..31
@@ -144,15 +147,30 @@ __device__ __forceinline__ void q8_quant_block32(float v, Q8Out o, uint32_t blk)
   }
 }
 
+// Cross-lane moves inside groups of 8 lanes with DPP (no LDS round trip):
+// lane ^ 1 and lane ^ 2 within a quad, and the mirror 7 - i of the 8-lane
+// half-row, which pairs every lane of one quad with a lane of the other.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
+
 // quantize_q8 of one 32-value block held as 4 consecutive values per lane in
-// 8 consecutive lanes (lane & 7 = which 4 values). Same arithmetic as
-// q8_quant_block32; stores 4 packed bytes per lane.
+// 8 consecutive lanes (lane & 7 = which 4 values; the group starts at a lane
+// multiple of 8 and all 8 lanes are active). Same arithmetic as
+// q8_quant_block32; amax is order-free and the sums are exact integers, so
+// the DPP reduction order does not matter. Stores 4 packed bytes per lane.
 __device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, float v3, Q8Out o, uint32_t blk) {
   const int l = threadIdx.x & 7;
-  float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-  a = fmaxf(a, __shfl_xor(a, 1, 8));
-  a = fmaxf(a, __shfl_xor(a, 2, 8));
-  a = fmaxf(a, __shfl_xor(a, 4, 8));
+  const float a0 = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+  float a = fmaxf(a0, dpp_f<kDppXor1>(a0));
+  a = fmaxf(a, dpp_f<kDppXor2>(a));
+  a = fmaxf(a, dpp_f<kDppHalfMirror>(a));
   const float d = a / 127.0f;
   const float inv = d > 0.0f ? 1.0f / d : 0.0f;
   const int q0 = cvtps_packs_i8(__builtin_rintf(v0 * inv));
@@ -160,9 +178,9 @@ __device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, 
   const int q2 = cvtps_packs_i8(__builtin_rintf(v2 * inv));
   const int q3 = cvtps_packs_i8(__builtin_rintf(v3 * inv));
   int s = q0 + q1 + q2 + q3;
-  s = s + __shfl_xor(s, 1, 8);
-  s = s + __shfl_xor(s, 2, 8);  // sum of the 16-value half (lanes 0-3 / 4-7)
-  const int tot = s + __shfl_xor(s, 4, 8);
+  s = s + dpp_i<kDppXor1>(s);
+  s = s + dpp_i<kDppXor2>(s);  // sum of the 16-value half (lanes 0-3 / 4-7)
+  const int tot = s + dpp_i<kDppHalfMirror>(s);
   const uint32_t packed =
       (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
   *(RLH_GLOBAL uint32_t*)(o.qs + (size_t)blk * 32 + 4 * l) = packed;
@@ -186,6 +204,13 @@ __device__ __forceinline__ float rms_sumsq_lds(const RLH_LDS float* x, int n) {
   float acc = 0.0f;
   if (lane < 32) {
     int i = lane;
+    for (; i + 32 * 31 < n32; i += 32 * 32) {  // 32 reads in flight, then the chain
+      float v[32];
+#pragma unroll
+      for (int k = 0; k < 32; k++) v[k] = x[i + 32 * k];
+#pragma unroll
+      for (int k = 0; k < 32; k++) acc = __builtin_fmaf(v[k], v[k], acc);
+    }
     for (; i + 32 * 7 < n32; i += 32 * 8) {
       float v[8];
 #pragma unroll
