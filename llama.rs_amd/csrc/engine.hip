@@ -21,6 +21,7 @@
 #include "kernels.h"
 #include "attention.h"
 #include "matvec.h"
+#include "gemm.h"
 #include "rlh_format.h"
 
 using namespace rlh;
@@ -284,6 +285,15 @@ struct rlh_cache {
   float* dbg = nullptr;  // [L][kDbgTokens][E]
   uint64_t dbg_tokens = 0;
   bool logits_valid = false;
+  // batched prefill workspace (allocated on the first forward_batch): up to
+  // kBatch tokens per chunk, token-major
+  uint32_t bcap = 0;
+  float *xb = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *attnb = nullptr, *gb = nullptr, *ub = nullptr,
+        *scoresb = nullptr;
+  Q8Buf act_eb{}, act_qb{}, act_fb{};
+  uint32_t* tokb = nullptr;   // token ids of the whole call
+  uint32_t* posb = nullptr;   // first position of every chunk
+  uint64_t tokb_cap = 0, posb_cap = 0;
 };
 
 namespace {
@@ -647,6 +657,11 @@ static void cache_free(rlh_cache* c) {
                   c->pi, c->dbg};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
+  void* bptrs[] = {c->xb, c->qb, c->kb, c->vb, c->attnb, c->gb, c->ub, c->scoresb, c->act_eb.qs, c->act_eb.d,
+                   c->act_eb.s, c->act_eb.s16, c->act_qb.qs, c->act_qb.d, c->act_qb.s, c->act_qb.s16, c->act_fb.qs,
+                   c->act_fb.d, c->act_fb.s, c->act_fb.s16, c->tokb, c->posb};
+  for (void* p : bptrs)
+    if (p) (void)hipFree(p);
   if (c->host_st) (void)hipHostFree(c->host_st);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
@@ -773,6 +788,125 @@ int rlh_forward_one(rlh_model* m, rlh_cache* c, uint32_t token, uint64_t pos, fl
   return copy_logits(c, logits);
 }
 
+// Tokens per prefill chunk: the batched workspace holds this many rows.
+static constexpr uint32_t kBatch = 512;
+
+static int ensure_batch(rlh_cache* c) {
+  if (c->bcap) return RLH_OK;
+  const rlh_config& cfg = c->m->cfg;
+  const uint32_t B = (uint32_t)std::min<uint64_t>(kBatch, c->max_ctx);
+  const size_t E = cfg.n_embd, F = cfg.n_ff, qd = (size_t)cfg.n_head * cfg.head_dim,
+               kvd = (size_t)cfg.n_head_kv * cfg.head_dim;
+  bool ok = hipMalloc((void**)&c->xb, B * E * 4) == hipSuccess && hipMalloc((void**)&c->qb, B * qd * 4) == hipSuccess &&
+            hipMalloc((void**)&c->kb, B * kvd * 4) == hipSuccess && hipMalloc((void**)&c->vb, B * kvd * 4) == hipSuccess &&
+            hipMalloc((void**)&c->attnb, B * qd * 4) == hipSuccess && hipMalloc((void**)&c->gb, B * F * 4) == hipSuccess &&
+            hipMalloc((void**)&c->ub, B * F * 4) == hipSuccess &&
+            hipMalloc((void**)&c->scoresb, (size_t)B * cfg.n_head * c->max_ctx * 4) == hipSuccess;
+  if (!ok) return fail(RLH_ENOMEM, "prefill workspace allocation failed");
+  int rc = alloc_q8(c->act_eb, B * E);
+  if (!rc) rc = alloc_q8(c->act_qb, B * qd);
+  if (!rc) rc = alloc_q8(c->act_fb, B * F);
+  if (rc) return rc;
+  c->bcap = B;
+  return RLH_OK;
+}
+
+// Model::forward_batch (model.rs:384-583) with the integer batch products of
+// RUST_LLAMA_BATCH_INT=1: the prompt runs through every layer in chunks of
+// up to kBatch tokens (a chunk's attention reads the K/V rows the earlier
+// chunks wrote, so chunking changes no value). Per layer: rmsnorm + Q8 of
+// every token, q/k/v products, QK-norm + RoPE + K/V write, causal attention
+// (query rows in parallel), attn_output product added to the residual,
+// rmsnorm + Q8, gate/up products, SwiGLU + Q8, ffn_down product added to the
+// residual. Logits for the last token only (model.rs:578-582).
+static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos) {
+  int rc = ensure_batch(c);
+  if (rc) return rc;
+  const rlh_config& cfg = m->cfg;
+  hipStream_t st = c->st;
+  const uint32_t E = cfg.n_embd, H = cfg.n_head, KVH = cfg.n_head_kv, hd = cfg.head_dim;
+  const float eps = cfg.rms_eps, scale = 1.0f / std::sqrt((float)hd);
+  const uint32_t B = c->bcap;
+  const uint64_t nchunks = (n + B - 1) / B;
+  HIPCHK(hipStreamSynchronize(st));
+  if (n > c->tokb_cap) {
+    if (c->tokb) (void)hipFree(c->tokb);
+    c->tokb = nullptr;
+    if (hipMalloc((void**)&c->tokb, n * 4) != hipSuccess) return fail(RLH_ENOMEM, "hipMalloc prompt ids");
+    c->tokb_cap = n;
+  }
+  if (nchunks > c->posb_cap) {
+    if (c->posb) (void)hipFree(c->posb);
+    c->posb = nullptr;
+    if (hipMalloc((void**)&c->posb, nchunks * 4) != hipSuccess) return fail(RLH_ENOMEM, "hipMalloc chunk positions");
+    c->posb_cap = nchunks;
+  }
+  std::vector<uint32_t> p0s(nchunks);
+  for (uint64_t i = 0; i < nchunks; i++) p0s[i] = (uint32_t)(start_pos + i * B);
+  HIPCHK(hipMemcpy(c->tokb, tokens, n * 4, hipMemcpyHostToDevice));
+  HIPCHK(hipMemcpy(c->posb, p0s.data(), nchunks * 4, hipMemcpyHostToDevice));
+  uint32_t last_m = 0;
+  for (uint64_t ci = 0; ci < nchunks; ci++) {
+    const uint64_t c0 = ci * B;
+    const uint32_t mtok = (uint32_t)std::min<uint64_t>(B, n - c0);
+    const uint32_t p0 = p0s[ci];
+    const uint32_t* pos = c->posb + ci;
+    last_m = mtok;
+    launch_embed(st, m->token_embd.dm, c->tokb + c0, mtok, c->xb);
+    for (uint32_t l = 0; l < cfg.n_layer; l++) {
+      Layer& L = m->layers[l];
+      launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, nullptr);
+      launch_gemm(st, L.q.dm, c->act_eb, mtok, c->qb, nullptr);
+      launch_gemm(st, L.k.dm, c->act_eb, mtok, c->kb, nullptr);
+      launch_gemm(st, L.v.dm, c->act_eb, mtok, c->vb, nullptr);
+      launch_qk_norm_rope_kv(st, c->qb, c->kb, c->vb, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
+                             cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
+                             (int)H, (int)KVH, mtok, eps);
+      AttnArgs a{};
+      a.q = c->qb;
+      a.rope_cs = m->rope_cs;
+      a.pos0 = pos;
+      a.kcache = layer_k(c, l);
+      a.vcache = layer_v(c, l);
+      a.scores = c->scoresb;
+      a.t_stride = (uint32_t)c->max_ctx;
+      a.t_max = p0 + mtok;
+      a.vtile = c->vtile;
+      a.H = (int)H;
+      a.KVH = (int)KVH;
+      a.eps = eps;
+      a.scale = scale;
+      a.out = c->attnb;
+      a.out_q8 = c->act_qb;
+      launch_attn_scores(st, a, mtok, false);
+      launch_attn_out(st, a, mtok);
+      launch_gemm(st, L.o.dm, c->act_qb, mtok, nullptr, c->xb);
+      launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, nullptr);
+      launch_gemm(st, L.gate.dm, c->act_eb, mtok, c->gb, nullptr);
+      launch_gemm(st, L.up.dm, c->act_eb, mtok, c->ub, nullptr);
+      launch_swiglu_q8(st, c->gb, c->ub, mtok * cfg.n_ff, c->act_fb, nullptr);
+      launch_gemm(st, L.down.dm, c->act_fb, mtok, nullptr, c->xb);
+      if (c->debug && c->dbg && c0 < c->dbg_tokens) {
+        const uint64_t nd = std::min<uint64_t>(mtok, c->dbg_tokens - c0);
+        HIPCHK(hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + c0) * E, c->xb, nd * E * 4,
+                              hipMemcpyDeviceToDevice, st));
+      }
+    }
+    HIPCHK(hipGetLastError());
+  }
+  // logits of the last token: rmsnorm(x, output_norm), then the decode matvec
+  HIPCHK(hipMemcpyAsync(c->x, c->xb + (size_t)(last_m - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, st));
+  launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
+  const DevTensor& ow = m->output.set ? m->output : m->token_embd;
+  MvPlan p;
+  mv_plan_init(p, E, c->act_e);
+  mv_plan_add(p, ow.dm, c->logits, nullptr);
+  mv_plan_finish(p);
+  mv_launch(st, p);
+  HIPCHK(hipGetLastError());
+  return RLH_OK;
+}
+
 int rlh_forward_batch(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
                       float* logits) {
   int rc = check_forward_args(m, c);
@@ -782,10 +916,7 @@ int rlh_forward_batch(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64
   if (n == 0) return RLH_OK;
   for (uint64_t i = 0; i < n; i++)
     if (tokens[i] >= m->cfg.vocab_size) return fail(RLH_EINVAL, "token id out of range");
-  for (uint64_t i = 0; i < n; i++) {
-    if ((rc = set_tok_pos(c, tokens[i], (uint32_t)(start_pos + i)))) return rc;
-    if ((rc = run_step(c, i + 1 == n ? STEP_LOGITS : STEP_NOLOGITS, (int64_t)i))) return rc;
-  }
+  if ((rc = forward_batch_impl(m, c, tokens, n, start_pos))) return rc;
   c->len = start_pos + n;
   c->logits_valid = true;
   return copy_logits(c, logits);
@@ -949,10 +1080,34 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
 int rlh_matmul_batch(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const float* xs, uint64_t n,
                      float* ys) {
   if (!xs || !ys) return fail(RLH_EINVAL, "null argument");
-  for (uint64_t k = 0; k < n; k++) {
-    int rc = rlh_matvec(ty, w, rows, cols, xs + k * cols, ys + k * rows);
-    if (rc) return rc;
+  if (n == 0) return RLH_OK;
+  if (n == 1) return rlh_matvec(ty, w, rows, cols, xs, ys);  // ops.rs:158-161
+  if (!gemm_supported(ty)) return fail(RLH_EUNSUP, "no batched kernel for ggml type " + std::to_string(ty));
+  if (cols == 0 || cols % 256) return fail(RLH_EINVAL, "cols must be a positive multiple of 256");
+  if (rows == 0 || rows > 0xffffffffull || n > 0xffffffffull / cols) return fail(RLH_EINVAL, "shape out of range");
+  DevTensor t;
+  int rc = op_upload(t, ty, w, rows, cols);
+  if (rc) return rc;
+  hipStream_t st = op_stream();
+  const uint64_t nv = n * cols;
+  DevBuf<float> dx, dy, dd;
+  DevBuf<int8_t> dq;
+  DevBuf<int32_t> ds, ds16;
+  if (dx.alloc(nv) || dy.alloc(n * rows) || dq.alloc(nv) || dd.alloc(nv / 32) || ds.alloc(nv / 32) ||
+      ds16.alloc(nv / 16)) {
+    free_tensor(t);
+    return fail(RLH_ENOMEM, "hipMalloc");
   }
+  // quantize_q8 of every token row (ops.rs:207-209), then the products
+  const Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
+  hipError_t e = hipMemcpyAsync(dx.p, xs, nv * 4, hipMemcpyHostToDevice, st);
+  launch_quantize_q8(st, dx.p, (uint32_t)nv, act);
+  launch_gemm(st, t.dm, act, (uint32_t)n, dy.p, nullptr);
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(ys, dy.p, n * rows * 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  free_tensor(t);
+  if (e != hipSuccess) return fail(RLH_EDEVICE, hipGetErrorString(e));
   return RLH_OK;
 }
 

@@ -1,0 +1,535 @@
+// gemm.hip — batched prefill products on int8 MFMA (ops.rs:150-313 with
+// RUST_LLAMA_BATCH_INT=1: quantize_q8 of every token, then dot_qk_q8_row per
+// (row, token), simd.rs:898-910).
+//
+// Exactness: for every (token, row) the output is the reference's f32 chain
+// `total += term` over the row's terms in index order; each term is formed
+// with the reference's expression (simd.rs:581 Q4_K, 663 Q6_K, 863 Q4_0,
+// 891 Q8_0). The integer block dots inside the terms come from
+// v_mfma_i32_16x16x32_i8 and are exact:
+//   Q4_K  unsigned nibbles (0..15) x Q8 bytes, one MFMA per 32-value block;
+//   Q6_K  q = u - 32 as signed bytes, so the MFMA gives sum(q a) = ss - 32 sa
+//         exactly, which is what (ss as f32 - 32.0 * sa as f32) evaluates to
+//         (both are integers below 2^24); one MFMA per 16-value half, the
+//         other half of the operand zeroed;
+//   Q8_0  signed bytes; Q4_0 nibble - 8, i.e. i0 + i1 - 8 * sum exactly.
+// The per-element float epilogue runs on the VALU and dominates the cost.
+//
+// Tiling: a block owns 64 tokens x 64 rows; 4 waves of 32 x 32, each 2 x 2
+// MFMA tiles of 16 x 16. Per super-block (256 values) the block stages the
+// 64 tokens' Q8 bytes and block scales into LDS with global_load_lds (double
+// buffered); every lane loads the weight bytes of its row straight from the
+// tiled layout, one super-block ahead. Block b runs on XCD b % 8; the blocks
+// of one XCD walk the token tiles of a row tile first, so each weight tile
+// is fetched into that XCD's L2 once and reused by all token tiles.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gemm.h"
+#include "rlh_device.h"
+
+namespace rlh {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef RLH_LDS uint8_t lbyte;
+
+constexpr uint32_t kTile = 64;                          // tokens and rows per block
+constexpr uint32_t kXStride = 272;                      // LDS bytes per token per super-block (16-byte pad)
+constexpr uint32_t kXBytes = kTile * kXStride;          // 17408
+constexpr uint32_t kDBytes = kTile * 8 * 4;             // da of 8 blocks per token
+constexpr uint32_t kStageBytes = kXBytes + 2 * kDBytes;  // + sums (Q4_K)
+
+__device__ __forceinline__ uint64_t g8(const uint8_t* p) { return *(const RLH_GLOBAL uint64_t*)p; }
+__device__ __forceinline__ u32x4_t g16(const uint8_t* p) { return *(const RLH_GLOBAL u32x4_t*)p; }
+__device__ __forceinline__ long l8(const lbyte* p) { return *(const RLH_LDS long*)p; }
+
+__device__ __forceinline__ v4i mfma(long a, uint64_t b) {
+  const v4i z = {0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, (long)b, z, 0, 0, 0);
+}
+
+// Bytes of item (row, j) in the tiled layout: byte o < 16 * (ib / 16) lies
+// at base + (o / 16) * 1024 + o % 16; the ib % 16 tail bytes at `tail`.
+struct ItemPtr {
+  const uint8_t* base;
+  const uint8_t* tail;
+};
+__device__ __forceinline__ ItemPtr item_ptr(const DevMat& w, uint32_t row, uint32_t j) {
+  const uint32_t rt = row / w.tr, jt = j / w.tj, l = (j % w.tj) * w.tr + row % w.tr;
+  const uint8_t* tb = w.a + ((size_t)rt * w.ntj + jt) * 64 * w.ib;
+  const uint32_t ch = w.ib / 16;
+  return ItemPtr{tb + l * 16, tb + ch * 1024 + l * (w.ib - ch * 16)};
+}
+__device__ __forceinline__ const uint8_t* at(const ItemPtr& p, uint32_t o) { return p.base + (o >> 4) * 1024 + (o & 15); }
+
+// Lane coordinates inside the block: lane = 16 q + i16; wave = 2 rw + tw.
+struct Lane {
+  uint32_t q, i16, tw, rw;
+};
+
+// Token-scale view of a staged super-block.
+struct StageView {
+  const lbyte* xs;      // [64][kXStride] Q8 bytes
+  const RLH_LDS float* d;    // [64][8] block scales
+  const RLH_LDS int32_t* s;  // [64][8] block sums
+};
+
+__device__ __forceinline__ StageView view(const lbyte* buf) {
+  return StageView{buf, (const RLH_LDS float*)(buf + kXBytes), (const RLH_LDS int32_t*)(buf + kXBytes + kDBytes)};
+}
+
+// A operands of block kb (0..7 inside the super-block) for token tile tr.
+__device__ __forceinline__ long a_frag(const StageView& v, const Lane& ln, uint32_t tr, uint32_t kb) {
+  const uint32_t tok = 32 * ln.tw + 16 * tr + ln.i16;
+  return l8(v.xs + tok * kXStride + kb * 32 + 8 * ln.q);
+}
+
+// The per-type loops below are not unrolled (unrolling them makes the
+// compiler keep every iteration's MFMA results and operands live at once);
+// instead of indexing a register array with the loop counter (which would
+// move the array to scratch memory), each iteration uses element 0 and the
+// arrays are rotated by one at its end.
+template <int N>
+__device__ __forceinline__ void rotate(uint64_t (&a)[N]) {
+#pragma unroll
+  for (int i = 0; i + 1 < N; i++) a[i] = a[i + 1];
+}
+
+// ---- per-type weight fragments and term evaluation --------------------------
+template <uint32_t TY>
+struct GT;
+
+// Q4_K: lane k-range 8q..8q+7 of block 2g is the low nibbles of item bytes
+// 16 + 32g + 8q .. +8, of block 2g+1 their high nibbles.
+template <>
+struct GT<RLH_TYPE_Q4_K> {
+  static constexpr bool kNeedS = true;
+  struct W {
+    u32x4_t hdr;
+    uint64_t qs[4];
+  };
+  __device__ __forceinline__ static void load(W& r, const DevMat& w, uint32_t row, uint32_t j, uint32_t q) {
+    const ItemPtr p = item_ptr(w, row, j);
+    r.hdr = g16(at(p, 0));
+#pragma unroll
+    for (int g = 0; g < 4; g++) r.qs[g] = g8(at(p, 16 + 32 * g + 8 * q));
+  }
+  __device__ __forceinline__ static void compute(const W (&w)[2], const StageView& v, const Lane& ln,
+                                                 float (&acc)[2][2][4]) {
+    const uint64_t m4 = 0x0F0F0F0F0F0F0F0Full;
+#pragma unroll 1
+    for (int g = 0; g < 4; g++) {
+      long alo[2], ahi[2];
+#pragma unroll
+      for (int tr = 0; tr < 2; tr++) {
+        alo[tr] = a_frag(v, ln, tr, 2 * g);
+        ahi[tr] = a_frag(v, ln, tr, 2 * g + 1);
+      }
+      float d1[2], mm1[2], d2[2], mm2[2];
+      uint64_t blo[2], bhi[2];
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {
+        const uint64_t qg = g == 0 ? w[tc].qs[0] : (g == 1 ? w[tc].qs[1] : (g == 2 ? w[tc].qs[2] : w[tc].qs[3]));
+        blo[tc] = qg & m4;
+        bhi[tc] = (qg >> 4) & m4;
+        const float d = f16_to_f32(w[tc].hdr.x & 0xffff), dmin = f16_to_f32(w[tc].hdr.x >> 16);
+        const uint32_t s0 = w[tc].hdr.y, s1 = w[tc].hdr.z, s2 = w[tc].hdr.w;
+        const uint32_t sh1 = 16 * (g & 1), sh2 = sh1 + 8;
+        uint32_t sc1, m1, sc2, m2;  // get_scale_min_k4 (quant.rs:176-185), j = 2g, 2g+1
+        if (g < 2) {
+          sc1 = (s0 >> sh1) & 63;
+          m1 = (s1 >> sh1) & 63;
+          sc2 = (s0 >> sh2) & 63;
+          m2 = (s1 >> sh2) & 63;
+        } else {
+          sc1 = ((s2 >> sh1) & 0xF) | (((s0 >> sh1) >> 6 & 3) << 4);
+          m1 = ((s2 >> sh1) >> 4 & 0xF) | (((s1 >> sh1) >> 6 & 3) << 4);
+          sc2 = ((s2 >> sh2) & 0xF) | (((s0 >> sh2) >> 6 & 3) << 4);
+          m2 = ((s2 >> sh2) >> 4 & 0xF) | (((s1 >> sh2) >> 6 & 3) << 4);
+        }
+        d1[tc] = d * (float)sc1;
+        mm1[tc] = dmin * (float)m1;
+        d2[tc] = d * (float)sc2;
+        mm2[tc] = dmin * (float)m2;
+      }
+#pragma unroll
+      for (int tr = 0; tr < 2; tr++) {
+        float da[4], db[4], sa[4], sb[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t tok = 32 * ln.tw + 16 * tr + 4 * ln.q + e;
+          da[e] = v.d[tok * 8 + 2 * g];
+          db[e] = v.d[tok * 8 + 2 * g + 1];
+          sa[e] = (float)v.s[tok * 8 + 2 * g];
+          sb[e] = (float)v.s[tok * 8 + 2 * g + 1];
+        }
+#pragma unroll
+        for (int tc = 0; tc < 2; tc++) {
+          const v4i c1 = mfma(alo[tr], blo[tc]);
+          const v4i c2 = mfma(ahi[tr], bhi[tc]);
+#pragma unroll
+          for (int e = 0; e < 4; e++)  // simd.rs:581
+            acc[tr][tc][e] = acc[tr][tc][e] + (da[e] * (d1[tc] * (float)c1[e] - mm1[tc] * sa[e]) +
+                                               db[e] * (d2[tc] * (float)c2[e] - mm2[tc] * sb[e]));
+        }
+      }
+    }
+  }
+};
+
+// Q6_K: block c of half h covers item bytes ql[64h + 32(c&1) + p] (nibble
+// c >> 1) and qh[128 + 32h + p] (bits 2c, 2c+1), p = position 0..31; the
+// lane's positions 8q..8q+7 all belong to sub-half s = q >> 1.
+template <>
+struct GT<RLH_TYPE_Q6_K> {
+  static constexpr bool kNeedS = false;
+  struct W {
+    uint64_t ql[2][2], qh[2];
+    u32x4_t sc;
+    uint32_t d;
+  };
+  __device__ __forceinline__ static void load(W& r, const DevMat& w, uint32_t row, uint32_t j, uint32_t q) {
+    const ItemPtr p = item_ptr(w, row, j);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      r.ql[h][0] = g8(at(p, 64 * h + 8 * q));
+      r.ql[h][1] = g8(at(p, 64 * h + 32 + 8 * q));
+      r.qh[h] = g8(at(p, 128 + 32 * h + 8 * q));
+    }
+    r.sc = g16(at(p, 192));
+    r.d = ld_g2(p.tail);
+  }
+  __device__ __forceinline__ static void compute(const W (&w)[2], const StageView& v, const Lane& ln,
+                                                 float (&acc)[2][2][4]) {
+    const uint64_t m4 = 0x0F0F0F0F0F0F0F0Full, m2 = 0x0303030303030303ull;
+    const uint64_t hi = 0x8080808080808080ull, k32 = 0x2020202020202020ull;
+    const bool sub1 = ln.q >= 2;
+    uint64_t hq[2][4], hh[2][2];  // per row tile: ql pieces of half 0 then 1, qh of half 0 then 1
+    uint32_t hs[2][4];            // scale words of half 0 then 1
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++) {
+      hq[tc][0] = w[tc].ql[0][0];
+      hq[tc][1] = w[tc].ql[0][1];
+      hq[tc][2] = w[tc].ql[1][0];
+      hq[tc][3] = w[tc].ql[1][1];
+      hh[tc][0] = w[tc].qh[0];
+      hh[tc][1] = w[tc].qh[1];
+      hs[tc][0] = w[tc].sc.x;
+      hs[tc][1] = w[tc].sc.y;
+      hs[tc][2] = w[tc].sc.z;
+      hs[tc][3] = w[tc].sc.w;
+    }
+#pragma unroll 1
+    for (int h = 0; h < 2; h++) {
+      // signed weights q = u - 32 of the half's 4 blocks, per row tile
+      uint64_t bq[2][4];
+      float dsc[2][2][4];
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {
+        const float d = f16_to_f32(w[tc].d);
+        const uint32_t swlo = hs[tc][0], swhi = hs[tc][1];  // the half's 8 scales
+        const uint64_t ql0 = hq[tc][0], ql1 = hq[tc][1], qh = hh[tc][0];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint64_t nib = (((c & 1) ? ql1 : ql0) >> (4 * (c >> 1))) & m4;
+          const uint64_t u = nib | (((qh >> (2 * c)) & m2) << 4);
+          bq[tc][c] = ((u | hi) - k32) ^ hi;
+#pragma unroll
+          for (int s = 0; s < 2; s++) {
+            const uint32_t bi = s + 2 * c;  // scales[sub + 2c] of the half (simd.rs:626-629)
+            dsc[tc][s][c] = d * (float)(int8_t)(((bi < 4 ? swlo : swhi) >> (8 * (bi & 3))) & 0xff);
+          }
+        }
+      }
+      long a[2][4];
+      f32x4_t da[2][4];  // [tr][e] -> da of blocks 4h..4h+3
+#pragma unroll
+      for (int tr = 0; tr < 2; tr++) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) a[tr][c] = a_frag(v, ln, tr, 4 * h + c);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const uint32_t tok = 32 * ln.tw + 16 * tr + 4 * ln.q + e;
+          da[tr][e] = *(const RLH_LDS f32x4_t*)(v.d + tok * 8 + 4 * h);
+        }
+      }
+      // terms in the order s = 0 (c = 0..3), then s = 1 (simd.rs:630-665)
+#pragma unroll
+      for (int s = 0; s < 2; s++) {
+        const bool keep = (s == 1) == sub1;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+          for (int tr = 0; tr < 2; tr++) {
+#pragma unroll
+            for (int tc = 0; tc < 2; tc++) {
+              const v4i ci = mfma(a[tr][c], keep ? bq[tc][c] : 0ull);
+#pragma unroll
+              for (int e = 0; e < 4; e++)  // simd.rs:663
+                acc[tr][tc][e] = acc[tr][tc][e] + dsc[tc][s][c] * (float)ci[e] * da[tr][e][c];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {  // half 1 moves into place
+        hq[tc][0] = hq[tc][2];
+        hq[tc][1] = hq[tc][3];
+        hh[tc][0] = hh[tc][1];
+        hs[tc][0] = hs[tc][2];
+        hs[tc][1] = hs[tc][3];
+      }
+    }
+  }
+};
+
+// Q8_0: item = 8 blocks; lane bytes 32k + 8q .. +8 of block k, then the 8
+// f16 scales at item bytes 256..271.
+template <>
+struct GT<RLH_TYPE_Q8_0> {
+  static constexpr bool kNeedS = false;
+  struct W {
+    uint64_t qs[8];
+    u32x4_t dv;
+  };
+  __device__ __forceinline__ static void load(W& r, const DevMat& w, uint32_t row, uint32_t j, uint32_t q) {
+    const ItemPtr p = item_ptr(w, row, j);
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.qs[k] = g8(at(p, 32 * k + 8 * q));
+    r.dv = g16(at(p, 256));
+  }
+  __device__ __forceinline__ static void compute(const W (&wr)[2], const StageView& v, const Lane& ln,
+                                                 float (&acc)[2][2][4]) {
+    uint64_t qs[2][8];
+    uint32_t dw[2][4];
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) qs[tc][k] = wr[tc].qs[k];
+      dw[tc][0] = wr[tc].dv.x;
+      dw[tc][1] = wr[tc].dv.y;
+      dw[tc][2] = wr[tc].dv.z;
+      dw[tc][3] = wr[tc].dv.w;
+    }
+#pragma unroll 1
+    for (int k = 0; k < 8; k++) {
+      float dk[2];
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) dk[tc] = f16_to_f32((dw[tc][0] >> (16 * (k & 1))) & 0xffff);
+#pragma unroll
+      for (int tr = 0; tr < 2; tr++) {
+        const long a = a_frag(v, ln, tr, k);
+        float da[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) da[e] = v.d[(32 * ln.tw + 16 * tr + 4 * ln.q + e) * 8 + k];
+#pragma unroll
+        for (int tc = 0; tc < 2; tc++) {
+          const v4i ci = mfma(a, qs[tc][0]);
+#pragma unroll
+          for (int e = 0; e < 4; e++)  // simd.rs:891
+            acc[tr][tc][e] = acc[tr][tc][e] + dk[tc] * (float)ci[e] * da[e];
+        }
+      }
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {
+        rotate(qs[tc]);
+        if (k & 1) {  // next pair of f16 scales
+          dw[tc][0] = dw[tc][1];
+          dw[tc][1] = dw[tc][2];
+          dw[tc][2] = dw[tc][3];
+        }
+      }
+    }
+  }
+};
+
+// Q4_0: item = 8 blocks of 16 bytes; positions 0..15 are the low nibbles,
+// 16..31 the high nibbles, so lane q reads bytes 16k + 8(q & 1) .. +8 and
+// takes nibble q >> 1; weights are nibble - 8.
+template <>
+struct GT<RLH_TYPE_Q4_0> {
+  static constexpr bool kNeedS = false;
+  struct W {
+    uint64_t qs[8];
+    u32x4_t dv;
+  };
+  __device__ __forceinline__ static void load(W& r, const DevMat& w, uint32_t row, uint32_t j, uint32_t q) {
+    const ItemPtr p = item_ptr(w, row, j);
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.qs[k] = g8(at(p, 16 * k + 8 * (q & 1)));
+    r.dv = g16(at(p, 128));
+  }
+  __device__ __forceinline__ static void compute(const W (&wr)[2], const StageView& v, const Lane& ln,
+                                                 float (&acc)[2][2][4]) {
+    const uint64_t m4 = 0x0F0F0F0F0F0F0F0Full, hi = 0x8080808080808080ull, k8 = 0x0808080808080808ull;
+    uint64_t qs[2][8];
+    uint32_t dw[2][4];
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++) {
+#pragma unroll
+      for (int k = 0; k < 8; k++) qs[tc][k] = wr[tc].qs[k];
+      dw[tc][0] = wr[tc].dv.x;
+      dw[tc][1] = wr[tc].dv.y;
+      dw[tc][2] = wr[tc].dv.z;
+      dw[tc][3] = wr[tc].dv.w;
+    }
+#pragma unroll 1
+    for (int k = 0; k < 8; k++) {
+      float dk[2];
+      uint64_t b[2];
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {
+        dk[tc] = f16_to_f32((dw[tc][0] >> (16 * (k & 1))) & 0xffff);
+        const uint64_t nib = (qs[tc][0] >> (4 * (ln.q >> 1))) & m4;
+        b[tc] = ((nib | hi) - k8) ^ hi;
+      }
+#pragma unroll
+      for (int tr = 0; tr < 2; tr++) {
+        const long a = a_frag(v, ln, tr, k);
+        float da[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) da[e] = v.d[(32 * ln.tw + 16 * tr + 4 * ln.q + e) * 8 + k];
+#pragma unroll
+        for (int tc = 0; tc < 2; tc++) {
+          const v4i ci = mfma(a, b[tc]);
+#pragma unroll
+          for (int e = 0; e < 4; e++)  // simd.rs:863
+            acc[tr][tc][e] = acc[tr][tc][e] + dk[tc] * (float)ci[e] * da[e];
+        }
+      }
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) {
+        rotate(qs[tc]);
+        if (k & 1) {
+          dw[tc][0] = dw[tc][1];
+          dw[tc][1] = dw[tc][2];
+          dw[tc][2] = dw[tc][3];
+        }
+      }
+    }
+  }
+};
+
+// Stages super-block j of the block's 64 tokens: Q8 bytes into the padded
+// [64][272] layout (17 slots of 16 bytes per token, the 17th masked), the 8
+// block scales and (Q4_K) the 8 block sums per token. One copy instruction
+// fills 64 consecutive 16-byte slots; each lane picks the source of its slot.
+__device__ __forceinline__ void stage(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf, bool need_s) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t cols = a.w.cols, nb = cols / 32;
+  const uint32_t nx = kTile * 17, nd = kTile * 2;
+  const uint32_t total = nx + nd + (need_s ? nd : 0);
+  for (uint32_t s0 = wave * 64; s0 < total; s0 += 4 * 64) {
+    const uint32_t p = s0 + lane;
+    const uint8_t* src = nullptr;
+    if (p < nx) {
+      const uint32_t tok = p / 17, ch = p - tok * 17;
+      if (ch < 16 && t0 + tok < a.n) src = (const uint8_t*)a.x.qs + (size_t)(t0 + tok) * cols + 256 * j + 16 * ch;
+    } else if (p < nx + nd) {
+      const uint32_t r = p - nx, tok = r >> 1;
+      if (t0 + tok < a.n) src = (const uint8_t*)(a.x.d + (size_t)(t0 + tok) * nb + 8 * j + 4 * (r & 1));
+    } else if (p < total) {
+      const uint32_t r = p - nx - nd, tok = r >> 1;
+      if (t0 + tok < a.n) src = (const uint8_t*)(a.x.s + (size_t)(t0 + tok) * nb + 8 * j + 4 * (r & 1));
+    }
+    if (src) __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)src, (RLH_LDS void*)(buf + s0 * 16), 16, 0, 0);
+  }
+}
+
+template <uint32_t TY>
+__global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
+  using G = GT<TY>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_generic[];
+  lbyte* lds = (lbyte*)lds_generic;
+  // XCD-aware tile order (see file header)
+  const uint32_t b = blockIdx.x, xcd = b & 7, k = b >> 3;
+  const uint32_t tt = k % a.n_tt, rt = (k / a.n_tt) * 8 + xcd;
+  if (rt >= a.n_rt) return;  // whole block, before any barrier
+  const uint32_t t0 = tt * kTile, r0 = rt * kTile;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  Lane ln{lane >> 4, lane & 15, wave & 1, wave >> 1};
+  const uint32_t rows = a.w.rows, nsb = a.w.cols >> 8;
+  uint32_t rowc[2];
+#pragma unroll
+  for (int tc = 0; tc < 2; tc++) {
+    const uint32_t r = r0 + 32 * ln.rw + 16 * tc + ln.i16;
+    rowc[tc] = r < rows ? r : rows - 1;  // loads stay inside the matrix
+  }
+  float acc[2][2][4];
+#pragma unroll
+  for (int tr = 0; tr < 2; tr++)
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc[tr][tc][e] = 0.0f;
+
+  typename G::W wc[2], wn[2];
+#pragma unroll
+  for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
+  stage(a, t0, 0, lds, G::kNeedS);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (uint32_t j = 0; j < nsb; j++) {
+    const bool more = j + 1 < nsb;
+    if (more) {
+      stage(a, t0, j + 1, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS);
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) G::load(wn[tc], a.w, rowc[tc], j + 1, ln.q);
+    }
+    G::compute(wc, view(lds + (j & 1) * kStageBytes), ln, acc);
+    if (more) {
+#pragma unroll
+      for (int tc = 0; tc < 2; tc++) wc[tc] = wn[tc];
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // next stage landed in this wave
+    __syncthreads();                // ... and in every wave; current buffer free
+  }
+#pragma unroll
+  for (int tr = 0; tr < 2; tr++)
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const uint32_t tok = t0 + 32 * ln.tw + 16 * tr + 4 * ln.q + e;
+        const uint32_t row = r0 + 32 * ln.rw + 16 * tc + ln.i16;
+        if (tok < a.n && row < rows) {
+          const size_t idx = (size_t)tok * rows + row;
+          if (a.resid) {
+            RLH_GLOBAL float* x = (RLH_GLOBAL float*)a.resid;
+            x[idx] = x[idx] + acc[tr][tc][e];  // xs += xb (model.rs:548-552, 569-573)
+          }
+          if (a.y) ((RLH_GLOBAL float*)a.y)[idx] = acc[tr][tc][e];
+        }
+      }
+}
+
+}  // namespace
+
+bool gemm_supported(uint32_t ty) {
+  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
+}
+
+void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, float* y, float* resid) {
+  GemmArgs a{};
+  a.w = w;
+  a.x = Q8Ptr{x.qs, x.d, x.s, x.s16};
+  a.n = n;
+  a.y = y;
+  a.resid = resid;
+  a.n_tt = (n + kTile - 1) / kTile;
+  a.n_rt = (w.rows + kTile - 1) / kTile;
+  const uint32_t blocks = a.n_tt * ((a.n_rt + 7) / 8) * 8;
+  const size_t lds = 2 * kStageBytes;
+  switch (w.ty) {
+    case RLH_TYPE_Q4_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_K>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q6_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q6_K>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q8_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q8_0>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q4_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_0>, dim3(blocks), dim3(256), lds, st, a); break;
+    default: break;
+  }
+}
+
+}  // namespace rlh

@@ -364,3 +364,12 @@ def block_dots(ty, w, rows, cols, q8):
     check(load().rlh_block_dots(ty, np.ascontiguousarray(w).ctypes.data, rows, cols, q8.ctypes.data,
                                 out.ctypes.data))
     return out
+
+
+def matmul_batch(ty, w, rows, cols, xs, n):
+    """ops::matmul_batch with integer semantics (BATCH_INT): ys[n][rows]."""
+    ys = np.empty(n * rows, np.float32)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    check(load().rlh_matmul_batch(ty, np.ascontiguousarray(w).ctypes.data, rows, cols, xs.ctypes.data, n,
+                                  ys.ctypes.data))
+    return ys

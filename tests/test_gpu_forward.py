@@ -121,3 +121,27 @@ def test_cache_max_ctx_clamped_to_n_ctx():
     c = m.new_cache(10 ** 6)
     assert c.max_ctx == spec.n_ctx
     c.close()
+
+
+def test_long_prefill_chunks_and_continuation():
+    """A prompt longer than one prefill chunk (512 tokens), then a second
+    batch continuing at start_pos > 0: logits and every K/V row bit-exact
+    against the oracle's single forward_batch calls."""
+    spec, tensors, m, om = _get("small-q4km")
+    prompt = rlh.synth_tokens(123, 600, spec.vocab)
+    more = rlh.synth_tokens(321, 30, spec.vocab)
+    c = m.new_cache(700)
+    oc = om.new_cache(700)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    print(f"  600-token prefill logits rel L2 {rel_l2(lg, rg):.3e}", flush=True)
+    assert np.array_equal(bits(lg), bits(rg))
+    lg2 = c.forward_into(more, 600)
+    rg2 = oc.forward_into(more, 600, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg2), bits(rg2))
+    for l in (0, spec.n_layer - 1):
+        for which in (0, 1):
+            assert np.array_equal(bits(c.read_kv(l, which, 630)), bits(oc.read_kv(l, which, 630)))
+    assert c.len == 630
+    c.close()
+    oc.close()
