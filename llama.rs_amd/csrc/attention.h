@@ -20,21 +20,39 @@ struct AttnArgs {
   const uint32_t* pos0;  // device: position of token 0
   float* kcache;         // layer base [max_ctx][KVH*128]
   float* vcache;
-  float* scores;         // [n_tok][H][t_stride]
+  float* scores;         // [n_tok][H][t_stride]: scores, then softmax probabilities in place
   uint32_t t_stride;
-  uint32_t t_max;  // bound on positions attended in this launch (grid / LDS sizing)
-  uint32_t vtile;  // V positions per LDS tile (attn_vtile)
+  uint32_t t_max;        // bound on positions attended in this launch (grid / LDS sizing)
+  uint32_t max_ctx;      // rows of the cache (K/V tiles never read past it)
+  uint32_t n_tok;
   int H, KVH;
   float eps, scale;
   float* out;    // [n_tok][H*128]
   Q8Mut out_q8;  // Q8 blocks of out
 };
 
-uint32_t attn_vtile(uint32_t t_max);
-size_t attn_out_lds(uint32_t t_max, uint32_t vtile);
-// fused = decode: QK-norm + RoPE + K/V write inside the scores kernel.
-void launch_attn_scores(hipStream_t st, const AttnArgs& a, uint32_t n_tok, bool fused);
-void launch_attn_out(hipStream_t st, const AttnArgs& a, uint32_t n_tok);
-bool attn_set_max_lds(size_t bytes);
+// Query heads per KV head the kernels accept (1..8).
+constexpr int kAttnMaxGroup = 8;
+// Positions a softmax row may hold (dynamic LDS of one row).
+constexpr uint32_t kAttnMaxCtx = 32768;
+
+// Scores s_j = dot(q_h, K_j) * scale for every token and head. fused =
+// decode (one token): QK-norm + RoPE of q and k and the K/V write at pos are
+// done here as well.
+void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused);
+// softmax_inplace of every score row (probabilities overwrite the scores).
+void launch_attn_softmax(hipStream_t st, const AttnArgs& a);
+// Decode (one token) after the scores: softmax and the ordered V
+// accumulation in one kernel when the group's score rows fit its LDS,
+// otherwise launch_attn_softmax + the decode PV kernel.
+void launch_attn_decode(hipStream_t st, const AttnArgs& a);
+// LDS of the fused decode kernel for t_max positions and `group` query heads
+// per KV head (0 when the rows do not fit).
+size_t attn_dec_fused_lds(uint32_t t_max, uint32_t group);
+// Ordered V accumulation of the probabilities; writes out and its Q8 blocks.
+// decode = one token (d-sliced blocks), else token tiles sharing V chunks.
+void launch_attn_pv(hipStream_t st, const AttnArgs& a, bool decode);
+// Raises the softmax kernel's dynamic LDS limit to cover max_ctx positions.
+bool attn_init(uint32_t max_ctx);
 
 }  // namespace rlh

@@ -3,19 +3,29 @@
 //   s_j  = dot_f32_avx2(q_h, K_j) * scale            (simd.rs:328-377)
 //   p    = softmax_inplace(s)                        (ops.rs:398-419:
 //          max, e_j = expf(s_j - max), sum = sequential sum of e_j,
-//          p_j = e_j * (1/sum))
+//          p_j = e_j * (1/sum) when sum > 0)
 //   o_d  = sequential over j of (p_j * V_j[d]) + o_d (saxpy, simd.rs:674-691)
 //
-// Kernel A (k_attn_scores) is wide: one block per (kv head, 64-position
-// chunk, token); each thread evaluates whole 128-dim dot products with the
-// reference's 32-slot FMA tree. In decode it also applies QK-norm
-// (rmsnorm_head) and NeoX RoPE to the group's q heads and, in the block that
-// owns the new position, to k, and writes K/V at pos (model.rs:642-656).
-// Kernel B (k_attn_out) runs one block per (head, 32-wide slice of the head
-// dimension, token). The softmax sum is one sequential chain; while it runs
-// the V slice streams into LDS; the products p_j * V_j[d] are formed in LDS
-// and 32 lanes run the ordered saxpy chains over double-buffered V tiles.
-// The 32 outputs of a slice are one Q8 block of the attn_output input.
+// k_attn_qk: one block per (KV head, 64-position tile, tile of query
+// tokens). The tile's K rows are staged in LDS once; each lane owns a
+// position and holds its K row in registers for all of its wave's (token,
+// head) combinations, whose q vectors are LDS broadcasts. K rows and q are
+// stored slot-major (element e = 8m + l + 32k at 16l + 4m + k): the FMA
+// chains, A_l = (a0+a1)+(a2+a3) and the reduction tree then follow the
+// reference exactly. Tiles above the causal diagonal exit at once. In decode
+// the kernel also applies QK-norm (rmsnorm_head) and NeoX RoPE to the q
+// heads and, in the block whose tile holds the new position, to k, and
+// writes K/V at pos (model.rs:642-656); all of it in registers.
+// k_attn_softmax: one block per (head, token): the row in LDS, max and exp
+// in parallel, the sequential sum in one lane, probabilities written back
+// over the scores.
+// k_attn_pv_dec (decode): one block per (KV head, 32-wide slice of the head
+// dimension). V slices and probabilities stream through double-buffered LDS
+// chunks while one lane per (head, dimension) runs its ordered saxpy chain.
+// k_attn_pv_pre (prefill): one block per (KV head, tile of query tokens);
+// each V chunk staged in LDS serves every token and head of the tile, and
+// each thread runs eight independent chains. The 32 outputs of a half wave
+// are one Q8 block of the attn_output input in both variants.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -27,261 +37,733 @@ namespace rlh {
 namespace {
 
 constexpr int kHd = 128;
-constexpr int kChunk = 64;  // positions per scores block
+constexpr int kPosTile = 64;    // positions per scores block
+constexpr int kKStride = 132;   // floats per staged K row (permuted + 4 pad)
+constexpr int kQkComb = 16;     // (token, head) combinations per scores block
+constexpr int kDecChunk = 256;  // positions per LDS chunk, decode PV
+constexpr int kPreChunk = 64;   // positions per LDS chunk, prefill PV
+constexpr int kPreComb = 32;    // (token, head) combinations per prefill PV block
+// dynamic LDS of the fused decode kernel's score rows (its V chunks take
+// 66.5 KB of static LDS)
+constexpr size_t kDecFusedLds = 88u * 1024u;
 typedef RLH_LDS float lfloat;
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef RLH_LDS f32x4_t lf32x4;
 
-// One head of 128 values in LDS: (+bias), rmsnorm_head (exact tree, one
-// wave), then NeoX RoPE at `pos` from the glibc-built cos/sin table. The
-// calling wave must be whole (64 lanes).
-__device__ __forceinline__ void norm_rope_head(lfloat* hb, const float* nw, const float* rope_cs, uint32_t pos,
+__device__ __forceinline__ int perm(int e) { return (e & 7) * 16 + ((e >> 3) & 3) * 4 + (e >> 5); }
+
+// rmsnorm_head + NeoX RoPE of one 128-value head held by a whole wave:
+// lane l owns elements l (x0) and l + 64 (x1). Slot s of rmsnorm_core's
+// 32 FMA chains takes elements s, s+32, s+64, s+96 in that order; lanes
+// 0..31 build them with the partner lane l ^ 32, then the exact AVX2 tree.
+// out = (x * s) * w; RoPE pair (l, l + 64) with the glibc-built cos/sin.
+__device__ __forceinline__ void norm_rope_regs(float& x0, float& x1, bool norm, float w0, float w1, float c, float sn,
                                                float eps) {
-  const int lane = threadIdx.x & 63;
-  if (nw) {
-    const int n = kHd;
-    float acc = 0.0f;
-    if (lane < 32)
-      for (int i = lane; i < n; i += 32) acc = __builtin_fmaf(hb[i], hb[i], acc);
-    float ss = avx2_tree32(acc);
-    float s = 1.0f / sqrtf(ss / (float)n + eps);
-    float a0 = hb[lane] * s * ld_gf(nw + lane);
-    float a1 = hb[lane + 64] * s * ld_gf(nw + lane + 64);
-    hb[lane] = a0;
-    hb[lane + 64] = a1;
+  if (norm) {
+    const float y0 = __shfl_xor(x0, 32), y1 = __shfl_xor(x1, 32);
+    float acc = __builtin_fmaf(x0, x0, 0.0f);
+    acc = __builtin_fmaf(y0, y0, acc);
+    acc = __builtin_fmaf(x1, x1, acc);
+    acc = __builtin_fmaf(y1, y1, acc);
+    const float ss = avx2_tree32(acc);
+    const float s = 1.0f / sqrtf(ss / (float)kHd + eps);
+    x0 = x0 * s * w0;
+    x1 = x1 * s * w1;
   }
-  const float c = ld_gf(rope_cs + (size_t)pos * kHd + 2 * lane);
-  const float sn = ld_gf(rope_cs + (size_t)pos * kHd + 2 * lane + 1);
-  float x0 = hb[lane], x1 = hb[lane + 64];
-  hb[lane] = x0 * c - x1 * sn;
-  hb[lane + 64] = x0 * sn + x1 * c;
+  const float r0 = x0 * c - x1 * sn;
+  const float r1 = x0 * sn + x1 * c;
+  x0 = r0;
+  x1 = r1;
 }
 
-// grid: (KVH * nchunks, n_tok); block 256; static LDS.
+// grid: (KVH * ntiles, ceil(n_tok / TT)); block 256.
 template <bool FUSED>
-__global__ void __launch_bounds__(256) k_attn_scores(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) float qv[8 * kHd];
-  __shared__ __attribute__((aligned(16))) float kpos[kHd];
+__global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
+  __shared__ __attribute__((aligned(16))) float qv_g[kQkComb * kHd];
+  lfloat* kt = (lfloat*)kt_g;
+  lfloat* qv = (lfloat*)qv_g;
   const int G = a.H / a.KVH;
-  const uint32_t nchunks = (a.t_max + kChunk - 1) / kChunk;
-  const uint32_t g = blockIdx.x / nchunks, chunk = blockIdx.x % nchunks;
-  const uint32_t tok = blockIdx.y;
-  const uint32_t pos = a.pos0[0] + tok;
-  const uint32_t t = pos + 1;
-  const uint32_t j0 = chunk * kChunk;
-  if (j0 >= t) return;
-  const uint32_t jn = t - j0 < (uint32_t)kChunk ? t - j0 : (uint32_t)kChunk;
+  const uint32_t TT = FUSED ? 1u : (uint32_t)(kQkComb / G);
+  const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
+  const uint32_t g = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const uint32_t tok0 = blockIdx.y * TT;
+  const uint32_t ntok = a.n_tok - tok0 < TT ? a.n_tok - tok0 : TT;
+  const uint32_t pos_first = a.pos0[0] + tok0, pos_last = pos_first + ntok - 1;
+  const uint32_t j0 = tile * kPosTile;
+  if (j0 > pos_last) return;  // whole tile above the causal diagonal
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qd = a.H * kHd, kvd = a.KVH * kHd;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool own_pos = pos >= j0 && pos < j0 + kChunk;
-  // q heads of the group -> LDS (normalised + roped here in decode)
-  for (int h = wave; h < G; h += 4) {
-    lfloat* hb = (lfloat*)qv + h * kHd;
-    const float* src = a.q + (size_t)tok * qd + (g * G + h) * kHd;
-    float v0 = ld_gf(src + lane), v1 = ld_gf(src + lane + 64);
-    if (FUSED && a.bq) {
-      v0 = v0 + ld_gf(a.bq + (g * G + h) * kHd + lane);
-      v1 = v1 + ld_gf(a.bq + (g * G + h) * kHd + lane + 64);
-    }
-    hb[lane] = v0;
-    hb[lane + 64] = v1;
-    if (FUSED) norm_rope_head(hb, a.qn, a.rope_cs, pos, a.eps);
+  const int ncomb = (int)ntok * G;
+  const int nmine = ncomb > wave ? (ncomb - wave + 3) / 4 : 0;  // combinations wave, wave+4, ...
+  const bool own_pos = FUSED && pos_last < j0 + kPosTile;
+
+  // every global load first: K tile rows (the new position's row, in
+  // decode, is produced below), q heads, and the decode norm/rope operands
+  // every global load first and unconditionally (indices clamped into
+  // bounds, absent optional vectors replaced by a valid row whose values are
+  // then not used): a load under a branch gets a wait for every load before
+  // it. K tile rows (the new position's row, in decode, is produced below),
+  // q heads, and the decode norm/rope operands.
+  float4 kr[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t c = (uint32_t)(tid + 256 * i), jl = c >> 5, f4 = c & 31, j = min(j0 + jl, pos_last);
+    kr[i] = ld_gf4(a.kcache + (size_t)j * kvd + g * kHd + 4 * f4);
   }
-  if (FUSED && own_pos && wave == 0) {
-    lfloat* kb = (lfloat*)kpos;
-    const float* ks = a.k + (size_t)tok * kvd + g * kHd;
-    float v0 = ld_gf(ks + lane), v1 = ld_gf(ks + lane + 64);
-    if (a.bk) {
-      v0 = v0 + ld_gf(a.bk + g * kHd + lane);
-      v1 = v1 + ld_gf(a.bk + g * kHd + lane + 64);
-    }
-    kb[lane] = v0;
-    kb[lane + 64] = v1;
-    norm_rope_head(kb, a.kn, a.rope_cs, pos, a.eps);
-    float* kd = a.kcache + (size_t)pos * kvd + g * kHd;
-    kd[lane] = kb[lane];
-    kd[lane + 64] = kb[lane + 64];
-    const float* vs = a.v + (size_t)tok * kvd + g * kHd;
-    float* vd = a.vcache + (size_t)pos * kvd + g * kHd;
-    float w0 = ld_gf(vs + lane), w1 = ld_gf(vs + lane + 64);
-    if (a.bv) {
-      w0 = w0 + ld_gf(a.bv + g * kHd + lane);
-      w1 = w1 + ld_gf(a.bv + g * kHd + lane + 64);
-    }
-    vd[lane] = w0;
-    vd[lane + 64] = w1;
-  }
-  __syncthreads();
-  // one (position, head) dot per thread: 32 slot FMA chains + AVX2 tree
-  for (uint32_t idx = threadIdx.x; idx < jn * (uint32_t)G; idx += 256) {
-    const uint32_t jl = idx % jn, h = idx / jn, j = j0 + jl;
-    const lfloat* qh = (const lfloat*)qv + h * kHd;
-    const float* kr = (FUSED && j == pos) ? nullptr : a.kcache + (size_t)j * kvd + g * kHd;
-    float acc[32];
+  const bool hb = FUSED && a.bq != nullptr;
+  const float* bq = hb ? a.bq : a.q;
+  float q0[4], q1[4];
 #pragma unroll
-    for (int s = 0; s < 32; s++) acc[s] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int s4 = 0; s4 < 8; s4++) {
-        float4 kk;
-        if (kr) {
-          kk = ld_gf4(kr + i * 32 + s4 * 4);
-        } else {
-          const lfloat* kp = (const lfloat*)kpos + i * 32 + s4 * 4;
-          kk = make_float4(kp[0], kp[1], kp[2], kp[3]);
-        }
-        const int s = s4 * 4, e = i * 32 + s;
-        acc[s] = __builtin_fmaf(qh[e], kk.x, acc[s]);
-        acc[s + 1] = __builtin_fmaf(qh[e + 1], kk.y, acc[s + 1]);
-        acc[s + 2] = __builtin_fmaf(qh[e + 2], kk.z, acc[s + 2]);
-        acc[s + 3] = __builtin_fmaf(qh[e + 3], kk.w, acc[s + 3]);
+  for (int i = 0; i < 4; i++) {
+    const int cb = min(wave + 4 * i, ncomb - 1), tt = cb / G, h = g * G + cb % G;
+    const float* src = a.q + (size_t)(tok0 + tt) * qd + h * kHd;
+    q0[i] = ld_gf(src + lane);
+    q1[i] = ld_gf(src + lane + 64);
+    if (FUSED) {
+      const float b0 = ld_gf(bq + h * kHd + lane), b1 = ld_gf(bq + h * kHd + lane + 64);
+      if (hb) {
+        q0[i] = q0[i] + b0;
+        q1[i] = q1[i] + b1;
       }
     }
+  }
+  if (FUSED) {
+    const float c = ld_gf(a.rope_cs + (size_t)pos_first * kHd + 2 * lane);
+    const float sn = ld_gf(a.rope_cs + (size_t)pos_first * kHd + 2 * lane + 1);
+    const bool nq = a.qn != nullptr;
+    const float* qn = nq ? a.qn : a.rope_cs;
+    const float w0 = ld_gf(qn + lane), w1 = ld_gf(qn + lane + 64);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      if (i < nmine) norm_rope_regs(q0[i], q1[i], nq, w0, w1, c, sn, a.eps);
+    if (own_pos && wave == 3) {  // k and v of the new position (model.rs:642-656)
+      const uint32_t pos = pos_last;
+      const bool hbk = a.bk != nullptr, hbv = a.bv != nullptr, nk = a.kn != nullptr;
+      const float* bk = hbk ? a.bk : a.k;
+      const float* bv = hbv ? a.bv : a.v;
+      const float* kn = nk ? a.kn : a.rope_cs;
+      float k0 = ld_gf(a.k + g * kHd + lane), k1 = ld_gf(a.k + g * kHd + lane + 64);
+      float v0 = ld_gf(a.v + g * kHd + lane), v1 = ld_gf(a.v + g * kHd + lane + 64);
+      const float bk0 = ld_gf(bk + g * kHd + lane), bk1 = ld_gf(bk + g * kHd + lane + 64);
+      const float bv0 = ld_gf(bv + g * kHd + lane), bv1 = ld_gf(bv + g * kHd + lane + 64);
+      const float u0 = ld_gf(kn + lane), u1 = ld_gf(kn + lane + 64);
+      if (hbk) {
+        k0 = k0 + bk0;
+        k1 = k1 + bk1;
+      }
+      if (hbv) {
+        v0 = v0 + bv0;
+        v1 = v1 + bv1;
+      }
+      norm_rope_regs(k0, k1, nk, u0, u1, c, sn, a.eps);
+      float* kd = a.kcache + (size_t)pos * kvd + g * kHd;
+      kd[lane] = k0;
+      kd[lane + 64] = k1;
+      float* vd = a.vcache + (size_t)pos * kvd + g * kHd;
+      vd[lane] = v0;
+      vd[lane + 64] = v1;
+      lfloat* row = kt + (pos - j0) * kKStride;
+      row[perm(lane)] = k0;
+      row[perm(lane + 64)] = k1;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t c = (uint32_t)(tid + 256 * i), jl = c >> 5, f4 = c & 31, j = j0 + jl;
+    if (j <= pos_last && !(FUSED && j == pos_last)) {
+      lfloat* row = kt + jl * kKStride;
+      row[perm(4 * f4)] = kr[i].x;
+      row[perm(4 * f4 + 1)] = kr[i].y;
+      row[perm(4 * f4 + 2)] = kr[i].z;
+      row[perm(4 * f4 + 3)] = kr[i].w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (i < nmine) {
+      const int cb = wave + 4 * i;
+      qv[cb * kHd + perm(lane)] = q0[i];
+      qv[cb * kHd + perm(lane + 64)] = q1[i];
+    }
+  }
+  __syncthreads();
+  if (nmine == 0) return;
+  // lane = position: the K row sits in registers for all the wave's
+  // combinations; q is read from LDS as a broadcast
+  const uint32_t j = j0 + (uint32_t)lane;
+  const lf32x4* krow = (const lf32x4*)(kt + lane * kKStride);
+  f32x4_t kreg[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) kreg[i] = krow[i];
+#pragma unroll 1
+  for (int c = 0; c < nmine; c++) {
+    const int cb = wave + 4 * c, tt = cb / G, h = g * G + cb % G;
+    const lf32x4* qc = (const lf32x4*)(qv + cb * kHd);
     float A[8];
 #pragma unroll
-    for (int l = 0; l < 8; l++) A[l] = (acc[l] + acc[8 + l]) + (acc[16 + l] + acc[24 + l]);
-    const float dot = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
-    a.scores[((size_t)tok * a.H + g * G + h) * a.t_stride + j] = dot * a.scale;
+    for (int l = 0; l < 8; l++) {
+      float acc[4];
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const f32x4_t x = qc[l * 4 + m];
+        const f32x4_t y = kreg[l * 4 + m];
+        float s = __builtin_fmaf(x.x, y.x, 0.0f);
+        s = __builtin_fmaf(x.y, y.y, s);
+        s = __builtin_fmaf(x.z, y.z, s);
+        acc[m] = __builtin_fmaf(x.w, y.w, s);
+      }
+      A[l] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    if (j <= pos_first + (uint32_t)tt) {
+      const float d = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+      a.scores[((size_t)(tok0 + tt) * a.H + h) * a.t_stride + j] = d * a.scale;
+    }
   }
 }
 
-// grid: (H, 4 slices, n_tok); block 256; dynamic LDS: e[t_max] + 2 V tiles of
-// vtile positions x 32 floats.
-__global__ void __launch_bounds__(256) k_attn_out(AttnArgs a) {
+// grid: (H, n_tok); block 256; dynamic LDS: one row of t_max floats.
+__global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
-  lfloat* lds = (lfloat*)lds_generic;
-  __shared__ float red[256];
+  __shared__ float red[4];
   __shared__ float s_inv;
   __shared__ int s_on;
-  const int h = blockIdx.x, slice = blockIdx.y, tok = blockIdx.z;
-  const int G = a.H / a.KVH;
-  const int kvh = h / G;
-  const int qd = a.H * kHd, kvd = a.KVH * kHd;
-  const uint32_t t = a.pos0[0] + tok + 1;
-  const uint32_t vt = a.vtile;
-  lfloat* e = lds;                                          // [t_max] (rounded to 4)
-  lfloat* vb = lds + ((a.t_max + 3) & ~3u);                 // [2][vt][32]
-  const float* srow = a.scores + ((size_t)tok * a.H + h) * a.t_stride;
-  // V slice rows: vcache[j][kvh*128 + slice*32 .. +32]
-  const float* vbase = a.vcache + kvh * kHd + slice * 32;
-  // thread -> (position in tile, float4 of the 32-float row)
-  const uint32_t vq = threadIdx.x & 7, vj = threadIdx.x >> 3;  // 8 float4 per row, 32 rows per pass
-  const uint32_t passes = vt / 32;
-  float4 pre[16];  // V of one tile (vt <= 512): passes <= 16
-  auto load_tile = [&](uint32_t j0) {
-#pragma unroll
-    for (int p = 0; p < 16; p++) {
-      uint32_t j = j0 + (uint32_t)p * 32 + vj;
-      if ((uint32_t)p < passes && j < t) pre[p] = ld_gf4(vbase + (size_t)j * kvd + vq * 4);
-    }
-  };
-  // V tile 0 starts streaming now; it lands while the softmax sum runs.
-  load_tile(0);
-  // scores -> e, max
+  __shared__ uint64_t tab_g[32];
+  lu64* tab = (lu64*)tab_g;
+  exp_tab_to_lds(tab);
+  lfloat* e = (lfloat*)lds_generic;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t t = a.pos0[0] + blockIdx.y + 1;
+  float* row = a.scores + ((size_t)blockIdx.y * a.H + blockIdx.x) * a.t_stride;
+  // max: the reference keeps x[0] and takes every later v > max, so a NaN
+  // first score gives NaN and later NaNs are skipped, as fmaxf does
   float mx = -__int_as_float(0x7f800000);
-  for (uint32_t j = threadIdx.x; j < t; j += 256) {
-    float s = ld_gf(srow + j);
+  for (uint32_t j = tid; j < t; j += 256) {
+    const float s = ld_gf(row + j);
     e[j] = s;
     mx = fmaxf(mx, s);
   }
-  red[threadIdx.x] = mx;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if ((int)threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
-    __syncthreads();
-  }
-  mx = red[0];
-  for (uint32_t j = threadIdx.x; j < t; j += 256) e[j] = expf_glibc(e[j] - mx);
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float x0 = e[0];
+  if (x0 != x0) mx = x0;
+  for (uint32_t j = tid; j < t; j += 256) e[j] = expf_glibc_t(e[j] - mx, tab);
   __syncthreads();
-  if (threadIdx.x == 0) {  // sequential sum of softmax_inplace
+  if (tid == 0) {  // the sequential sum of softmax_inplace, 16 values read ahead
     float sum = 0.0f;
-    uint32_t j = 0;
-    for (; j + 4 <= t; j += 4) {
-      f32x4_t v = *(const RLH_LDS f32x4_t*)(e + j);
+    const lf32x4* e4 = (const lf32x4*)e;
+    const uint32_t nq = t / 4;
+    uint32_t q = 0;
+    if (nq >= 4) {
+      f32x4_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = e4[i];
+      for (q = 4; q + 4 <= nq; q += 4) {
+        f32x4_t vn[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) vn[i] = e4[q + i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sum = sum + v[i].x;
+          sum = sum + v[i].y;
+          sum = sum + v[i].z;
+          sum = sum + v[i].w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = vn[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sum = sum + v[i].x;
+        sum = sum + v[i].y;
+        sum = sum + v[i].z;
+        sum = sum + v[i].w;
+      }
+    }
+    for (; q < nq; q++) {
+      const f32x4_t v = e4[q];
       sum = sum + v.x;
       sum = sum + v.y;
       sum = sum + v.z;
       sum = sum + v.w;
     }
-    for (; j < t; j++) sum = sum + e[j];
+    for (uint32_t j = 4 * nq; j < t; j++) sum = sum + e[j];
     s_on = sum > 0.0f;
     s_inv = 1.0f / sum;
   }
   __syncthreads();
-  if (s_on) {  // p_j = e_j * inv
-    const float inv = s_inv;
-    for (uint32_t j = threadIdx.x; j < t; j += 256) e[j] = e[j] * inv;
+  const bool on = s_on;
+  const float inv = s_inv;
+  for (uint32_t j = tid; j < t; j += 256) {
+    const float v = e[j];
+    row[j] = on ? v * inv : v;
+  }
+}
+
+// grid: (KVH, 4 slices of 32 dimensions); block 512. Lanes tid < G*32 run
+// the chains of (head tid/32, dimension d0 + tid%32); every thread loads.
+__global__ void __launch_bounds__(512) k_attn_pv_dec(AttnArgs a) {
+  constexpr int CS = kDecChunk + 4;
+  __shared__ __attribute__((aligned(16))) float vs_g[2 * 32 * CS];
+  __shared__ __attribute__((aligned(16))) float ps_g[2 * kAttnMaxGroup * CS];
+  lfloat* vs = (lfloat*)vs_g;
+  lfloat* ps = (lfloat*)ps_g;
+  const int G = a.H / a.KVH;
+  const uint32_t g = blockIdx.x, d0 = blockIdx.y * 32;
+  const int tid = threadIdx.x, hl = tid >> 5, dd = tid & 31;
+  const int kvd = a.KVH * kHd;
+  const uint32_t t = a.pos0[0] + 1;
+  const uint32_t nch = (t + kDecChunk - 1) / kDecChunk;
+  const float* vsrc = a.vcache + g * kHd + d0;
+  const float* prow = a.scores + (size_t)g * G * a.t_stride;
+  float4 vr[4];
+  float pr[4];
+  // chunk k: V rows (8 float4 of the slice each) and G probability rows
+  auto load = [&](uint32_t k) {
+    const uint32_t jb = k * kDecChunk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // unconditional: indices clamped into bounds
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 3, f4 = c & 7;
+      vr[i] = ld_gf4(vsrc + (size_t)min(jb + jl, t - 1) * kvd + 4 * f4);
+      const uint32_t h = min(c / kDecChunk, (uint32_t)G - 1), pl = c % kDecChunk;
+      pr[i] = ld_gf(prow + (size_t)h * a.t_stride + min(jb + pl, t - 1));
+    }
+  };
+  auto store = [&](uint32_t k) {
+    const uint32_t jb = k * kDecChunk;
+    lfloat* vb = vs + (k & 1) * 32 * CS;
+    lfloat* pb = ps + (k & 1) * kAttnMaxGroup * CS;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 3, f4 = c & 7;
+      if (jb + jl < t) {
+        vb[(4 * f4 + 0) * CS + jl] = vr[i].x;
+        vb[(4 * f4 + 1) * CS + jl] = vr[i].y;
+        vb[(4 * f4 + 2) * CS + jl] = vr[i].z;
+        vb[(4 * f4 + 3) * CS + jl] = vr[i].w;
+      }
+      const uint32_t h = c / kDecChunk, pl = c % kDecChunk;
+      if ((int)h < G && jb + pl < t) pb[h * CS + pl] = pr[i];
+    }
+  };
+  const bool chain = tid < G * 32;
+  float o = 0.0f;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (uint32_t k = 0; k < nch; k++) {
+    if (k + 1 < nch) load(k + 1);
+    if (chain) {
+      const lf32x4* vb = (const lf32x4*)(vs + (k & 1) * 32 * CS + dd * CS);
+      const lf32x4* pb = (const lf32x4*)(ps + (k & 1) * kAttnMaxGroup * CS + hl * CS);
+      const uint32_t rem = t - k * kDecChunk;
+      const uint32_t jn = rem < (uint32_t)kDecChunk ? rem : (uint32_t)kDecChunk;
+      const uint32_t nq = jn / 4;
+      uint32_t q = 0;
+      if (nq >= 4) {  // 16 positions in flight while the previous 16 are chained
+        f32x4_t v[4], p[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = vb[i], p[i] = pb[i];
+        for (q = 4; q + 4 <= nq; q += 4) {
+          f32x4_t vn[4], pn[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) vn[i] = vb[q + i], pn[i] = pb[q + i];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            o = p[i].x * v[i].x + o;
+            o = p[i].y * v[i].y + o;
+            o = p[i].z * v[i].z + o;
+            o = p[i].w * v[i].w + o;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) v[i] = vn[i], p[i] = pn[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          o = p[i].x * v[i].x + o;
+          o = p[i].y * v[i].y + o;
+          o = p[i].z * v[i].z + o;
+          o = p[i].w * v[i].w + o;
+        }
+      }
+      for (; q < nq; q++) {
+        const f32x4_t v = vb[q], p = pb[q];
+        o = p.x * v.x + o;
+        o = p.y * v.y + o;
+        o = p.z * v.z + o;
+        o = p.w * v.w + o;
+      }
+      const lfloat* vs1 = (const lfloat*)vb;
+      const lfloat* ps1 = (const lfloat*)pb;
+      for (uint32_t jj = 4 * nq; jj < jn; jj++) o = ps1[jj] * vs1[jj] + o;
+    }
+    if (k + 1 < nch) store(k + 1);
     __syncthreads();
   }
-  // products of tile 0
-  auto store_tile = [&](uint32_t j0, lfloat* dst) {
+  if (chain) {
+    const uint32_t col = (uint32_t)(g * G + hl) * kHd + d0 + dd;
+    ((RLH_GLOBAL float*)a.out)[col] = o;
+    q8_quant_block32(o, a.out_q8, col / 32);
+  }
+}
+
+// Decode with the softmax fused: grid (KVH, 4 slices of 32 dimensions),
+// block 512, dynamic LDS: the group's G score rows (stride RS, a multiple of
+// 64). Each block computes softmax_inplace of the G rows itself (the same
+// arithmetic as k_attn_softmax): the rows arrive by global_load_lds while
+// the first V chunk's loads are in flight, max and exp run over head groups
+// of threads, lanes 0..G-1 run the G sequential sums side by side, and the
+// probabilities stay in LDS for the saxpy chains (as in k_attn_pv_dec).
+__host__ __device__ inline uint32_t dec_row_stride(uint32_t t_max) { return (t_max + 63) & ~63u; }
+
+__global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
+  constexpr int CS = kDecChunk + 4;
+  __shared__ __attribute__((aligned(16))) float vs_g[2 * 32 * CS];
+  __shared__ float red[8 * kAttnMaxGroup];
+  __shared__ float s_mx[kAttnMaxGroup], s_inv[kAttnMaxGroup];
+  __shared__ int s_on[kAttnMaxGroup];
+  __shared__ uint64_t tab_g[32];
+  extern __shared__ __attribute__((aligned(16))) float lds_generic[];
+  lu64* tab = (lu64*)tab_g;
+  exp_tab_to_lds(tab);
+  lfloat* vs = (lfloat*)vs_g;
+  lfloat* e = (lfloat*)lds_generic;
+  const int G = a.H / a.KVH;
+  const uint32_t RS = dec_row_stride(a.t_max);
+  const uint32_t g = blockIdx.x, d0 = blockIdx.y * 32;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, hl = tid >> 5, dd = tid & 31;
+  const int kvd = a.KVH * kHd;
+  const uint32_t t = a.pos0[0] + 1;
+  const uint32_t nch = (t + kDecChunk - 1) / kDecChunk;
+  const float* vsrc = a.vcache + g * kHd + d0;
+  const float* srow = a.scores + (size_t)g * G * a.t_stride;
+  // score rows -> LDS, 64 positions per wave instruction (positions past t
+  // repeat the last score; their slots lie inside the row stride)
+  const uint32_t pieces = (t + 63) / 64;
+  for (uint32_t pc = wave; pc < (uint32_t)G * pieces; pc += 8) {
+    const uint32_t h = pc / pieces, j0 = (pc % pieces) * 64;
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(srow + (size_t)h * a.t_stride + min(j0 + lane, t - 1)),
+                                     (RLH_LDS void*)(e + h * RS + j0), 4, 0, 0);
+  }
+  // first V chunk to registers (unconditional, indices clamped)
+  float4 vr[4];
+  auto load = [&](uint32_t k) {
+    const uint32_t jb = k * kDecChunk;
 #pragma unroll
-    for (int p = 0; p < 16; p++) {
-      uint32_t jl = (uint32_t)p * 32 + vj, j = j0 + jl;
-      if ((uint32_t)p < passes && j < t) {
-        const float pj = e[j];
-        lfloat* d = dst + jl * 32 + vq * 4;
-        d[0] = pj * pre[p].x;
-        d[1] = pj * pre[p].y;
-        d[2] = pj * pre[p].z;
-        d[3] = pj * pre[p].w;
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 3, f4 = c & 7;
+      vr[i] = ld_gf4(vsrc + (size_t)min(jb + jl, t - 1) * kvd + 4 * f4);
+    }
+  };
+  auto store = [&](uint32_t k) {
+    const uint32_t jb = k * kDecChunk;
+    lfloat* vb = vs + (k & 1) * 32 * CS;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 3, f4 = c & 7;
+      if (jb + jl < t) {
+        vb[(4 * f4 + 0) * CS + jl] = vr[i].x;
+        vb[(4 * f4 + 1) * CS + jl] = vr[i].y;
+        vb[(4 * f4 + 2) * CS + jl] = vr[i].z;
+        vb[(4 * f4 + 3) * CS + jl] = vr[i].w;
       }
     }
   };
-  store_tile(0, vb);
+  load(0);
+  // the score copies are older than the 4 V loads: wait until at most those
+  // 4 are outstanding (vmcnt 4, expcnt and lgkmcnt not waited on)
+  __builtin_amdgcn_s_waitcnt(0x0F74);
   __syncthreads();
-  float o = 0.0f;
-  uint32_t buf = 0;
-  for (uint32_t j0 = 0; j0 < t; j0 += vt) {
-    const uint32_t jn = t - j0 < vt ? t - j0 : vt;
-    const bool more = j0 + vt < t;
-    if (more) load_tile(j0 + vt);
-    if (threadIdx.x < 32) {  // the ordered saxpy chains
-      const lfloat* pr = vb + buf * vt * 32 + threadIdx.x;
-      for (uint32_t jl = 0; jl < jn; jl++) o = pr[jl * 32] + o;
-    }
-    if (more) store_tile(j0 + vt, vb + (buf ^ 1) * vt * 32);
-    __syncthreads();
-    buf ^= 1;
+  // softmax_inplace of the G rows (ops.rs:398-419); head hg is taken by
+  // TPH = 64 * floor(8 / G) threads
+  const uint32_t TPH = 64u * (8u / (uint32_t)G), WPH = TPH / 64;
+  const uint32_t hg = tid / TPH, lt = tid % TPH;
+  lfloat* eh = e + min(hg, (uint32_t)G - 1) * RS;
+  float mx = -__int_as_float(0x7f800000);
+  if (hg < (uint32_t)G)
+    for (uint32_t j = lt; j < t; j += TPH) mx = fmaxf(mx, eh[j]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  if (tid < G) {  // NaN first score: the reference's max stays NaN
+    float m = red[tid * WPH];
+    for (uint32_t w = 1; w < WPH; w++) m = fmaxf(m, red[tid * WPH + w]);
+    const float x0 = e[tid * RS];
+    s_mx[tid] = x0 != x0 ? x0 : m;
   }
-  if (threadIdx.x < 32) {
-    const uint32_t d = (uint32_t)h * kHd + (uint32_t)slice * 32 + threadIdx.x;
-    ((RLH_GLOBAL float*)a.out)[(size_t)tok * qd + d] = o;
-    const uint32_t nbq = (uint32_t)qd / 32;
-    Q8Out ot{a.out_q8.qs + (size_t)tok * qd, a.out_q8.d + (size_t)tok * nbq, a.out_q8.s + (size_t)tok * nbq,
-             a.out_q8.s16 + (size_t)tok * nbq * 2};
-    q8_quant_block32(o, ot, d / 32);
+  __syncthreads();
+  if (hg < (uint32_t)G) {
+    const float m = s_mx[hg];
+    for (uint32_t j = lt; j < t; j += TPH) eh[j] = expf_glibc_t(eh[j] - m, tab);
+  }
+  __syncthreads();
+  if (tid < G) {  // the G sequential sums, one lane each, 16 values read ahead
+    const lf32x4* e4 = (const lf32x4*)(e + tid * RS);
+    float sum = 0.0f;
+    const uint32_t nq = t / 4;
+    uint32_t q = 0;
+    if (nq >= 4) {
+      f32x4_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = e4[i];
+      for (q = 4; q + 4 <= nq; q += 4) {
+        f32x4_t vn[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) vn[i] = e4[q + i];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sum = sum + v[i].x;
+          sum = sum + v[i].y;
+          sum = sum + v[i].z;
+          sum = sum + v[i].w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = vn[i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        sum = sum + v[i].x;
+        sum = sum + v[i].y;
+        sum = sum + v[i].z;
+        sum = sum + v[i].w;
+      }
+    }
+    for (; q < nq; q++) {
+      const f32x4_t v = e4[q];
+      sum = sum + v.x;
+      sum = sum + v.y;
+      sum = sum + v.z;
+      sum = sum + v.w;
+    }
+    const lfloat* e1 = e + tid * RS;
+    for (uint32_t j = 4 * nq; j < t; j++) sum = sum + e1[j];
+    s_on[tid] = sum > 0.0f;
+    s_inv[tid] = 1.0f / sum;
+  }
+  __syncthreads();
+  if (hg < (uint32_t)G && s_on[hg]) {
+    const float inv = s_inv[hg];
+    for (uint32_t j = lt; j < t; j += TPH) eh[j] = eh[j] * inv;
+  }
+  store(0);
+  __syncthreads();
+  // the ordered saxpy chains over double-buffered V chunks
+  const bool chain = tid < G * 32;
+  float o = 0.0f;
+  for (uint32_t k = 0; k < nch; k++) {
+    if (k + 1 < nch) load(k + 1);
+    if (chain) {
+      const lf32x4* vb = (const lf32x4*)(vs + (k & 1) * 32 * CS + dd * CS);
+      const lf32x4* pb = (const lf32x4*)(e + hl * RS + k * kDecChunk);
+      const uint32_t rem = t - k * kDecChunk;
+      const uint32_t jn = rem < (uint32_t)kDecChunk ? rem : (uint32_t)kDecChunk;
+      const uint32_t nq = jn / 4;
+      uint32_t q = 0;
+      if (nq >= 4) {  // 16 positions in flight while the previous 16 are chained
+        f32x4_t v[4], p[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = vb[i], p[i] = pb[i];
+        for (q = 4; q + 4 <= nq; q += 4) {
+          f32x4_t vn[4], pn[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) vn[i] = vb[q + i], pn[i] = pb[q + i];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            o = p[i].x * v[i].x + o;
+            o = p[i].y * v[i].y + o;
+            o = p[i].z * v[i].z + o;
+            o = p[i].w * v[i].w + o;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; i++) v[i] = vn[i], p[i] = pn[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          o = p[i].x * v[i].x + o;
+          o = p[i].y * v[i].y + o;
+          o = p[i].z * v[i].z + o;
+          o = p[i].w * v[i].w + o;
+        }
+      }
+      for (; q < nq; q++) {
+        const f32x4_t v = vb[q], p = pb[q];
+        o = p.x * v.x + o;
+        o = p.y * v.y + o;
+        o = p.z * v.z + o;
+        o = p.w * v.w + o;
+      }
+      const lfloat* vs1 = (const lfloat*)vb;
+      const lfloat* ps1 = (const lfloat*)pb;
+      for (uint32_t jj = 4 * nq; jj < jn; jj++) o = ps1[jj] * vs1[jj] + o;
+    }
+    if (k + 1 < nch) store(k + 1);
+    __syncthreads();
+  }
+  if (chain) {
+    const uint32_t col = (uint32_t)(g * G + hl) * kHd + d0 + dd;
+    ((RLH_GLOBAL float*)a.out)[col] = o;
+    q8_quant_block32(o, a.out_q8, col / 32);
   }
 }
+
+// grid: (KVH, ceil(n_tok / TT)), TT = 32 / G tokens per block, latest (most
+// positions) token tiles first; block 512: thread (d = tid % 128, quarter
+// tid / 128) runs the chains of combinations quarter + 4i.
+__global__ void __launch_bounds__(512) k_attn_pv_pre(AttnArgs a) {
+  constexpr int CS = kPreChunk + 4;
+  constexpr int NC = kPreComb / 4;  // chains per thread
+  __shared__ __attribute__((aligned(16))) float vs_g[kPreChunk * kHd];
+  __shared__ __attribute__((aligned(16))) float ps_g[kPreComb * CS];
+  lfloat* vs = (lfloat*)vs_g;
+  lfloat* ps = (lfloat*)ps_g;
+  const int G = a.H / a.KVH;
+  const uint32_t TT = (uint32_t)(kPreComb / G);
+  const int ncomb = (int)TT * G;
+  const uint32_t g = blockIdx.x;
+  const uint32_t tok0 = (gridDim.y - 1 - blockIdx.y) * TT;
+  const uint32_t ntok = a.n_tok - tok0 < TT ? a.n_tok - tok0 : TT;
+  const int tid = threadIdx.x, d = tid & 127, qtr = tid >> 7;
+  const int qd = a.H * kHd, kvd = a.KVH * kHd;
+  const uint32_t p0 = a.pos0[0];
+  const uint32_t t_lo = p0 + tok0 + 1, t_hi = p0 + tok0 + ntok;
+  float o[NC];
+  uint32_t tlim[NC];  // positions chain i takes (0 for combinations past the last token)
+#pragma unroll
+  for (int i = 0; i < NC; i++) {
+    o[i] = 0.0f;
+    const int cb = qtr + 4 * i;
+    const uint32_t tt = (uint32_t)(cb / G);
+    tlim[i] = cb < ncomb && tt < ntok ? p0 + tok0 + tt + 1 : 0u;
+  }
+  // chunk loads go to registers one chunk ahead and into LDS after the
+  // chunk in use is consumed
+  float4 vr[4];
+  float pr[4];
+  auto load = [&](uint32_t j0) {
+    const uint32_t jn = t_hi - j0 < (uint32_t)kPreChunk ? t_hi - j0 : (uint32_t)kPreChunk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // unconditional: indices clamped into bounds
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 5, f4 = c & 31;
+      vr[i] = ld_gf4(a.vcache + (size_t)(j0 + min(jl, jn - 1)) * kvd + g * kHd + 4 * f4);
+      const uint32_t cb = min(c / kPreChunk, (uint32_t)ncomb - 1), pl = c % kPreChunk;
+      const uint32_t tt = min(cb / G, ntok - 1);
+      pr[i] = ld_gf(a.scores + ((size_t)(tok0 + tt) * a.H + g * G + cb % G) * a.t_stride +
+                    min(j0 + pl, p0 + tok0 + tt));
+    }
+  };
+  auto store = [&](uint32_t j0) {
+    const uint32_t jn = t_hi - j0 < (uint32_t)kPreChunk ? t_hi - j0 : (uint32_t)kPreChunk;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t c = (uint32_t)(tid + 512 * i), jl = c >> 5, f4 = c & 31;
+      if (jl < jn) *(lf32x4*)(vs + jl * kHd + 4 * f4) = f32x4_t{vr[i].x, vr[i].y, vr[i].z, vr[i].w};
+      const uint32_t cb = c / kPreChunk, pl = c % kPreChunk, tt = cb / G;
+      if ((int)cb < ncomb && tt < ntok && j0 + pl < p0 + tok0 + tt + 1) ps[cb * CS + pl] = pr[i];
+    }
+  };
+  load(0);
+  store(0);
+  __syncthreads();
+  for (uint32_t j0 = 0; j0 < t_hi; j0 += kPreChunk) {
+    const uint32_t jn = t_hi - j0 < (uint32_t)kPreChunk ? t_hi - j0 : (uint32_t)kPreChunk;
+    const bool more = j0 + kPreChunk < t_hi;
+    if (more) load(j0 + kPreChunk);
+    // positions below t_lo are taken by every chain
+    const uint32_t jf = t_lo > j0 ? (t_lo - j0 < jn ? t_lo - j0 : jn) : 0u;
+    uint32_t jj = 0;
+    for (; jj + 4 <= jf; jj += 4) {
+      const float v0 = vs[jj * kHd + d], v1 = vs[(jj + 1) * kHd + d];
+      const float v2 = vs[(jj + 2) * kHd + d], v3 = vs[(jj + 3) * kHd + d];
+#pragma unroll
+      for (int i = 0; i < NC; i++) {
+        if (tlim[i]) {
+          const f32x4_t p = *(const lf32x4*)(ps + (qtr + 4 * i) * CS + jj);
+          o[i] = p.x * v0 + o[i];
+          o[i] = p.y * v1 + o[i];
+          o[i] = p.z * v2 + o[i];
+          o[i] = p.w * v3 + o[i];
+        }
+      }
+    }
+    for (; jj < jn; jj++) {
+      const uint32_t j = j0 + jj;
+      const float v = vs[jj * kHd + d];
+#pragma unroll
+      for (int i = 0; i < NC; i++)
+        if (j < tlim[i]) o[i] = ps[(qtr + 4 * i) * CS + jj] * v + o[i];
+    }
+    __syncthreads();  // the chunk is consumed
+    if (more) {
+      store(j0 + kPreChunk);
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NC; i++) {
+    if (tlim[i]) {
+      const int cb = qtr + 4 * i;
+      const uint32_t tok = tok0 + (uint32_t)(cb / G);
+      const uint32_t col = (uint32_t)(g * G + cb % G) * kHd + d;
+      ((RLH_GLOBAL float*)a.out)[(size_t)tok * qd + col] = o[i];
+      const uint32_t nbq = (uint32_t)qd / 32;
+      Q8Out ot{a.out_q8.qs + (size_t)tok * qd, a.out_q8.d + (size_t)tok * nbq, a.out_q8.s + (size_t)tok * nbq,
+               a.out_q8.s16 + (size_t)tok * nbq * 2};
+      q8_quant_block32(o[i], ot, col / 32);
+    }
+  }
+}
+
+size_t softmax_lds(uint32_t t_max) { return (size_t)((t_max + 3) & ~3u) * 4; }
 
 }  // namespace
 
-uint32_t attn_vtile(uint32_t t_max) {
-  // LDS budget ~150 KB: e[t_max] + 2 tiles x vt x 32 floats
-  uint32_t avail = 150u * 1024u - ((t_max + 3) & ~3u) * 4u;
-  uint32_t vt = 512;
-  while (vt > 32 && 2u * vt * 32u * 4u > avail) vt /= 2;
-  return vt;
-}
-
-size_t attn_out_lds(uint32_t t_max, uint32_t vtile) { return (size_t)((t_max + 3) & ~3u) * 4 + 2 * (size_t)vtile * 32 * 4; }
-
-void launch_attn_scores(hipStream_t st, const AttnArgs& a, uint32_t n_tok, bool fused) {
-  uint32_t nchunks = (a.t_max + kChunk - 1) / kChunk;
-  dim3 grid(a.KVH * nchunks, n_tok);
+void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
+  const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
+  const uint32_t G = (uint32_t)(a.H / a.KVH), TT = (uint32_t)kQkComb / G;
   if (fused)
-    hipLaunchKernelGGL(k_attn_scores<true>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_qk<true>, dim3(a.KVH * ntiles, a.n_tok), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL(k_attn_scores<false>, grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_attn_qk<false>, dim3(a.KVH * ntiles, (a.n_tok + TT - 1) / TT), dim3(256), 0, st, a);
 }
 
-void launch_attn_out(hipStream_t st, const AttnArgs& a, uint32_t n_tok) {
-  hipLaunchKernelGGL(k_attn_out, dim3(a.H, 4, n_tok), dim3(256), attn_out_lds(a.t_max, a.vtile), st, a);
+void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
+  hipLaunchKernelGGL(k_attn_softmax, dim3(a.H, a.n_tok), dim3(256), softmax_lds(a.t_max), st, a);
 }
 
-bool attn_set_max_lds(size_t bytes) {
-  return hipFuncSetAttribute((const void*)k_attn_out, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) ==
-         hipSuccess;
+size_t attn_dec_fused_lds(uint32_t t_max, uint32_t group) {
+  const size_t b = (size_t)group * dec_row_stride(t_max) * 4;
+  return b <= kDecFusedLds ? b : 0;
+}
+
+void launch_attn_decode(hipStream_t st, const AttnArgs& a) {
+  const size_t lds = attn_dec_fused_lds(a.t_max, (uint32_t)(a.H / a.KVH));
+  if (lds) {
+    hipLaunchKernelGGL(k_attn_smpv_dec, dim3(a.KVH, 4), dim3(512), lds, st, a);
+  } else {
+    launch_attn_softmax(st, a);
+    hipLaunchKernelGGL(k_attn_pv_dec, dim3(a.KVH, 4), dim3(512), 0, st, a);
+  }
+}
+
+void launch_attn_pv(hipStream_t st, const AttnArgs& a, bool decode) {
+  if (decode) {
+    hipLaunchKernelGGL(k_attn_pv_dec, dim3(a.KVH, 4), dim3(512), 0, st, a);
+  } else {
+    const uint32_t TT = (uint32_t)(kPreComb / (a.H / a.KVH));
+    hipLaunchKernelGGL(k_attn_pv_pre, dim3(a.KVH, (a.n_tok + TT - 1) / TT), dim3(512), 0, st, a);
+  }
+}
+
+bool attn_init(uint32_t max_ctx) {
+  if (max_ctx > kAttnMaxCtx) return false;
+  return hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_smpv_dec, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kDecFusedLds) == hipSuccess;
 }
 
 }  // namespace rlh

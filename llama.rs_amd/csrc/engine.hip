@@ -270,7 +270,6 @@ struct rlh_cache {
   float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *g = nullptr, *u = nullptr,
         *logits = nullptr, *scratch = nullptr;
   float* scores = nullptr;  // attention scores [H][max_ctx]
-  uint32_t vtile = 0;       // V positions per LDS tile of the attention output kernel
   Q8Buf act_e{}, act_q{}, act_f{};
   // step state (device): tok, pos, step, argmax out
   uint32_t* st_dev = nullptr;  // [0]=tok [1]=pos [2]=step [3]=argmax
@@ -322,15 +321,15 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   const float scale = 1.0f / std::sqrt((float)hd);  // model.rs:616
   uint32_t* tok = c->st_dev;
   uint32_t* pos = c->st_dev + 1;
-  // x = embedding row; Q8 of rmsnorm(x) for the first layer (model.rs:612-621)
+  // x = embedding row (model.rs:612); every rmsnorm(x) of the step runs in
+  // the prologue of the matvec that consumes it
   launch_embed(st, m->token_embd.dm, tok, 1, c->x);
-  launch_rmsnorm_q8(st, c->x, m->layers[0].attn_norm.p, E, 1, eps, c->act_e, nullptr);
   const uint32_t qd = H * hd, F = cfg.n_ff;
   for (uint32_t l = 0; l < cfg.n_layer; l++) {
     Layer& L = m->layers[l];
-    {  // q, k, v (model.rs:622-624)
+    {  // rmsnorm(x, attn_norm); q, k, v (model.rs:621-624)
       MvPlan p;
-      mv_plan_init(p, E, c->act_e);
+      mv_plan_init_norm(p, E, c->x, L.attn_norm.p, eps);
       mv_plan_add(p, L.q.dm, c->q, nullptr);
       mv_plan_add(p, L.k.dm, c->k, nullptr);
       mv_plan_add(p, L.v.dm, c->v, nullptr);
@@ -354,39 +353,37 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       a.scores = c->scores;
       a.t_stride = (uint32_t)c->max_ctx;
       a.t_max = (uint32_t)c->max_ctx;
-      a.vtile = c->vtile;
+      a.max_ctx = (uint32_t)c->max_ctx;
+      a.n_tok = 1;
       a.H = (int)H;
       a.KVH = (int)KVH;
       a.eps = eps;
       a.scale = scale;
       a.out = c->attn;
       a.out_q8 = c->act_q;
-      launch_attn_scores(st, a, 1, true);
-      launch_attn_out(st, a, 1);
+      launch_attn_scores(st, a, true);
+      launch_attn_decode(st, a);
     }
-    {  // attn_output, x += (model.rs:713-716); Q8 of rmsnorm(x, ffn_norm) (719)
+    {  // attn_output, x += (model.rs:713-716)
       MvPlan p;
       mv_plan_init(p, qd, c->act_q);
       mv_plan_add(p, L.o.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
-      launch_rmsnorm_q8(st, c->x, L.ffn_norm.p, E, 1, eps, c->act_e, nullptr);
     }
-    {  // gate, up, silu(g)*u and its Q8 blocks (model.rs:720-724)
+    {  // rmsnorm(x, ffn_norm); gate, up, silu(g)*u and its Q8 blocks (model.rs:719-724)
       MvPlan p;
-      mv_plan_init(p, E, c->act_e);
+      mv_plan_init_norm(p, E, c->x, L.ffn_norm.p, eps);
       mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
       mv_plan_finish(p);
       mv_launch(st, p);
     }
-    {  // ffn_down, x += (model.rs:725-728); Q8 of the next rmsnorm(x)
-      const float* next_norm = l + 1 < cfg.n_layer ? m->layers[l + 1].attn_norm.p : m->output_norm.p;
+    {  // ffn_down, x += (model.rs:725-728)
       MvPlan p;
       mv_plan_init(p, F, c->act_f);
       mv_plan_add(p, L.down.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
-      launch_rmsnorm_q8(st, c->x, next_norm, E, 1, eps, c->act_e, nullptr);
     }
     if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
       (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
@@ -394,7 +391,9 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   }
   if (kind == STEP_NOLOGITS) return;
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
-  {  // logits of rmsnorm(x, output_norm) (model.rs:733-737), greedy argmax fused
+  {  // logits of rmsnorm(x, output_norm) (model.rs:733-737), greedy argmax fused;
+     // the norm runs once here rather than in each of the many logits blocks
+    launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
     MvPlan p;
     mv_plan_init(p, E, c->act_e);
     mv_plan_add(p, ow.dm, c->logits, nullptr);
@@ -576,7 +575,7 @@ int rlh_model_finalize(rlh_model* m) {
       return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": ffn_gate and ffn_up must share a ggml type");
     const Q8Mut none{};
     MvPlan p;
-    mv_plan_init(p, (uint32_t)E, none);
+    mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
     mv_plan_add(p, L.q.dm, nullptr, nullptr);
     mv_plan_add(p, L.k.dm, nullptr, nullptr);
     mv_plan_add(p, L.v.dm, nullptr, nullptr);
@@ -584,7 +583,7 @@ int rlh_model_finalize(rlh_model* m) {
     mv_plan_init(p, (uint32_t)qd, none);
     mv_plan_add(p, L.o.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
-    mv_plan_init(p, (uint32_t)E, none);
+    mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
     mv_plan_add_pair(p, L.gate.dm, L.up.dm, none, nullptr);
     ok = ok && mv_plan_finish(p);
     mv_plan_init(p, (uint32_t)F, none);
@@ -681,16 +680,14 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   const rlh_config& cfg = m->cfg;
   max_ctx = std::min<uint64_t>(max_ctx, cfg.n_ctx);  // model.rs:340
   if (max_ctx == 0) return fail(RLH_EINVAL, "max_ctx is 0");
-  if (max_ctx > 32768) return fail(RLH_EUNSUP, "max_ctx above 32768 is not supported by the attention kernels");
-  if (cfg.n_head / cfg.n_head_kv > 8) return fail(RLH_EUNSUP, "more than 8 query heads per KV head");
-  uint32_t vtile = attn_vtile((uint32_t)max_ctx);
-  if (!attn_set_max_lds(attn_out_lds((uint32_t)max_ctx, vtile))) return fail(RLH_EDEVICE, "attention LDS attribute");
+  if (max_ctx > kAttnMaxCtx) return fail(RLH_EUNSUP, "max_ctx above 32768 is not supported by the attention kernels");
+  if (cfg.n_head / cfg.n_head_kv > (uint32_t)kAttnMaxGroup) return fail(RLH_EUNSUP, "more than 8 query heads per KV head");
+  if (!attn_init((uint32_t)max_ctx)) return fail(RLH_EDEVICE, "attention LDS attribute");
   rlh_cache* c = new rlh_cache();
   c->m = m;
   c->max_ctx = max_ctx;
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
   const uint32_t npv = std::max(c->nparts, mv_blocks_for(ow.ty, cfg.vocab_size, cfg.n_embd));
-  c->vtile = vtile;
   uint64_t E = cfg.n_embd, F = cfg.n_ff, qd = (uint64_t)cfg.n_head * cfg.head_dim,
            kvd = (uint64_t)cfg.n_head_kv * cfg.head_dim;
   size_t kvbytes = (size_t)cfg.n_layer * max_ctx * kvd * 4;
@@ -871,15 +868,17 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       a.scores = c->scoresb;
       a.t_stride = (uint32_t)c->max_ctx;
       a.t_max = p0 + mtok;
-      a.vtile = c->vtile;
+      a.max_ctx = (uint32_t)c->max_ctx;
+      a.n_tok = mtok;
       a.H = (int)H;
       a.KVH = (int)KVH;
       a.eps = eps;
       a.scale = scale;
       a.out = c->attnb;
       a.out_q8 = c->act_qb;
-      launch_attn_scores(st, a, mtok, false);
-      launch_attn_out(st, a, mtok);
+      launch_attn_scores(st, a, false);
+      launch_attn_softmax(st, a);
+      launch_attn_pv(st, a, false);
       launch_gemm(st, L.o.dm, c->act_qb, mtok, nullptr, c->xb);
       launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, nullptr);
       launch_gemm(st, L.gate.dm, c->act_eb, mtok, c->gb, nullptr);
@@ -1174,7 +1173,11 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   const Q8Buf& act = cols == m->cfg.n_ff ? c->act_f : (cols == qd ? c->act_q : c->act_e);
   std::vector<MvPlan> plans(mats.size());
   for (size_t i = 0; i < mats.size(); i++) {
-    mv_plan_init(plans[i], (uint32_t)cols, act);
+    // E-wide layer matrices take rmsnorm(x) in their prologue, as in decode
+    if (cols == m->cfg.n_embd && !global)
+      mv_plan_init_norm(plans[i], (uint32_t)cols, c->x, m->output_norm.p, m->cfg.rms_eps);
+    else
+      mv_plan_init(plans[i], (uint32_t)cols, act);
     mv_plan_add(plans[i], mats[i]->dm, c->logits, nullptr);
     if (!mv_plan_finish(plans[i])) return fail(RLH_EUNSUP, "matvec shape");
   }

@@ -24,8 +24,6 @@ void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, 
                             const float* bv, const float* qn, const float* kn, const float* rope_cs,
                             const uint32_t* pos0, float* kcache, float* vcache, int H, int KVH, uint32_t n_tok,
                             float eps);
-void launch_attention(hipStream_t st, const float* q, const float* kcache, const float* vcache, const uint32_t* pos0,
-                      int H, int KVH, uint32_t n_tok, uint32_t t_max, float scale, float* out, const Q8Buf& out_q8);
 void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
                       float* h_out);
 // Final reduction of per-block (max, lowest index) candidates; with `step`
@@ -34,7 +32,5 @@ void launch_argmax_final(hipStream_t st, const float* pv, const uint32_t* pi, ui
                          uint32_t* pos, uint32_t* step, uint32_t* hist);
 void launch_argmax(hipStream_t st, const float* x, uint32_t n, float* pv, uint32_t* pi, uint32_t nparts,
                    uint32_t* tok_out, uint32_t* pos, uint32_t* step, uint32_t* hist);
-// Raises the dynamic-LDS limit of the attention kernel (returns false on error).
-bool attention_set_max_lds(size_t bytes);
 
 }  // namespace rlh

@@ -208,97 +208,6 @@ __global__ void __launch_bounds__(64) k_qk_norm_rope_kv(float* q, float* k, cons
 }
 
 // ---------------------------------------------------------------------------
-// Attention for one (query token, head), exact in the reference order
-// (model.rs:692-711 / 525-543): s_j = dot_f32_avx2(q, K_j) * scale,
-// softmax_inplace (ops.rs:398-419: sequential sum of glibc expf), then the
-// saxpy chain out = (p_j * V_j) + out over j in order (simd.rs:674-691).
-// Output is also quantised to Q8 (the attn_output matvec input).
-// grid (H, n_tokens); block 256; dynamic LDS = t_max floats.
-// Token t attends positions [0, pos0 + t].
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) k_attention(const float* q, const float* kcache, const float* vcache,
-                                                   const uint32_t* pos0, int H, int KVH, float scale, float* out,
-                                                   Q8Out out_q8) {
-  constexpr int hd = 128;
-  extern __shared__ float scores[];
-  __shared__ float qv[hd];
-  __shared__ float red[256];
-  __shared__ float s_inv;
-  __shared__ int s_scale_on;
-  int h = blockIdx.x, tok = blockIdx.y;
-  int group = H / KVH;
-  if (group < 1) group = 1;
-  int kvh = h / group;
-  const int qd = H * hd, kvd = KVH * hd;
-  uint32_t t = pos0[0] + (uint32_t)tok + 1;
-  const float* qh = q + (size_t)tok * qd + h * hd;
-  if (threadIdx.x < hd) qv[threadIdx.x] = qh[threadIdx.x];
-  __syncthreads();
-  // scores: one position per thread, the full 32-slot FMA tree in registers.
-  for (uint32_t j = threadIdx.x; j < t; j += 256) {
-    const float4* kr = (const float4*)(kcache + (size_t)j * kvd + kvh * hd);
-    float acc[32];
-#pragma unroll
-    for (int s = 0; s < 32; s++) acc[s] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int s4 = 0; s4 < 8; s4++) {
-        float4 kk = kr[i * 8 + s4];
-        int s = s4 * 4;
-        acc[s] = __builtin_fmaf(qv[i * 32 + s], kk.x, acc[s]);
-        acc[s + 1] = __builtin_fmaf(qv[i * 32 + s + 1], kk.y, acc[s + 1]);
-        acc[s + 2] = __builtin_fmaf(qv[i * 32 + s + 2], kk.z, acc[s + 2]);
-        acc[s + 3] = __builtin_fmaf(qv[i * 32 + s + 3], kk.w, acc[s + 3]);
-      }
-    }
-    float A[8];
-#pragma unroll
-    for (int l = 0; l < 8; l++) A[l] = (acc[l] + acc[8 + l]) + (acc[16 + l] + acc[24 + l]);
-    float dot = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
-    scores[j] = dot * scale;
-  }
-  __syncthreads();
-  // max (order-independent)
-  float mx = -__int_as_float(0x7f800000);
-  for (uint32_t j = threadIdx.x; j < t; j += 256) mx = fmaxf(mx, scores[j]);
-  red[threadIdx.x] = mx;
-  __syncthreads();
-  for (int st = 128; st > 0; st >>= 1) {
-    if ((int)threadIdx.x < st) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + st]);
-    __syncthreads();
-  }
-  mx = red[0];
-  for (uint32_t j = threadIdx.x; j < t; j += 256) scores[j] = expf_glibc(scores[j] - mx);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float sum = 0.0f;
-    for (uint32_t j = 0; j < t; j++) sum = sum + scores[j];
-    s_scale_on = sum > 0.0f;
-    s_inv = 1.0f / sum;
-  }
-  __syncthreads();
-  if (s_scale_on) {
-    float inv = s_inv;
-    for (uint32_t j = threadIdx.x; j < t; j += 256) scores[j] = scores[j] * inv;
-    __syncthreads();
-  }
-  // saxpy chain: threads 0..127 own one output dimension each.
-  float o = 0.0f;
-  if (threadIdx.x < hd) {
-    const float* vb = vcache + kvh * hd + threadIdx.x;
-    for (uint32_t j = 0; j < t; j++) o = scores[j] * vb[(size_t)j * kvd] + o;
-    out[(size_t)tok * qd + h * hd + threadIdx.x] = o;
-  }
-  if (threadIdx.x < hd) {
-    uint32_t nbq = (uint32_t)qd / 32;
-    Q8Out ot{out_q8.qs + (size_t)tok * qd, out_q8.d + (size_t)tok * nbq, out_q8.s + (size_t)tok * nbq,
-             out_q8.s16 + (size_t)tok * nbq * 2};
-    q8_quant_block32(o, ot, (uint32_t)(h * hd + threadIdx.x) / 32);
-  }
-}
-
-// ---------------------------------------------------------------------------
 // SwiGLU + Q8: h = silu(g) * u, silu(x) = x / (1 + expf(-x)) (ops.rs:393-395,
 // model.rs:722-724, 565-567), then quantize_q8 of h (ffn_down input).
 // grid covers n_total = n_tokens * F elements, 256 per block.
@@ -443,13 +352,6 @@ void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, 
                      pos0, kcache, vcache, H, KVH, eps);
 }
 
-void launch_attention(hipStream_t st, const float* q, const float* kcache, const float* vcache, const uint32_t* pos0,
-                      int H, int KVH, uint32_t n_tok, uint32_t t_max, float scale, float* out, const Q8Buf& out_q8) {
-  size_t lds = (size_t)t_max * sizeof(float);
-  hipLaunchKernelGGL(k_attention, dim3(H, n_tok), dim3(256), lds, st, q, kcache, vcache, pos0, H, KVH, scale, out,
-                     q8out(out_q8));
-}
-
 void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
                       float* h_out) {
   hipLaunchKernelGGL(k_swiglu_q8, dim3((n_total + 255) / 256), dim3(256), 0, st, g, u, n_total, q8out(out), h_out);
@@ -468,9 +370,3 @@ void launch_argmax(hipStream_t st, const float* x, uint32_t n, float* pv, uint32
 
 }  // namespace rlh
 
-namespace rlh {
-bool attention_set_max_lds(size_t bytes) {
-  return hipFuncSetAttribute((const void*)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) ==
-         hipSuccess;
-}
-}  // namespace rlh

@@ -40,6 +40,12 @@ struct MvLaunch {
   uint32_t cols;
   uint32_t rows_per_blk;  // R: rows of one block (all segments)
   Q8Ptr act;              // Q8 activation row in HBM, staged into LDS by each block
+  // norm input (nx set): the activation is quantize_q8(rmsnorm(nx, nw)) of
+  // the f32 row nx (simd.rs:282-326, 116-203), computed by every block in
+  // its prologue while its first weights are in flight; act is unused
+  const float* nx;
+  const float* nw;
+  float eps;
   uint32_t region_off;    // byte offset of the term tiles in LDS
   uint32_t tile_stride;   // floats per term-tile row
   uint32_t has_argmax;
@@ -54,6 +60,7 @@ struct MvPlan {
   uint32_t waves = 0;  // waves per block
   uint32_t max_terms = 0;
   uint32_t rows = 0;   // rows over all segments
+  bool norm = false;   // activation from the norm prologue
 };
 
 // Terms (float summands of the reference's per-row chain) per 256-value
@@ -68,6 +75,10 @@ __host__ __device__ inline uint32_t mv_terms_per_sb(uint32_t ty) {
 // exactly one segment. mv_plan_finish fixes the block shape (returns false
 // when no shape fits the LDS).
 void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act);
+// Same, with the activation computed in the kernel from the f32 row x and
+// the rmsnorm weight w (cols <= kMvMaxNormCols).
+void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w, float eps);
+constexpr uint32_t kMvMaxNormCols = 7168;
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
 void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h);
 void mv_plan_argmax(MvPlan& p, const MvArgmax& am);

@@ -295,6 +295,57 @@ __device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& 
   __syncthreads();
 }
 
+// Norm input: every block computes quantize_q8(rmsnorm(x, w)) itself
+// (k_rmsnorm_q8's arithmetic): the row and the weights go to registers in
+// one batch of loads, the row to LDS (`xs`, free until the terms are
+// written) for the 32 FMA chains of the sum of squares, and each group of 8
+// threads quantizes one 32-value block straight into the LDS activation.
+// Needs blockDim.x >= 256 (at most kV float4 per thread).
+__device__ __forceinline__ void stage_norm(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* misc) {
+  constexpr int kV = kMvMaxNormCols / 4 / 256;
+  const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
+  // unconditional loads (index clamped into the row): a load under a branch
+  // gets a wait for every load before it
+  float4 xr[kV], wr[kV];
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const uint32_t i = min(tid + NT * k, n4 - 1);
+    xr[k] = ld_gf4(L.nx + 4 * i);
+    wr[k] = ld_gf4(L.nw + 4 * i);
+  }
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const uint32_t i = tid + NT * k;
+    if (i < n4) *(lf32x4*)(xs + 4 * i) = f32x4_t{xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const float ss = rms_sumsq_lds(xs, (int)L.cols);
+    if (tid == 0) misc[0] = 1.0f / sqrtf(ss / (float)L.cols + L.eps);
+  }
+  __syncthreads();
+  const float s = misc[0];
+#pragma unroll
+  for (int k = 0; k < kV; k++) {
+    const uint32_t i = tid + NT * k;
+    if (i < n4) {  // n4 and NT are multiples of 8: whole 8-lane groups
+      const float v0 = (xr[k].x * s) * wr[k].x, v1 = (xr[k].y * s) * wr[k].y;
+      const float v2 = (xr[k].z * s) * wr[k].z, v3 = (xr[k].w * s) * wr[k].w;
+      const Q8Blk8x4 r = q8_block8x4(v0, v1, v2, v3);
+      const uint32_t blk = i / 8, l = i & 7;
+      *(RLH_LDS uint32_t*)(la.qs + (blk >> 3) * kSbStride + (blk & 7) * 32 + 4 * l) = r.packed;
+      if (l == 0) {
+        la.d[blk] = r.d;
+        la.s[blk] = r.tot;
+        la.s16x32[2 * blk] = 32.0f * (float)r.s;
+      } else if (l == 4) {
+        la.s16x32[2 * blk + 1] = 32.0f * (float)r.s;
+      }
+    }
+  }
+  __syncthreads();
+}
+
 __device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
   if (v > bv || (v == bv && i < bi)) {
     bv = v;
@@ -314,7 +365,8 @@ __device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
 // The body of one block for weight type TY; NM = 2 in PAIR mode (gate and
 // up share type and tiling).
 template <uint32_t TY, int NM>
-__device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc) {
+__device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc,
+                                         const lu64* exp_tab) {
   using I = MI<TY>;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
@@ -333,24 +385,44 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   la.s16x32 = (RLH_LDS float*)(la.s + nb);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
 
-  // first tile: its weights are in flight while the activation is staged
-  typename I::W wr[NM];
-  uint32_t t = wave;
-  if (t < ntiles) {
+  // two tiles per wave in flight: the next tile's weights load while the
+  // current tile's terms are computed; the first tile's weights are in
+  // flight while the activation is staged
+  auto load = [&](typename I::W* w, uint32_t t) {
     const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
-    I::load(wr[0], g.w.a + off, lane);
-    if (NM == 2) I::load(wr[NM - 1], g.w2.a + off, lane);
-  }
-  stage_activation(L, la);
-  while (t < ntiles) {
+    I::load(w[0], g.w.a + off, lane);
+    if (NM == 2) I::load(w[NM - 1], g.w2.a + off, lane);
+  };
+  auto terms = [&](const typename I::W* w, uint32_t t) {
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
-    I::terms(wr[0], la, j, region + rl * stride + j * I::kT);
-    if (NM == 2) I::terms(wr[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
-    t += nwaves;
-    if (t < ntiles) {
-      const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
-      I::load(wr[0], g.w.a + off, lane);
-      if (NM == 2) I::load(wr[NM - 1], g.w2.a + off, lane);
+    I::terms(w[0], la, j, region + rl * stride + j * I::kT);
+    if (NM == 2) I::terms(w[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
+  };
+  // ping-pong over two register sets, except for PAIR launches of the
+  // larger item types, whose second set would not fit the register budget
+  constexpr bool kPP = NM == 1 || sizeof(typename I::W) <= 9 * 16;
+  // the residual of the chain lane's row, read now so that the epilogue
+  // does not wait for it
+  float rsd = 0.0f;
+  if (NM == 1 && g.resid && wave == 0) rsd = ld_gf(g.resid + row0 + min(lane, nrows - 1));
+  typename I::W wa[NM], wb[kPP ? NM : 1];
+  uint32_t t = wave;
+  if (t < ntiles) load(wa, t);
+  if (L.nx) stage_norm(L, la, region, misc);
+  else stage_activation(L, la);
+  if (kPP) {
+    for (; t < ntiles; t += 2 * nwaves) {
+      const uint32_t t2 = t + nwaves;
+      if (t2 < ntiles) load(wb, t2);
+      terms(wa, t);
+      if (t2 >= ntiles) break;
+      if (t2 + nwaves < ntiles) load(wa, t2 + nwaves);
+      terms(wb, t2);
+    }
+  } else {
+    for (; t < ntiles; t += nwaves) {
+      terms(wa, t);
+      if (t + nwaves < ntiles) load(wa, t + nwaves);
     }
   }
   __syncthreads();
@@ -367,7 +439,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     // h = silu(gate) * up for the block's rows (R is a multiple of 32 and
     // divides the rows, so the lanes form whole Q8 blocks)
     const float x = acc, up = misc[4 + lane];
-    const float h = (x / (1.0f + expf_glibc(-x))) * up;  // ops.rs:393-395
+    const float h = (x / (1.0f + expf_glibc_t(-x, exp_tab))) * up;  // ops.rs:393-395
     if (lane < nrows) {
       if (g.y) ((RLH_GLOBAL float*)g.y)[row0 + lane] = h;
       q8_quant_block32(h, g.hq, (row0 + lane) / 32);
@@ -378,10 +450,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   const bool mine = wave == 0 && lane < nrows;
   const uint32_t row = row0 + lane;
   if (mine) {
-    if (g.resid) {
-      RLH_GLOBAL float* x = (RLH_GLOBAL float*)g.resid;
-      x[row] = x[row] + acc;
-    }
+    if (g.resid) ((RLH_GLOBAL float*)g.resid)[row] = rsd + acc;
     if (g.y) ((RLH_GLOBAL float*)g.y)[row] = acc;
   }
   if (wave != 0 || !L.has_argmax) return;
@@ -396,24 +465,46 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   }
 }
 
-template <int NM, int MAXT>
-__global__ void __launch_bounds__(MAXT) k_mv(MvLaunch L) {
+// TY = the weight type of every segment, or 0 for launches that mix types
+// (a switch per block); one instantiation per type keeps each kernel's
+// register allocation to what its own item type needs.
+template <uint32_t TY, int NM>
+__global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   __shared__ float misc_generic[4 + 64];
+  __shared__ uint64_t tab_g[NM == 2 ? 32 : 1];
   lfloat* lds = (lfloat*)lds_generic;
   lfloat* misc = (lfloat*)misc_generic;
+  if (NM == 2) exp_tab_to_lds((lu64*)tab_g);  // silu's expf table (read after the prologue's barriers)
   // segment of this block, selected without indexing the argument array
   // (a dynamic index would copy the kernel argument to private memory)
   MvSeg g = L.seg[0];
   if (L.nseg > 1 && blockIdx.x >= L.seg[1].blk_begin) g = L.seg[1];
   if (L.nseg > 2 && blockIdx.x >= L.seg[2].blk_begin) g = L.seg[2];
   const uint32_t blk = blockIdx.x - g.blk_begin;
-  switch (g.w.ty) {
-    case RLH_TYPE_Q4_K: mv_block<RLH_TYPE_Q4_K, NM>(L, g, blk, lds, misc); break;
-    case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM>(L, g, blk, lds, misc); break;
-    case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc); break;
-    case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc); break;
-    default: break;
+  if constexpr (TY != 0) {
+    mv_block<TY, NM>(L, g, blk, lds, misc, (lu64*)tab_g);
+  } else {
+    switch (g.w.ty) {
+      case RLH_TYPE_Q4_K: mv_block<RLH_TYPE_Q4_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      default: break;
+    }
+  }
+}
+
+typedef void (*MvKernel)(MvLaunch);
+
+template <int NM>
+MvKernel mv_kernel(uint32_t ty) {
+  switch (ty) {
+    case RLH_TYPE_Q4_K: return k_mv<RLH_TYPE_Q4_K, NM>;
+    case RLH_TYPE_Q6_K: return k_mv<RLH_TYPE_Q6_K, NM>;
+    case RLH_TYPE_Q8_0: return k_mv<RLH_TYPE_Q8_0, NM>;
+    case RLH_TYPE_Q4_0: return k_mv<RLH_TYPE_Q4_0, NM>;
+    default: return k_mv<0, NM>;
   }
 }
 
@@ -426,7 +517,7 @@ uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   const uint32_t act = (nsb * kSbStride + nb * 16 + 15) & ~15u;
   const uint32_t stride = nsb * p.max_terms + 4;
   const uint32_t tile = nm * R * stride * 4;
-  return act + tile;
+  return act + std::max(tile, p.norm ? cols * 4 : 0u);
 }
 
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
@@ -441,6 +532,15 @@ void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act) {
   p = MvPlan{};
   p.L.cols = cols;
   p.L.act = Q8Ptr{act.qs, act.d, act.s, act.s16};
+}
+
+void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w, float eps) {
+  p = MvPlan{};
+  p.L.cols = cols;
+  p.L.nx = x ? x : w;  // a plan made only for its shape may pass null rows
+  p.L.nw = w;
+  p.L.eps = eps;
+  p.norm = true;
 }
 
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
@@ -486,12 +586,16 @@ bool mv_plan_finish(MvPlan& p) {
     return false;
   const uint32_t R = nm == 2 ? std::max<uint32_t>(tr, 32) : tr;
   if (plan_lds(p, R, nm) > kMaxLds) return false;
+  if (p.norm && (p.L.cols > kMvMaxNormCols || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
   p.L.tile_stride = nsb * p.max_terms + 4;
   const uint32_t act = nsb * kSbStride + (p.L.cols / 32) * 16;
   p.L.region_off = (act + 15) & ~15u;
   p.lds = plan_lds(p, R, nm);
-  p.waves = std::max<uint32_t>(nm, std::min<uint32_t>(16, (R / tr) * ntj));
+  // two tiles per wave (the load/compute ping-pong); the norm prologue
+  // needs at least 4 waves
+  const uint32_t ntiles = (R / tr) * ntj;
+  p.waves = std::max<uint32_t>(std::max<uint32_t>(nm, p.norm ? 4u : 1u), std::min<uint32_t>(8, (ntiles + 1) / 2));
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;
@@ -518,21 +622,20 @@ uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
 
 void mv_launch(hipStream_t st, const MvPlan& p) {
   const bool pair = p.L.nseg == 1 && p.L.seg[0].pair;
-  const dim3 grid(p.blocks), blk(64 * p.waves);
-  if (pair) {
-    if (p.waves <= 8) hipLaunchKernelGGL((k_mv<2, 512>), grid, blk, p.lds, st, p.L);
-    else hipLaunchKernelGGL((k_mv<2, 1024>), grid, blk, p.lds, st, p.L);
-  } else {
-    if (p.waves <= 8) hipLaunchKernelGGL((k_mv<1, 512>), grid, blk, p.lds, st, p.L);
-    else hipLaunchKernelGGL((k_mv<1, 1024>), grid, blk, p.lds, st, p.L);
-  }
+  uint32_t ty = p.L.seg[0].w.ty;
+  for (uint32_t s = 1; s < p.L.nseg; s++)
+    if (p.L.seg[s].w.ty != ty) ty = 0;
+  const MvKernel k = pair ? mv_kernel<2>(ty) : mv_kernel<1>(ty);
+  hipLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, p.L);
 }
 
 bool mv_set_max_lds(size_t bytes) {
-  const void* fns[] = {(const void*)k_mv<1, 512>, (const void*)k_mv<1, 1024>, (const void*)k_mv<2, 512>,
-                       (const void*)k_mv<2, 1024>};
-  for (const void* f : fns)
-    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) return false;
+  const uint32_t tys[] = {0, RLH_TYPE_Q4_K, RLH_TYPE_Q6_K, RLH_TYPE_Q8_0, RLH_TYPE_Q4_0};
+  for (uint32_t ty : tys) {
+    const void* fns[] = {(const void*)mv_kernel<1>(ty), (const void*)mv_kernel<2>(ty)};
+    for (const void* f : fns)
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) return false;
+  }
   return true;
 }
 

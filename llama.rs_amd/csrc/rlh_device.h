@@ -44,7 +44,11 @@ __device__ __constant__ static const uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
 
-__device__ __forceinline__ float expf_glibc(float x) {
+// tab: the 32 entries of kExp2Tab, read through `tab[i]` (the constant
+// table itself, or a copy in LDS where many lanes look entries up at once:
+// a divergent lookup in the constant table is a global memory round trip).
+template <class Tab>
+__device__ __forceinline__ float expf_glibc_t(float x, Tab tab) {
   const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double kShift = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -63,7 +67,7 @@ __device__ __forceinline__ float expf_glibc(float x) {
   uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= kShift;
   double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = kExp2Tab[ki % 32] + (ki << 47);
+  uint64_t t = tab[ki % 32] + (ki << 47);
   double s = __longlong_as_double((long long)t);
   double z = __builtin_fma(C0, r, C1);
   double r2 = r * r;
@@ -71,6 +75,15 @@ __device__ __forceinline__ float expf_glibc(float x) {
   y = __builtin_fma(z, r2, y);
   y = y * s;
   return (float)y;
+}
+
+__device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
+
+// LDS copy of kExp2Tab: every thread of the block calls it; visible to the
+// block after the next barrier.
+typedef RLH_LDS uint64_t lu64;
+__device__ __forceinline__ void exp_tab_to_lds(lu64* tab) {
+  if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
@@ -165,8 +178,13 @@ constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141;
 // multiple of 8 and all 8 lanes are active). Same arithmetic as
 // q8_quant_block32; amax is order-free and the sums are exact integers, so
 // the DPP reduction order does not matter. Stores 4 packed bytes per lane.
-__device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, float v3, Q8Out o, uint32_t blk) {
-  const int l = threadIdx.x & 7;
+struct Q8Blk8x4 {
+  uint32_t packed;  // this lane's 4 quants
+  float d;          // block scale
+  int tot;          // sum of the 32 quants
+  int s;            // sum of this lane's 16-value half
+};
+__device__ __forceinline__ Q8Blk8x4 q8_block8x4(float v0, float v1, float v2, float v3) {
   const float a0 = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
   float a = fmaxf(a0, dpp_f<kDppXor1>(a0));
   a = fmaxf(a, dpp_f<kDppXor2>(a));
@@ -180,16 +198,25 @@ __device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, 
   int s = q0 + q1 + q2 + q3;
   s = s + dpp_i<kDppXor1>(s);
   s = s + dpp_i<kDppXor2>(s);  // sum of the 16-value half (lanes 0-3 / 4-7)
-  const int tot = s + dpp_i<kDppHalfMirror>(s);
-  const uint32_t packed =
+  Q8Blk8x4 r;
+  r.tot = s + dpp_i<kDppHalfMirror>(s);
+  r.s = s;
+  r.d = d;
+  r.packed =
       (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) | ((uint32_t)q3 << 24);
-  *(RLH_GLOBAL uint32_t*)(o.qs + (size_t)blk * 32 + 4 * l) = packed;
+  return r;
+}
+
+__device__ __forceinline__ void q8_quant_block8x4(float v0, float v1, float v2, float v3, Q8Out o, uint32_t blk) {
+  const int l = threadIdx.x & 7;
+  const Q8Blk8x4 r = q8_block8x4(v0, v1, v2, v3);
+  *(RLH_GLOBAL uint32_t*)(o.qs + (size_t)blk * 32 + 4 * l) = r.packed;
   if (l == 0) {
-    ((RLH_GLOBAL float*)o.d)[blk] = d;
-    ((RLH_GLOBAL int32_t*)o.s)[blk] = tot;
-    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2] = s;
+    ((RLH_GLOBAL float*)o.d)[blk] = r.d;
+    ((RLH_GLOBAL int32_t*)o.s)[blk] = r.tot;
+    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2] = r.s;
   } else if (l == 4) {
-    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2 + 1] = s;
+    ((RLH_GLOBAL int32_t*)o.s16)[(size_t)blk * 2 + 1] = r.s;
   }
 }
 

@@ -120,6 +120,8 @@ SPECS = {
     "tiny-q8_0": ModelSpec("tiny-q8_0", 2, 256, 512, 4, 2, 1000, True, _all(Q8_0), n_ctx=512),
     "tiny-q4_0": ModelSpec("tiny-q4_0", 2, 256, 512, 4, 4, 1000, True, _all(Q4_0), n_ctx=512),
     "small-q4km": ModelSpec("small-q4km", 4, 1024, 3072, 16, 8, 4096, False, _q4km(False, Q4_K, Q6_K), n_ctx=1024),
+    # 8 query heads per KV head (the 32B grouping) and a long context window
+    "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
 }
 
 

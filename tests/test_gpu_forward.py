@@ -79,6 +79,30 @@ def test_prefill_and_decode_bit_exact(name):
     oc.close()
 
 
+@pytest.mark.parametrize("max_ctx", [64, 6000])
+def test_decode_attention_paths(max_ctx):
+    """Decode attention with 8 query heads per KV head: a short cache takes
+    the fused softmax + V kernel, a 6000-position cache (score rows beyond
+    its LDS) the separate softmax and V kernels. Logits bit-exact."""
+    print(f"decode attention max_ctx {max_ctx}", flush=True)
+    spec, tensors, m, om = _get("tiny-g8-q4km")
+    prompt = rlh.synth_tokens(77, 40, spec.vocab)
+    c = m.new_cache(max_ctx)
+    oc = om.new_cache(max_ctx)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg), bits(rg))
+    lib = oracle.load()
+    tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    for i in range(6):
+        lg = c.forward_into(np.array([tok], np.uint32), len(prompt) + i)
+        rg = oc.forward_into(np.array([tok], np.uint32), len(prompt) + i, oracle.MODE_DEFAULT)
+        assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ (rel {rel_l2(lg, rg):.2e})"
+        tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    c.close()
+    oc.close()
+
+
 @pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
 def test_generate_greedy_matches_cpu_tokens(name):
     spec, tensors, m, om = _get(name)
