@@ -54,6 +54,39 @@ def cpu_baseline(spec, tensors, prompt, n_decode, threads):
     return res, toks
 
 
+def measured_traffic(config):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", f"k_mv_pair_{config}_pmc.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def calibration_copy(mb):
+    """A device-to-device copy of `mb` MiB (the runtime's copy kernel): the
+    known-size reference for scaling the HBM byte counters."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = mb << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(a), ctypes.c_size_t(n)) or hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(n)):
+        raise RuntimeError("hipMalloc for the calibration copy failed")
+    for _ in range(3):
+        if hip.hipMemcpy(b, a, ctypes.c_size_t(n), 3):  # hipMemcpyDeviceToDevice
+            raise RuntimeError("calibration copy failed")
+    hip.hipDeviceSynchronize()
+    hip.hipFree(a)
+    hip.hipFree(b)
+    log(f"calibration copy: 3 x {mb} MiB device to device")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -64,6 +97,8 @@ def main():
     ap.add_argument("--seed", type=int, default=20260)
     ap.add_argument("--cpu-decode", type=int, default=6, help="CPU baseline decode tokens (0 = skip)")
     ap.add_argument("--cpu-prompt", type=int, default=8, help="CPU baseline prompt tokens")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="also run a device-to-device copy of this many MiB (counter calibration under rocprofv3)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -114,12 +149,17 @@ def main():
     step_bytes = wbytes + kv_read_bytes(spec, t_avg) + kvw
     hbm_frac_decode = step_bytes * tok_s / (HBM_PEAK_GBS * 1e9)
 
-    # dominant kernel: the Q4_K decode matvec on ffn_gate (rotating layers)
-    gate_rows, gate_cols = spec.n_ff, spec.n_embd
-    gate_ty = spec.types[rlh.T_FFN_GATE]
-    mv_bytes = gate_rows * rlh.row_bytes(gate_ty, gate_cols) + gate_cols + gate_cols // 32 * 16
+    # dominant decode kernel: the fused rmsnorm + ffn_gate/ffn_up + silu*up
+    # launch (k_mv<TY, 2>), timed per launch with HIP events on the cache's
+    # stream, rotating over the layers' weights
+    E, F = spec.n_embd, spec.n_ff
+    ff_ty = spec.types[rlh.T_FFN_GATE]
+    pair_bytes = (2 * F * rlh.row_bytes(ff_ty, E)  # gate + up weights
+                  + 2 * E * 4                       # residual row and ffn_norm weights
+                  + F * 4 + F + (F // 32) * 16)     # h (f32) and its Q8 blocks
     mv_us = cache.profile_matvec(rlh.T_FFN_GATE, 4 * spec.n_layer)
-    mv_gbs = mv_bytes / (mv_us * 1e-6) / 1e9
+    mv_gbs = pair_bytes / (mv_us * 1e-6) / 1e9
+    traffic = measured_traffic(args.config)
 
     out = {
         "metric": "decode tok/s (Qwen3-8B Q4_K_M, 1 GPU); prefill tok/s and % HBM roofline reported alongside",
@@ -143,11 +183,12 @@ def main():
         "decode_hbm_bytes_per_token": int(step_bytes),
         "decode_hbm_frac": round(hbm_frac_decode, 4),
         "prefill_int8_frac": round(spec.int8_ops_per_token() * args.prompt / prefill_s / (INT8_PEAK_TOPS * 1e12), 5),
-        "roofline": {"bound": "hbm", "kernel": f"k_matvec<Q{'4_K' if gate_ty == rlh.Q4_K else gate_ty}> ffn_gate "
-                                               f"{gate_rows}x{gate_cols}",
+        "roofline": {"bound": "hbm",
+                     "kernel": f"k_mv<{rlh.TYPE_NAMES.get(ff_ty, ff_ty)}, pair>: rmsnorm + ffn_gate/ffn_up "
+                               f"2x{F}x{E} + silu*up",
                      "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(mv_us, 3), "bytes_per_launch": int(mv_bytes)},
+                     "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "avg_launch_us": round(mv_us, 3), "bytes_per_launch": int(pair_bytes)},
         "greedy_tokens_head": [int(t) for t in toks[:8]],
     }
 
@@ -164,6 +205,8 @@ def main():
 
     cache.close()
     model.close()
+    if args.calib_copy_mb > 0:
+        calibration_copy(args.calib_copy_mb)
     print(json.dumps(out), flush=True)
 
 

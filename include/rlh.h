@@ -179,11 +179,15 @@ int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t 
 int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
 
 /* ---- measurement ---------------------------------------------------------------------
- * Runs the decode matvec of one weight kind `iters` times back to back on the
- * cache's stream, rotating over the layers' copies of that matrix (so weights
- * stream from HBM as in a decode step), and reports the average time per
- * launch in microseconds from one HIP event pair around all launches on that
- * stream (launch-to-launch gaps included, as inside a captured step). */
+ * Runs the decode launch of one weight kind `iters` times on the cache's
+ * stream, rotating over the layers' copies (so weights stream from HBM as in
+ * a decode step), and reports the average time per launch in microseconds
+ * from one HIP event pair around the back-to-back launches (each launch's
+ * dispatch gap included, as inside a captured step). The launch is built as the
+ * decode step builds it: RLH_T_ATTN_Q = the fused rmsnorm + q/k/v launch,
+ * RLH_T_FFN_GATE / RLH_T_FFN_UP = the fused rmsnorm + gate/up + silu*up
+ * launch, other kinds = that matrix alone. No reference counterpart
+ * (measurement hook for the bench). */
 int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us);
 /* Average duration of one captured decode step (graph launch) over `iters`
  * steps at the cache's current length, in microseconds; the cache position

@@ -1155,47 +1155,70 @@ static const DevTensor* find_matrix(rlh_model* m, int kind, int layer) {
 int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us) {
   int rc = check_forward_args(m, c);
   if (rc) return rc;
-  if (!avg_us || iters <= 0) return fail(RLH_EINVAL, "bad argument");
-  // Rotate over every layer's copy of the matrix so that, as in a decode
-  // step, each launch streams its weights from HBM rather than from the
-  // 256 MB last-level cache a single re-launched matrix would sit in.
-  std::vector<const DevTensor*> mats;
-  bool global = kind == RLH_T_OUTPUT || kind == RLH_T_TOKEN_EMBD;
-  for (uint32_t l = 0; l < (global ? 1u : m->cfg.n_layer); l++) {
-    const DevTensor* t = find_matrix(m, kind, (int)l);
-    if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
-    mats.push_back(t);
+  if (!avg_us || iters <= 0 || iters > 4096) return fail(RLH_EINVAL, "bad argument");
+  const rlh_config& cfg = m->cfg;
+  const bool global = kind == RLH_T_OUTPUT || kind == RLH_T_TOKEN_EMBD;
+  const bool pair = kind == RLH_T_FFN_GATE || kind == RLH_T_FFN_UP;
+  const bool qkv = kind == RLH_T_ATTN_Q;
+  // One plan per layer, built as the decode step builds that launch, so the
+  // launches rotate over every layer's weights and stream them from HBM
+  // rather than from the 256 MB last-level cache a re-launched matrix would
+  // sit in.
+  std::vector<MvPlan> plans;
+  const uint64_t qd = (uint64_t)cfg.n_head * cfg.head_dim;
+  for (uint32_t l = 0; l < (global ? 1u : cfg.n_layer); l++) {
+    MvPlan p;
+    if (global) {
+      const DevTensor* t = find_matrix(m, kind, 0);
+      if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
+      mv_plan_init(p, (uint32_t)t->cols, c->act_e);
+      mv_plan_add(p, t->dm, c->logits, nullptr);
+    } else {
+      const Layer& L = m->layers[l];
+      if (pair) {
+        mv_plan_init_norm(p, cfg.n_embd, c->x, L.ffn_norm.p, cfg.rms_eps);
+        mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
+      } else if (qkv) {
+        mv_plan_init_norm(p, cfg.n_embd, c->x, L.attn_norm.p, cfg.rms_eps);
+        mv_plan_add(p, L.q.dm, c->q, nullptr);
+        mv_plan_add(p, L.k.dm, c->k, nullptr);
+        mv_plan_add(p, L.v.dm, c->v, nullptr);
+      } else {
+        const DevTensor* t = find_matrix(m, kind, (int)l);
+        if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
+        const uint64_t cols = t->cols;
+        if (cols == cfg.n_embd)
+          mv_plan_init_norm(p, (uint32_t)cols, c->x, L.attn_norm.p, cfg.rms_eps);
+        else if (cols == qd)
+          mv_plan_init(p, (uint32_t)cols, c->act_q);
+        else if (cols == cfg.n_ff)
+          mv_plan_init(p, (uint32_t)cols, c->act_f);
+        else
+          return fail(RLH_EINVAL, "matrix width matches no activation buffer");
+        mv_plan_add(p, t->dm, c->logits, nullptr);
+      }
+    }
+    if (!mv_plan_finish(p)) return fail(RLH_EUNSUP, "matvec shape");
+    plans.push_back(p);
   }
-  uint64_t qd = (uint64_t)m->cfg.n_head * m->cfg.head_dim;
-  uint64_t cols = mats[0]->cols;
-  if (cols != m->cfg.n_embd && cols != m->cfg.n_ff && cols != qd)
-    return fail(RLH_EINVAL, "matrix width matches no activation buffer");
-  const Q8Buf& act = cols == m->cfg.n_ff ? c->act_f : (cols == qd ? c->act_q : c->act_e);
-  std::vector<MvPlan> plans(mats.size());
-  for (size_t i = 0; i < mats.size(); i++) {
-    // E-wide layer matrices take rmsnorm(x) in their prologue, as in decode
-    if (cols == m->cfg.n_embd && !global)
-      mv_plan_init_norm(plans[i], (uint32_t)cols, c->x, m->output_norm.p, m->cfg.rms_eps);
-    else
-      mv_plan_init(plans[i], (uint32_t)cols, act);
-    mv_plan_add(plans[i], mats[i]->dm, c->logits, nullptr);
-    if (!mv_plan_finish(plans[i])) return fail(RLH_EUNSUP, "matvec shape");
-  }
-  // back-to-back launches between one event pair, as in a captured decode
-  // step; the average therefore includes the launch-to-launch gap
+  // back-to-back launches between one event pair on the cache's stream, as
+  // the kernels follow each other inside a captured step (an event pair
+  // around each launch would add the events' own cost to every launch)
   hipEvent_t e0, e1;
   HIPCHK(hipEventCreate(&e0));
   HIPCHK(hipEventCreate(&e1));
   mv_launch(c->st, plans[0]);  // warm-up
-  HIPCHK(hipEventRecord(e0, c->st));
+  (void)hipEventRecord(e0, c->st);
   for (int i = 0; i < iters; i++) mv_launch(c->st, plans[i % plans.size()]);
-  HIPCHK(hipEventRecord(e1, c->st));
-  HIPCHK(hipEventSynchronize(e1));
+  (void)hipEventRecord(e1, c->st);
+  hipError_t e = hipEventSynchronize(e1);
   float ms = 0.f;
-  HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
-  *avg_us = (double)ms * 1000.0 / iters;
+  if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("profile events: ") + hipGetErrorString(e));
+  const double total_ms = ms;
+  *avg_us = total_ms * 1000.0 / iters;
   return RLH_OK;
 }
 
