@@ -148,6 +148,37 @@ int rlh_greedy_next(rlh_model* m, rlh_cache* c, uint32_t* token);
  * with RLH_ECTX when the cache is full. */
 int rlh_generate_greedy(rlh_model* m, rlh_cache* c, uint32_t first, uint64_t n_steps, uint32_t* out_tokens);
 
+/* ---- sampling (src/sampler.rs, src/model.rs:741-776) ----------------------------- */
+/* SamplingParams (sampler.rs:3-26); defaults there: 0.7, 40, 0.95, 1.1, 64,
+ * 0x123456789abcdef0. */
+typedef struct rlh_sampling_params {
+  float temperature;        /* <= 0: greedy                                     */
+  uint32_t top_k;           /* 0: all tokens                                    */
+  float top_p;              /* applied when in (0, 1)                           */
+  float repetition_penalty; /* 1: off                                           */
+  uint32_t repeat_last_n;   /* window of the penalty; 0: whole history          */
+  uint64_t seed;            /* Sampler::new(seed) (used by rlh_generate)        */
+} rlh_sampling_params;
+/* Sampler::new (sampler.rs:33-37): the xorshift64* state for a seed. */
+uint64_t rlh_sampler_init(uint64_t seed);
+/* Sampler::sample (sampler.rs:56-163) on host logits[n] with the history
+ * `recent`; advances *rng_state. Equal probabilities inside top-k are
+ * ordered by token id (the reference leaves their order to Rust's
+ * select_nth_unstable). */
+int rlh_sample(const float* logits, uint64_t n, const rlh_sampling_params* p, const uint32_t* recent,
+               uint64_t n_recent, uint64_t* rng_state, uint32_t* token);
+/* The same on the logits of the last forward call on this cache: the greedy
+ * fast path (temperature <= 0 and no penalty) runs on the device, any other
+ * setting copies the logits to the host first. */
+int rlh_sample_next(rlh_model* m, rlh_cache* c, const rlh_sampling_params* p, const uint32_t* recent,
+                    uint64_t n_recent, uint64_t* rng_state, uint32_t* token);
+/* Model::generate (src/model.rs:741-776): reset the cache, prefill the
+ * prompt (n_prompt >= 1), then up to max_new steps of sample -> stop at
+ * `eos` -> append -> stop when the cache is full -> decode. out_tokens
+ * (max_new entries) receives the generated tokens, *n_out their count. */
+int rlh_generate(rlh_model* m, rlh_cache* c, const uint32_t* prompt, uint64_t n_prompt, uint64_t max_new,
+                 const rlh_sampling_params* p, uint32_t eos, uint32_t* out_tokens, uint64_t* n_out);
+
 /* ---- inspection for parity tests --------------------------------------------- */
 /* Residual stream after `layer` for the tokens of the last forward call
  * (n_tokens x n_embd f32, token-major). Requires rlh_cache_set_debug(c, 1)

@@ -23,6 +23,7 @@
 #include "matvec.h"
 #include "gemm.h"
 #include "rlh_format.h"
+#include "sampler.h"
 
 using namespace rlh;
 
@@ -34,6 +35,12 @@ int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+
+}  // namespace
+
+int rlh::set_error(int code, const char* msg) { return fail(code, msg); }
+
+namespace {
 
 #define HIPCHK(expr)                                                                              \
   do {                                                                                            \
@@ -68,8 +75,8 @@ int type_size(uint32_t ty) {  // quant.rs:53-66
 // Types whose device layout and dequantisation exist (the embedding gather
 // and the parity entries); matvec_supported() is the subset with a matvec.
 bool layout_supported(uint32_t ty) {
-  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
-         ty == RLH_TYPE_F32 || ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16;
+  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 ||
+         ty == RLH_TYPE_Q4_0 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -122,7 +129,7 @@ struct Layer {
 // taken as they are; for Q8_0/Q4_0 the quants of 8 blocks come first, then
 // their 8 f16 scales.
 void gather_item(uint32_t ty, const uint8_t* row, uint32_t j, uint8_t* item) {
-  if (ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K) {
+  if (ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q6_K) {
     const uint32_t ib = item_bytes(ty);
     std::memcpy(item, row + (size_t)j * ib, ib);
     return;
@@ -258,6 +265,7 @@ struct rlh_model {
   std::vector<Layer> layers;
   float* rope_cs = nullptr;  // [n_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i+1
   bool finalized = false;
+  bool f32_route = false;  // some layer matrix multiplies f32 activations in prefill (Q5_K)
 };
 
 struct rlh_cache {
@@ -288,7 +296,7 @@ struct rlh_cache {
   // kBatch tokens per chunk, token-major
   uint32_t bcap = 0;
   float *xb = nullptr, *qb = nullptr, *kb = nullptr, *vb = nullptr, *attnb = nullptr, *gb = nullptr, *ub = nullptr,
-        *scoresb = nullptr;
+        *scoresb = nullptr, *xnb = nullptr;  // xnb: f32 rmsnorm rows (inputs of f32-route products)
   Q8Buf act_eb{}, act_qb{}, act_fb{};
   uint32_t* tokb = nullptr;   // token ids of the whole call
   uint32_t* posb = nullptr;   // first position of every chunk
@@ -367,6 +375,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
     {  // attn_output, x += (model.rs:713-716)
       MvPlan p;
       mv_plan_init(p, qd, c->act_q);
+      mv_plan_set_f32(p, c->attn);
       mv_plan_add(p, L.o.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
@@ -381,6 +390,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
     {  // ffn_down, x += (model.rs:725-728)
       MvPlan p;
       mv_plan_init(p, F, c->act_f);
+      mv_plan_set_f32(p, c->g);
       mv_plan_add(p, L.down.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
@@ -393,9 +403,10 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
   {  // logits of rmsnorm(x, output_norm) (model.rs:733-737), greedy argmax fused;
      // the norm runs once here rather than in each of the many logits blocks
-    launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
+    launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, c->scratch);
     MvPlan p;
     mv_plan_init(p, E, c->act_e);
+    mv_plan_set_f32(p, c->scratch);
     mv_plan_add(p, ow.dm, c->logits, nullptr);
     if (kind == STEP_GREEDY) mv_plan_argmax(p, MvArgmax{c->pv, c->pi});
     mv_plan_finish(p);
@@ -524,8 +535,8 @@ static int check_matrix(const DevTensor& t, const char* name, int layer, uint64_
   if (t.rows != rows || t.cols != cols)
     return fail(RLH_EINVAL, "tensor '" + nm + "' has shape " + std::to_string(t.rows) + "x" + std::to_string(t.cols) +
                                 ", expected " + std::to_string(rows) + "x" + std::to_string(cols));
-  if (!matvec_supported(t.ty))
-    return fail(RLH_EUNSUP, "tensor '" + nm + "' has ggml type " + std::to_string(t.ty) + " with no matvec kernel");
+  if (!matvec_supported(t.ty) || (layer >= 0 && !gemm_supported(t.ty) && !gemm_f32_supported(t.ty)))
+    return fail(RLH_EUNSUP, "tensor '" + nm + "' has ggml type " + std::to_string(t.ty) + " with no kernel");
   return RLH_OK;
 }
 static int check_vec(const DevVec& v, const char* name, int layer, uint64_t n, bool required) {
@@ -568,12 +579,17 @@ int rlh_model_finalize(rlh_model* m) {
     if ((rc = check_vec(L.bk, "attn_k.bias", li, kvd, false))) return rc;
     if ((rc = check_vec(L.bv, "attn_v.bias", li, kvd, false))) return rc;
   }
+  m->f32_route = false;
+  for (const Layer& L : m->layers)
+    for (const DevTensor* t : {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down})
+      if (!gemm_supported(t->ty)) m->f32_route = true;
   // every decode matvec launch must fit the kernel's LDS budget
   for (uint32_t l = 0; l < c.n_layer; l++) {
     Layer& L = m->layers[l];
     if (L.gate.ty != L.up.ty)
       return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": ffn_gate and ffn_up must share a ggml type");
     const Q8Mut none{};
+    static const float kShapeOnly = 0.0f;  // plans below are built for their shape only
     MvPlan p;
     mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
     mv_plan_add(p, L.q.dm, nullptr, nullptr);
@@ -581,20 +597,24 @@ int rlh_model_finalize(rlh_model* m) {
     mv_plan_add(p, L.v.dm, nullptr, nullptr);
     bool ok = mv_plan_finish(p);
     mv_plan_init(p, (uint32_t)qd, none);
+    mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, L.o.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
     mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
     mv_plan_add_pair(p, L.gate.dm, L.up.dm, none, nullptr);
     ok = ok && mv_plan_finish(p);
     mv_plan_init(p, (uint32_t)F, none);
+    mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, L.down.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
     if (!ok) return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": matrix shapes or types are not supported by the matvec");
   }
   {
     const DevTensor& ow = m->output.set ? m->output : m->token_embd;
+    static const float kShapeOnly = 0.0f;  // built for its shape only
     MvPlan p;
     mv_plan_init(p, (uint32_t)E, Q8Mut{});
+    mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, ow.dm, nullptr, nullptr);
     if (!mv_plan_finish(p)) return fail(RLH_EUNSUP, "logits matrix shape or type is not supported by the matvec");
   }
@@ -656,7 +676,7 @@ static void cache_free(rlh_cache* c) {
                   c->pi, c->dbg};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  void* bptrs[] = {c->xb, c->qb, c->kb, c->vb, c->attnb, c->gb, c->ub, c->scoresb, c->act_eb.qs, c->act_eb.d,
+  void* bptrs[] = {c->xb, c->qb, c->kb, c->vb, c->attnb, c->gb, c->ub, c->scoresb, c->xnb, c->act_eb.qs, c->act_eb.d,
                    c->act_eb.s, c->act_eb.s16, c->act_qb.qs, c->act_qb.d, c->act_qb.s, c->act_qb.s16, c->act_fb.qs,
                    c->act_fb.d, c->act_fb.s, c->act_fb.s16, c->tokb, c->posb};
   for (void* p : bptrs)
@@ -797,7 +817,7 @@ static int ensure_batch(rlh_cache* c) {
   bool ok = hipMalloc((void**)&c->xb, B * E * 4) == hipSuccess && hipMalloc((void**)&c->qb, B * qd * 4) == hipSuccess &&
             hipMalloc((void**)&c->kb, B * kvd * 4) == hipSuccess && hipMalloc((void**)&c->vb, B * kvd * 4) == hipSuccess &&
             hipMalloc((void**)&c->attnb, B * qd * 4) == hipSuccess && hipMalloc((void**)&c->gb, B * F * 4) == hipSuccess &&
-            hipMalloc((void**)&c->ub, B * F * 4) == hipSuccess &&
+            hipMalloc((void**)&c->ub, B * F * 4) == hipSuccess && hipMalloc((void**)&c->xnb, B * E * 4) == hipSuccess &&
             hipMalloc((void**)&c->scoresb, (size_t)B * cfg.n_head * c->max_ctx * 4) == hipSuccess;
   if (!ok) return fail(RLH_ENOMEM, "prefill workspace allocation failed");
   int rc = alloc_q8(c->act_eb, B * E);
@@ -849,13 +869,24 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
     const uint32_t p0 = p0s[ci];
     const uint32_t* pos = c->posb + ci;
     last_m = mtok;
+    // tokens of this chunk that are in the call's groups of 4 (f32-route
+    // products give the last n % 4 tokens of the call the single-token order)
+    const uint64_t n4_all = n - n % 4;
+    const uint32_t n4 = (uint32_t)std::min<uint64_t>(mtok, n4_all > c0 ? n4_all - c0 : 0);
+    auto product = [&](const DevMat& w, const Q8Buf& q8, const float* xf, float* y, float* resid) {
+      if (gemm_supported(w.ty))
+        launch_gemm(st, w, q8, mtok, y, resid);
+      else
+        launch_gemm_f32(st, w, xf, mtok, n4, y, resid);
+    };
+    float* xn = m->f32_route ? c->xnb : nullptr;  // f32 rmsnorm rows, when a product needs them
     launch_embed(st, m->token_embd.dm, c->tokb + c0, mtok, c->xb);
     for (uint32_t l = 0; l < cfg.n_layer; l++) {
       Layer& L = m->layers[l];
-      launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, nullptr);
-      launch_gemm(st, L.q.dm, c->act_eb, mtok, c->qb, nullptr);
-      launch_gemm(st, L.k.dm, c->act_eb, mtok, c->kb, nullptr);
-      launch_gemm(st, L.v.dm, c->act_eb, mtok, c->vb, nullptr);
+      launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, xn);
+      product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
+      product(L.k.dm, c->act_eb, xn, c->kb, nullptr);
+      product(L.v.dm, c->act_eb, xn, c->vb, nullptr);
       launch_qk_norm_rope_kv(st, c->qb, c->kb, c->vb, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
                              cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
                              (int)H, (int)KVH, mtok, eps);
@@ -879,12 +910,14 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       launch_attn_scores(st, a, false);
       launch_attn_softmax(st, a);
       launch_attn_pv(st, a, false);
-      launch_gemm(st, L.o.dm, c->act_qb, mtok, nullptr, c->xb);
-      launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, nullptr);
-      launch_gemm(st, L.gate.dm, c->act_eb, mtok, c->gb, nullptr);
-      launch_gemm(st, L.up.dm, c->act_eb, mtok, c->ub, nullptr);
-      launch_swiglu_q8(st, c->gb, c->ub, mtok * cfg.n_ff, c->act_fb, nullptr);
-      launch_gemm(st, L.down.dm, c->act_fb, mtok, nullptr, c->xb);
+      product(L.o.dm, c->act_qb, c->attnb, nullptr, c->xb);
+      launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, xn);
+      product(L.gate.dm, c->act_eb, xn, c->gb, nullptr);
+      product(L.up.dm, c->act_eb, xn, c->ub, nullptr);
+      // h over the gate rows in place when ffn_down takes the f32 route
+      const bool hf = !gemm_supported(L.down.ty);
+      launch_swiglu_q8(st, c->gb, c->ub, mtok * cfg.n_ff, c->act_fb, hf ? c->gb : nullptr);
+      product(L.down.dm, c->act_fb, c->gb, nullptr, c->xb);
       if (c->debug && c->dbg && c0 < c->dbg_tokens) {
         const uint64_t nd = std::min<uint64_t>(mtok, c->dbg_tokens - c0);
         HIPCHK(hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + c0) * E, c->xb, nd * E * 4,
@@ -895,10 +928,11 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
   }
   // logits of the last token: rmsnorm(x, output_norm), then the decode matvec
   HIPCHK(hipMemcpyAsync(c->x, c->xb + (size_t)(last_m - 1) * E, (size_t)E * 4, hipMemcpyDeviceToDevice, st));
-  launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, nullptr);
+  launch_rmsnorm_q8(st, c->x, m->output_norm.p, E, 1, eps, c->act_e, c->scratch);
   const DevTensor& ow = m->output.set ? m->output : m->token_embd;
   MvPlan p;
   mv_plan_init(p, E, c->act_e);
+  mv_plan_set_f32(p, c->scratch);
   mv_plan_add(p, ow.dm, c->logits, nullptr);
   mv_plan_finish(p);
   mv_launch(st, p);
@@ -940,6 +974,44 @@ int rlh_greedy_next(rlh_model* m, rlh_cache* c, uint32_t* token) {
   HIPCHK(hipMemcpyAsync(c->host_st + 3, c->st_dev + 3, 4, hipMemcpyDeviceToHost, c->st));
   HIPCHK(hipStreamSynchronize(c->st));
   *token = c->host_st[3];
+  return RLH_OK;
+}
+
+int rlh_sample_next(rlh_model* m, rlh_cache* c, const rlh_sampling_params* p, const uint32_t* recent,
+                    uint64_t n_recent, uint64_t* rng_state, uint32_t* token) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!p || !rng_state || !token || (n_recent && !recent)) return fail(RLH_EINVAL, "null argument");
+  if (!c->logits_valid) return fail(RLH_ESTATE, "no logits computed on this cache yet");
+  // sampler.rs:62-70: the greedy fast path is the device argmax (same ties)
+  if (p->temperature <= 0.0f && p->repetition_penalty == 1.0f) return rlh_greedy_next(m, c, token);
+  std::vector<float> host(m->cfg.vocab_size);
+  HIPCHK(hipMemcpyAsync(host.data(), c->logits, host.size() * 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  *token = sample_logits(host.data(), host.size(), *p, recent, (size_t)n_recent, rng_state);
+  return RLH_OK;
+}
+
+int rlh_generate(rlh_model* m, rlh_cache* c, const uint32_t* prompt, uint64_t n_prompt, uint64_t max_new,
+                 const rlh_sampling_params* p, uint32_t eos, uint32_t* out_tokens, uint64_t* n_out) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!prompt || !p || !n_out || (max_new && !out_tokens)) return fail(RLH_EINVAL, "null argument");
+  if (n_prompt == 0) return fail(RLH_EINVAL, "empty prompt");
+  *n_out = 0;
+  uint64_t state = rlh_sampler_init(p->seed);
+  if ((rc = rlh_cache_reset(c))) return rc;
+  if ((rc = rlh_forward_into(m, c, prompt, n_prompt, 0, nullptr))) return rc;
+  std::vector<uint32_t> recent(prompt, prompt + n_prompt);
+  for (uint64_t i = 0; i < max_new; i++) {
+    uint32_t next = 0;
+    if ((rc = rlh_sample_next(m, c, p, recent.data(), recent.size(), &state, &next))) return rc;
+    if (next == eos) break;
+    out_tokens[(*n_out)++] = next;
+    recent.push_back(next);
+    if (c->len >= c->max_ctx) break;
+    if ((rc = rlh_forward_into(m, c, &next, 1, c->len, nullptr))) return rc;
+  }
   return RLH_OK;
 }
 
@@ -1060,6 +1132,7 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
   const Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
   MvPlan p;
   mv_plan_init(p, (uint32_t)cols, act);
+  mv_plan_set_f32(p, dx.p);
   mv_plan_add(p, t.dm, dy.p, nullptr);
   if (!mv_plan_finish(p)) {
     free_tensor(t);
@@ -1081,7 +1154,8 @@ int rlh_matmul_batch(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, c
   if (!xs || !ys) return fail(RLH_EINVAL, "null argument");
   if (n == 0) return RLH_OK;
   if (n == 1) return rlh_matvec(ty, w, rows, cols, xs, ys);  // ops.rs:158-161
-  if (!gemm_supported(ty)) return fail(RLH_EUNSUP, "no batched kernel for ggml type " + std::to_string(ty));
+  if (!gemm_supported(ty) && !gemm_f32_supported(ty))
+    return fail(RLH_EUNSUP, "no batched kernel for ggml type " + std::to_string(ty));
   if (cols == 0 || cols % 256) return fail(RLH_EINVAL, "cols must be a positive multiple of 256");
   if (rows == 0 || rows > 0xffffffffull || n > 0xffffffffull / cols) return fail(RLH_EINVAL, "shape out of range");
   DevTensor t;
@@ -1100,8 +1174,12 @@ int rlh_matmul_batch(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, c
   // quantize_q8 of every token row (ops.rs:207-209), then the products
   const Q8Buf act{dq.p, dd.p, ds.p, ds16.p};
   hipError_t e = hipMemcpyAsync(dx.p, xs, nv * 4, hipMemcpyHostToDevice, st);
-  launch_quantize_q8(st, dx.p, (uint32_t)nv, act);
-  launch_gemm(st, t.dm, act, (uint32_t)n, dy.p, nullptr);
+  if (gemm_supported(ty)) {
+    launch_quantize_q8(st, dx.p, (uint32_t)nv, act);
+    launch_gemm(st, t.dm, act, (uint32_t)n, dy.p, nullptr);
+  } else {  // the f32 route (ops.rs:237-312): no activation quantization
+    launch_gemm_f32(st, t.dm, dx.p, (uint32_t)n, (uint32_t)(n - n % 4), dy.p, nullptr);
+  }
   if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(ys, dy.p, n * rows * 4, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
@@ -1112,7 +1190,7 @@ int rlh_matmul_batch(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, c
 
 int rlh_block_dots(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out) {
   if (!q8 || !out) return fail(RLH_EINVAL, "null argument");
-  if (!matvec_supported(ty)) return fail(RLH_EUNSUP, "no integer dot for ggml type " + std::to_string(ty));
+  if (!gemm_supported(ty)) return fail(RLH_EUNSUP, "no integer dot for ggml type " + std::to_string(ty));
   uint32_t per_row = ty == RLH_TYPE_Q6_K ? (uint32_t)(cols / 16) : (uint32_t)(cols / 32);
   DevTensor t;
   int rc = op_upload(t, ty, w, rows, cols);
@@ -1172,6 +1250,7 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
       const DevTensor* t = find_matrix(m, kind, 0);
       if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
       mv_plan_init(p, (uint32_t)t->cols, c->act_e);
+      mv_plan_set_f32(p, c->scratch);
       mv_plan_add(p, t->dm, c->logits, nullptr);
     } else {
       const Layer& L = m->layers[l];
@@ -1189,11 +1268,13 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
         const uint64_t cols = t->cols;
         if (cols == cfg.n_embd)
           mv_plan_init_norm(p, (uint32_t)cols, c->x, L.attn_norm.p, cfg.rms_eps);
-        else if (cols == qd)
+        else if (cols == qd) {
           mv_plan_init(p, (uint32_t)cols, c->act_q);
-        else if (cols == cfg.n_ff)
+          mv_plan_set_f32(p, c->attn);
+        } else if (cols == cfg.n_ff) {
           mv_plan_init(p, (uint32_t)cols, c->act_f);
-        else
+          mv_plan_set_f32(p, c->g);
+        } else
           return fail(RLH_EINVAL, "matrix width matches no activation buffer");
         mv_plan_add(p, t->dm, c->logits, nullptr);
       }

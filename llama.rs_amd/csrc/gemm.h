@@ -22,5 +22,11 @@ struct GemmArgs {
 bool gemm_supported(uint32_t ty);
 // Y[n][rows] (token-major) for the n activation rows; cols % 256 == 0.
 void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, float* y, float* resid);
+// Weight types without an integer batch path (Q5_K): matmul_batch's f32
+// route on the f32 activations x[n][cols]; the tokens from n4 on (the last
+// n % 4 of the whole batch) take the single-token dot order.
+bool gemm_f32_supported(uint32_t ty);
+void launch_gemm_f32(hipStream_t st, const DevMat& w, const float* x, uint32_t n, uint32_t n4, float* y,
+                     float* resid);
 
 }  // namespace rlh

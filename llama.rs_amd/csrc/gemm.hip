@@ -506,10 +506,157 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
       }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill products for Q5_K, which has no integer batch path in the
+// reference: matmul_batch's f32 route (ops.rs:237-312) dequantizes rows
+// (quant.rs:313-349) and runs dot_multi_rows::<3, 4> (simd.rs:779-836) on the
+// f32 activations. Every output of a token group of 4 is one 8-lane FMA chain
+// over the row (lane l takes elements 8i + l in order) reduced by the AVX2
+// tree; the last n % 4 tokens take dot_f32_avx2 (32 chains over 32-value
+// chunks, (a0+a1)+(a2+a3), tree). ys starts at zero and gets `+= value`.
+// Block: 16 rows x 16 tokens, one thread per (row, token) running its
+// chains; each 256-value super-block of the 16 rows is dequantized into LDS
+// once and the 16 tokens' activations staged beside it.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kFR = 16, kFT = 16, kFS = 260;  // rows, tokens, LDS floats per 256 values
+
+struct GemmF32Args {
+  DevMat w;
+  const float* x;  // [n][cols] f32
+  uint32_t n;
+  float* y;
+  float* resid;
+  uint32_t n4;     // tokens handled in groups of 4 (n - n % 4)
+};
+
+__device__ __forceinline__ float tree8(const float* A) {
+  return ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+}
+
+__global__ void __launch_bounds__(256) k_gemm_f32_q5k(GemmF32Args a) {
+  __shared__ __attribute__((aligned(16))) float ws_g[kFR * kFS];
+  __shared__ __attribute__((aligned(16))) float xs_g[kFT * kFS];
+  typedef RLH_LDS float lfloat;
+  typedef RLH_LDS f32x4_t lf32x4;
+  lfloat* ws = (lfloat*)ws_g;
+  lfloat* xs = (lfloat*)xs_g;
+  const uint32_t tid = threadIdx.x, r0 = blockIdx.x * kFR, t0 = blockIdx.y * kFT;
+  const uint32_t rl = tid / kFT, tl = tid % kFT, row = r0 + rl, tok = t0 + tl;
+  const uint32_t nsb = a.w.cols / 256;
+  const bool tail = tok >= a.n4;
+  // dequant duty: row r0 + tid / 16, values 16 * (tid % 16) .. + 15 of the super-block
+  const uint32_t dr = tid / 16, dp = tid % 16, dsub = dp / 2, dl = 16 * (dp % 2);
+  const uint32_t drow = min(r0 + dr, a.w.rows - 1);
+  float c8[8], c32[4][8];
+#pragma unroll
+  for (int l = 0; l < 8; l++) {
+    c8[l] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; m++) c32[m][l] = 0.0f;
+  }
+  for (uint32_t j = 0; j < nsb; j++) {
+    // this thread's 16 dequantized values: the header chunk, its 16 quant
+    // bytes and 16 high-bit bytes (all 16-byte aligned inside the item)
+    const u32x4_t hdr = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 0));
+    const u32x4_t qv = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 48 + 32 * (dsub / 2) + dl));
+    const u32x4_t hv = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 16 + dl));
+    f32x4_t xv[4];
+    const uint32_t xt = min(t0 + tid / 16, a.n - 1);
+#pragma unroll
+    for (int q = 0; q < 4; q++)  // token t0 + tid / 16, values 16 * (tid % 16) + 4q
+      xv[q] = *(const RLH_GLOBAL f32x4_t*)(a.x + (size_t)xt * a.w.cols + 256 * j + 16 * (tid % 16) + 4 * q);
+    const float d = f16_to_f32(hdr.x & 0xffff), dmin = f16_to_f32(hdr.x >> 16);
+    uint8_t sb[12];
+    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
+#pragma unroll
+    for (int k = 0; k < 12; k++) sb[k] = (uint8_t)(sw[k / 4] >> (8 * (k % 4)));
+    uint32_t sc, m;
+    scale_min_k4((int)dsub, sb, sc, m);
+    const float d1 = d * (float)sc, mm1 = dmin * (float)m;
+    const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    __syncthreads();  // the previous super-block's tiles are consumed
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const uint32_t v = ((qw[q] >> (4 * (dsub & 1))) & 0x0F0F0F0Fu) | (((hw[q] >> dsub) & 0x01010101u) << 4);
+      f32x4_t o;
+      o.x = d1 * (float)(v & 0xff) - mm1;
+      o.y = d1 * (float)((v >> 8) & 0xff) - mm1;
+      o.z = d1 * (float)((v >> 16) & 0xff) - mm1;
+      o.w = d1 * (float)(v >> 24) - mm1;
+      *(lf32x4*)(ws + dr * kFS + 32 * dsub + dl + 4 * q) = o;
+      *(lf32x4*)(xs + (tid / 16) * kFS + 16 * (tid % 16) + 4 * q) = xv[q];
+    }
+    __syncthreads();
+    const lf32x4* w4 = (const lf32x4*)(ws + rl * kFS);
+    const lf32x4* x4 = (const lf32x4*)(xs + tl * kFS);
+    if (!tail) {  // dot_multi_rows: lane l of the 8-wide chain takes 8i + l
+#pragma unroll 8
+      for (int i = 0; i < 32; i++) {
+        const f32x4_t wa = w4[2 * i], wb = w4[2 * i + 1], xa = x4[2 * i], xb = x4[2 * i + 1];
+        c8[0] = __builtin_fmaf(wa.x, xa.x, c8[0]);
+        c8[1] = __builtin_fmaf(wa.y, xa.y, c8[1]);
+        c8[2] = __builtin_fmaf(wa.z, xa.z, c8[2]);
+        c8[3] = __builtin_fmaf(wa.w, xa.w, c8[3]);
+        c8[4] = __builtin_fmaf(wb.x, xb.x, c8[4]);
+        c8[5] = __builtin_fmaf(wb.y, xb.y, c8[5]);
+        c8[6] = __builtin_fmaf(wb.z, xb.z, c8[6]);
+        c8[7] = __builtin_fmaf(wb.w, xb.w, c8[7]);
+      }
+    } else {  // dot_f32_avx2: chain (m, l) takes 32c + 8m + l
+#pragma unroll 2
+      for (int c = 0; c < 8; c++) {
+#pragma unroll
+        for (int mq = 0; mq < 4; mq++) {
+          const f32x4_t wa = w4[8 * c + 2 * mq], wb = w4[8 * c + 2 * mq + 1];
+          const f32x4_t xa = x4[8 * c + 2 * mq], xb = x4[8 * c + 2 * mq + 1];
+          c32[mq][0] = __builtin_fmaf(wa.x, xa.x, c32[mq][0]);
+          c32[mq][1] = __builtin_fmaf(wa.y, xa.y, c32[mq][1]);
+          c32[mq][2] = __builtin_fmaf(wa.z, xa.z, c32[mq][2]);
+          c32[mq][3] = __builtin_fmaf(wa.w, xa.w, c32[mq][3]);
+          c32[mq][4] = __builtin_fmaf(wb.x, xb.x, c32[mq][4]);
+          c32[mq][5] = __builtin_fmaf(wb.y, xb.y, c32[mq][5]);
+          c32[mq][6] = __builtin_fmaf(wb.z, xb.z, c32[mq][6]);
+          c32[mq][7] = __builtin_fmaf(wb.w, xb.w, c32[mq][7]);
+        }
+      }
+    }
+  }
+  if (row >= a.w.rows || tok >= a.n) return;
+  float v;
+  if (!tail) {
+    v = 0.0f + (tree8(c8) + 0.0f);  // out += hsum(acc) + tail (no tail: cols % 8 == 0)
+  } else {
+    float A[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) A[l] = (c32[0][l] + c32[1][l]) + (c32[2][l] + c32[3][l]);
+    v = 0.0f + tree8(A);
+  }
+  const size_t idx = (size_t)tok * a.w.rows + row;
+  if (a.resid) {
+    RLH_GLOBAL float* x = (RLH_GLOBAL float*)a.resid;
+    x[idx] = x[idx] + v;
+  }
+  if (a.y) ((RLH_GLOBAL float*)a.y)[idx] = v;
+}
+
 }  // namespace
 
 bool gemm_supported(uint32_t ty) {
   return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
+}
+
+bool gemm_f32_supported(uint32_t ty) { return ty == RLH_TYPE_Q5_K; }
+
+void launch_gemm_f32(hipStream_t st, const DevMat& w, const float* x, uint32_t n, uint32_t n4, float* y,
+                     float* resid) {
+  GemmF32Args a{};
+  a.w = w;
+  a.x = x;
+  a.n = n;
+  a.n4 = n4;
+  a.y = y;
+  a.resid = resid;
+  hipLaunchKernelGGL(k_gemm_f32_q5k, dim3((w.rows + kFR - 1) / kFR, (n + kFT - 1) / kFT), dim3(256), 0, st, a);
 }
 
 void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, float* y, float* resid) {

@@ -331,7 +331,8 @@ void launch_quantize_q8(hipStream_t st, const float* x, uint32_t n, const Q8Buf&
 }
 
 bool matvec_supported(uint32_t ty) {
-  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
+  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
+         ty == RLH_TYPE_Q5_K;
 }
 
 void launch_block_dots(hipStream_t st, const DevMat& w, const int8_t* a, int32_t* out, uint32_t per_row) {

@@ -46,6 +46,12 @@ struct MvLaunch {
   const float* nx;
   const float* nw;
   float eps;
+  // f32 activation row, needed by Q5_K segments (the reference multiplies
+  // Q5_K weights with the unquantized activation, quant.rs:528-539): staged
+  // from xf in Q8 launches, written by the norm prologue otherwise
+  const float* xf;
+  uint32_t need_xf;
+  uint32_t xf_off;  // byte offset of the f32 row in LDS
   uint32_t region_off;    // byte offset of the term tiles in LDS
   uint32_t tile_stride;   // floats per term-tile row
   uint32_t has_argmax;
@@ -65,9 +71,9 @@ struct MvPlan {
 
 // Terms (float summands of the reference's per-row chain) per 256-value
 // super-block: one per 64 values for Q4_K, per 16 for Q6_K, per 32 for
-// Q8_0/Q4_0.
+// Q8_0/Q4_0, one per super-block for Q5_K (its f32 block dot).
 __host__ __device__ inline uint32_t mv_terms_per_sb(uint32_t ty) {
-  return ty == RLH_TYPE_Q6_K ? 16u : (ty == RLH_TYPE_Q4_K ? 4u : 8u);
+  return ty == RLH_TYPE_Q6_K ? 16u : (ty == RLH_TYPE_Q4_K ? 4u : (ty == RLH_TYPE_Q5_K ? 1u : 8u));
 }
 
 // Plan construction: act is the Q8 activation row (cols values, cols a
@@ -79,6 +85,8 @@ void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act);
 // the rmsnorm weight w (cols <= kMvMaxNormCols).
 void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w, float eps);
 constexpr uint32_t kMvMaxNormCols = 7168;
+// The f32 form of a Q8 launch's activation (used when a segment is Q5_K).
+void mv_plan_set_f32(MvPlan& p, const float* xf);
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
 void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h);
 void mv_plan_argmax(MvPlan& p, const MvArgmax& am);

@@ -50,7 +50,10 @@ struct LAct {
   RLH_LDS float* d;
   RLH_LDS int32_t* s;
   RLH_LDS float* s16x32;  // 32.0f * (float)sums16 (the Q6_K correction, exact in f32)
+  RLH_LDS float* xf;      // f32 row, padded: value i at (i / 256) * kXfStride + i % 256
 };
+
+constexpr uint32_t kXfStride = 260;  // LDS floats per 256 f32 activation values (16-byte pad)
 
 __device__ __forceinline__ const RLH_LDS int8_t* qblk(const LAct& a, uint32_t b) {
   return a.qs + (b >> 3) * kSbStride + (b & 7) * 32;
@@ -236,6 +239,72 @@ struct MI<RLH_TYPE_Q4_0> {
   }
 };
 
+// Q5_K: no integer kernel in the reference; the row is
+// sum over super-blocks, in order, of dot_f32_avx2(dequant(block), x_block)
+// (dequant_dot_scalar's generic fallback, quant.rs:528-539, with ops::dot =
+// simd.rs:328-377 for 256 values): slot (m, l) is the FMA chain over the
+// eight 32-value chunks c of element 32c + 8m + l, A_l = (a0+a1)+(a2+a3),
+// then the AVX2 tree. Dequant (quant.rs:313-349): d1 * (q + 16*hbit) - mm1.
+// One term per super-block.
+template <>
+struct MI<RLH_TYPE_Q5_K> {
+  static constexpr uint32_t kT = 1;
+  struct W {
+    u32x4_t hdr, qh[2], q[8];
+  };
+  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+    r.hdr = gl_u4(tile + lane * 16);
+    r.qh[0] = gl_u4(tile + 1024 + lane * 16);
+    r.qh[1] = gl_u4(tile + 2048 + lane * 16);
+#pragma unroll
+    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + (k + 3) * 1024 + lane * 16);
+  }
+  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+    const float d = f16_to_f32(r.hdr.x & 0xffff);
+    const float dmin = f16_to_f32(r.hdr.x >> 16);
+    const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+    const lf32x4* x4 = (const lf32x4*)(act.xf + j * kXfStride);
+    const uint32_t qh[8] = {r.qh[0].x, r.qh[0].y, r.qh[0].z, r.qh[0].w, r.qh[1].x, r.qh[1].y, r.qh[1].z, r.qh[1].w};
+    float a[4][8];
+#pragma unroll
+    for (int mm = 0; mm < 4; mm++)
+#pragma unroll
+      for (int l = 0; l < 8; l++) a[mm][l] = 0.0f;
+    // one sub-block (32 values, chunk c of dot_f32_avx2) per iteration; the
+    // chains start at +0.0 as _mm256_setzero_ps does
+#pragma unroll 1
+    for (int c = 0; c < 8; c++) {
+      const int g = c >> 1, sh4 = 4 * (c & 1), sh = 8 * (c & 3);
+      const uint32_t sc_lo = (s0 >> sh) & 63, m_lo = (s1 >> sh) & 63;
+      const uint32_t sc_hi = ((s2 >> sh) & 0xF) | (((s0 >> sh) >> 6 & 3) << 4);
+      const uint32_t m_hi = ((s2 >> sh) >> 4 & 0xF) | (((s1 >> sh) >> 6 & 3) << 4);
+      const uint32_t sc = c < 4 ? sc_lo : sc_hi, m = c < 4 ? m_lo : m_hi;
+      const float d1 = d * (float)sc, mm1 = dmin * (float)m;
+      const u32x4_t qa = g == 0 ? r.q[0] : (g == 1 ? r.q[2] : (g == 2 ? r.q[4] : r.q[6]));
+      const u32x4_t qb = g == 0 ? r.q[1] : (g == 1 ? r.q[3] : (g == 2 ? r.q[5] : r.q[7]));
+      const uint32_t qw[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+      for (int w4 = 0; w4 < 8; w4++) {  // values 4*w4 .. 4*w4+3 of the sub-block
+        const uint32_t nib = (qw[w4] >> sh4) & 0x0F0F0F0Fu;
+        const uint32_t hb = ((qh[w4] >> c) & 0x01010101u) << 4;
+        const uint32_t v = nib | hb;  // 4 bytes of q + 16 * hbit
+        const f32x4_t xv = x4[8 * c + w4];
+        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const int i = 4 * w4 + b, mi = i >> 3, l = i & 7;
+          const float wv = d1 * (float)((v >> (8 * b)) & 0xff) - mm1;
+          a[mi][l] = __builtin_fmaf(wv, xs[b], a[mi][l]);
+        }
+      }
+    }
+    float A[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) A[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+    t[0] = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+  }
+};
+
 // In-order sum of n terms (the per-row f32 chain); 32 terms per batch of
 // LDS reads so that the reads overlap the dependent adds.
 __device__ __forceinline__ float chain(const lfloat* t, uint32_t n) {
@@ -286,6 +355,10 @@ __device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& 
   lds_dma4(la.d, L.act.d, nb * 4, wave, nw);
   lds_dma4(la.s, L.act.s, nb * 4, wave, nw);
   lds_dma4(la.s16x32, L.act.s16, nb * 8, wave, nw);
+  if (L.need_xf)  // the f32 row, one 256-value super-block per wave instruction
+    for (uint32_t sb = wave; sb < nsb; sb += nw)
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.xf + sb * 256 + lane * 4),
+                                       (RLH_LDS void*)(la.xf + sb * kXfStride), 16, 0, 0);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and first weights) have landed
   __syncthreads();
   for (uint32_t i = tid; i < 2 * nb; i += blockDim.x) {
@@ -331,6 +404,7 @@ __device__ __forceinline__ void stage_norm(const MvLaunch& L, const LAct& la, lf
     if (i < n4) {  // n4 and NT are multiples of 8: whole 8-lane groups
       const float v0 = (xr[k].x * s) * wr[k].x, v1 = (xr[k].y * s) * wr[k].y;
       const float v2 = (xr[k].z * s) * wr[k].z, v3 = (xr[k].w * s) * wr[k].w;
+      if (L.need_xf) *(lf32x4*)(la.xf + (i >> 6) * kXfStride + 4 * (i & 63)) = f32x4_t{v0, v1, v2, v3};
       const Q8Blk8x4 r = q8_block8x4(v0, v1, v2, v3);
       const uint32_t blk = i / 8, l = i & 7;
       *(RLH_LDS uint32_t*)(la.qs + (blk >> 3) * kSbStride + (blk & 7) * 32 + 4 * l) = r.packed;
@@ -383,6 +457,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   la.d = (RLH_LDS float*)((RLH_LDS int8_t*)lds + nsb * kSbStride);
   la.s = (RLH_LDS int32_t*)(la.d + nb);
   la.s16x32 = (RLH_LDS float*)(la.s + nb);
+  la.xf = (RLH_LDS float*)((RLH_LDS int8_t*)lds + L.xf_off);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
 
   // two tiles per wave in flight: the next tile's weights load while the
@@ -399,8 +474,9 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     if (NM == 2) I::terms(w[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
   };
   // ping-pong over two register sets, except for PAIR launches of the
-  // larger item types, whose second set would not fit the register budget
-  constexpr bool kPP = NM == 1 || sizeof(typename I::W) <= 9 * 16;
+  // larger item types and for Q5_K, whose second set would not fit the
+  // register budget
+  constexpr bool kPP = (NM == 1 && TY != RLH_TYPE_Q5_K) || sizeof(typename I::W) <= 9 * 16;
   // the residual of the chain lane's row, read now so that the epilogue
   // does not wait for it
   float rsd = 0.0f;
@@ -490,6 +566,7 @@ __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
       case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_K: mv_block<RLH_TYPE_Q5_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       default: break;
     }
   }
@@ -504,6 +581,7 @@ MvKernel mv_kernel(uint32_t ty) {
     case RLH_TYPE_Q6_K: return k_mv<RLH_TYPE_Q6_K, NM>;
     case RLH_TYPE_Q8_0: return k_mv<RLH_TYPE_Q8_0, NM>;
     case RLH_TYPE_Q4_0: return k_mv<RLH_TYPE_Q4_0, NM>;
+    case RLH_TYPE_Q5_K: return k_mv<RLH_TYPE_Q5_K, NM>;
     default: return k_mv<0, NM>;
   }
 }
@@ -512,12 +590,19 @@ constexpr uint32_t kMaxLds = 150u * 1024u;
 
 // LDS bytes of a plan with R rows per block: the padded Q8 activation row,
 // then the term tiles.
+// LDS of a plan with R rows per block: the padded Q8 activation row, the
+// padded f32 row when a segment is Q5_K, then the term tiles (which the norm
+// prologue borrows for the unpadded f32 input row).
+uint32_t plan_act_bytes(const MvPlan& p) {
+  const uint32_t nsb = p.L.cols / 256, nb = p.L.cols / 32;
+  return (nsb * kSbStride + nb * 16 + 15) & ~15u;
+}
+uint32_t plan_xf_bytes(const MvPlan& p) { return p.L.need_xf ? (p.L.cols / 256) * kXfStride * 4 : 0u; }
 uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
-  const uint32_t cols = p.L.cols, nsb = cols / 256, nb = cols / 32;
-  const uint32_t act = (nsb * kSbStride + nb * 16 + 15) & ~15u;
+  const uint32_t cols = p.L.cols, nsb = cols / 256;
   const uint32_t stride = nsb * p.max_terms + 4;
   const uint32_t tile = nm * R * stride * 4;
-  return act + std::max(tile, p.norm ? cols * 4 : 0u);
+  return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? cols * 4 : 0u);
 }
 
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
@@ -542,6 +627,8 @@ void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w,
   p.L.eps = eps;
   p.norm = true;
 }
+
+void mv_plan_set_f32(MvPlan& p, const float* xf) { p.L.xf = xf; }
 
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
   MvSeg& g = p.L.seg[p.L.nseg++];
@@ -585,12 +672,16 @@ bool mv_plan_finish(MvPlan& p) {
                   p.L.seg[0].w.rows % 32 != 0))
     return false;
   const uint32_t R = nm == 2 ? std::max<uint32_t>(tr, 32) : tr;
+  p.L.need_xf = 0;
+  for (uint32_t s = 0; s < p.L.nseg; s++)
+    if (p.L.seg[s].w.ty == RLH_TYPE_Q5_K || (p.L.seg[s].pair && p.L.seg[s].w2.ty == RLH_TYPE_Q5_K)) p.L.need_xf = 1;
+  if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // Q5_K needs the f32 activation
   if (plan_lds(p, R, nm) > kMaxLds) return false;
   if (p.norm && (p.L.cols > kMvMaxNormCols || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
   p.L.tile_stride = nsb * p.max_terms + 4;
-  const uint32_t act = nsb * kSbStride + (p.L.cols / 32) * 16;
-  p.L.region_off = (act + 15) & ~15u;
+  p.L.xf_off = plan_act_bytes(p);
+  p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
   p.lds = plan_lds(p, R, nm);
   // two tiles per wave (the load/compute ping-pong); the norm prologue
   // needs at least 4 waves
@@ -630,7 +721,7 @@ void mv_launch(hipStream_t st, const MvPlan& p) {
 }
 
 bool mv_set_max_lds(size_t bytes) {
-  const uint32_t tys[] = {0, RLH_TYPE_Q4_K, RLH_TYPE_Q6_K, RLH_TYPE_Q8_0, RLH_TYPE_Q4_0};
+  const uint32_t tys[] = {0, RLH_TYPE_Q4_K, RLH_TYPE_Q6_K, RLH_TYPE_Q8_0, RLH_TYPE_Q4_0, RLH_TYPE_Q5_K};
   for (uint32_t ty : tys) {
     const void* fns[] = {(const void*)mv_kernel<1>(ty), (const void*)mv_kernel<2>(ty)};
     for (const void* f : fns)

@@ -322,6 +322,20 @@ __device__ __forceinline__ float dq_elem(const DevMat& w, uint32_t row, uint32_t
       const uint32_t q = (item_u8(w, row, j, 16 + 32 * g + l) >> (4 * hi)) & 0xF;
       return d1 * (float)q - mm1;
     }
+    case RLH_TYPE_Q5_K: {  // quant.rs:313-349: d1 * (q + 16 * hbit) - mm1
+      const uint32_t g = p >> 6, hi = (p >> 5) & 1, l = p & 31, sub = 2 * g + hi;
+      const float d = f16_to_f32(item_u16(w, row, j, 0));
+      const float dmin = f16_to_f32(item_u16(w, row, j, 2));
+      uint8_t sb[12];
+      for (int k = 0; k < 12; k++) sb[k] = (uint8_t)item_u8(w, row, j, 4 + k);
+      uint32_t sc, m;
+      scale_min_k4((int)sub, sb, sc, m);
+      const float d1 = d * (float)sc;
+      const float mm1 = dmin * (float)m;
+      const uint32_t q = (item_u8(w, row, j, 48 + 32 * g + l) >> (4 * hi)) & 0xF;
+      const uint32_t h = (item_u8(w, row, j, 16 + l) >> sub) & 1;
+      return d1 * (float)(q + 16 * h) - mm1;
+    }
     case RLH_TYPE_Q6_K: {
       const uint32_t half = p >> 7, pp = p & 127, quarter = pp >> 5, l = pp & 31;
       const float d = f16_to_f32(item_u16(w, row, j, 208));

@@ -2,8 +2,9 @@
 //
 // The bytes are the ggml block bytes of the reference (src/quant.rs:10-106);
 // only their placement in HBM differs. Quantized matrices (Q4_K, Q6_K, Q8_0,
-// Q4_0) are cut into items, one per 256 values of a row:
+// Q4_0, Q5_K) are cut into items, one per 256 values of a row:
 //   Q4_K  item = the 144-byte super-block as is;
+//   Q5_K  item = the 176-byte super-block as is (d, dmin, scales[12], qh[32], qs[128]);
 //   Q6_K  item = the 210-byte super-block as is (ql[128], qh[64], scales[16], d);
 //   Q8_0  item = 8 consecutive blocks: their 8 x 32 quants, then their 8 f16 d;
 //   Q4_0  item = 8 consecutive blocks: their 8 x 16 quant bytes, then 8 f16 d.
@@ -38,10 +39,11 @@ struct DevMat {
 };
 
 __host__ __device__ inline bool is_tiled(uint32_t ty) {
-  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
+  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
+         ty == RLH_TYPE_Q5_K;
 }
 __host__ __device__ inline uint32_t item_bytes(uint32_t ty) {
-  return ty == RLH_TYPE_Q6_K ? 210u : (ty == RLH_TYPE_Q8_0 ? 272u : 144u);
+  return ty == RLH_TYPE_Q6_K ? 210u : (ty == RLH_TYPE_Q8_0 ? 272u : (ty == RLH_TYPE_Q5_K ? 176u : 144u));
 }
 // Items per row must be a multiple of the tile width.
 __host__ __device__ inline uint32_t tile_width(uint32_t items_per_row) {

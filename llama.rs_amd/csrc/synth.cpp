@@ -153,6 +153,61 @@ void quant_q4_k(const float* x, size_t n, uint8_t* out) {
   }
 }
 
+// Q5_K: as Q4_K with 5-bit quants; the fifth bit of value l of sub-block j
+// is bit j of qh[l] (quant.rs:313-349 reads it back).
+void quant_q5_k(const float* x, size_t n, uint8_t* out) {
+  for (size_t b = 0; b < n / 256; b++) {
+    const float* xb = x + b * 256;
+    uint8_t* o = out + b * 176;
+    float scale[8], mins[8];
+    float max_scale = 0.f, max_min = 0.f;
+    for (int j = 0; j < 8; j++) {
+      float mn = xb[32 * j], mx = xb[32 * j];
+      for (int i = 1; i < 32; i++) {
+        mn = std::fmin(mn, xb[32 * j + i]);
+        mx = std::fmax(mx, xb[32 * j + i]);
+      }
+      if (mn > 0.f) mn = 0.f;
+      scale[j] = (mx - mn) / 31.f;
+      mins[j] = -mn;
+      max_scale = std::fmax(max_scale, scale[j]);
+      max_min = std::fmax(max_min, mins[j]);
+    }
+    put_f16(o, max_scale / 63.f);
+    put_f16(o + 2, max_min / 63.f);
+    float d = f16_to_f32((uint16_t)(o[0] | (o[1] << 8)));
+    float dmin = f16_to_f32((uint16_t)(o[2] | (o[3] << 8)));
+    uint8_t sc[8], m[8];
+    for (int j = 0; j < 8; j++) {
+      sc[j] = (uint8_t)(d > 0.f ? clampi((int)std::lrint(scale[j] / d), 0, 63) : 0);
+      m[j] = (uint8_t)(dmin > 0.f ? clampi((int)std::lrint(mins[j] / dmin), 0, 63) : 0);
+    }
+    uint8_t* s = o + 4;
+    for (int j = 0; j < 4; j++) {
+      s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+      s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+      s[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+    uint8_t q[256];
+    for (int j = 0; j < 8; j++) {
+      float dj = d * (float)sc[j], mj = dmin * (float)m[j];
+      for (int i = 0; i < 32; i++) {
+        int v = dj > 0.f ? (int)std::lrint((xb[32 * j + i] + mj) / dj) : 0;
+        q[32 * j + i] = (uint8_t)clampi(v, 0, 31);
+      }
+    }
+    uint8_t* qh = o + 16;
+    uint8_t* qs = o + 48;
+    for (int l = 0; l < 32; l++) {
+      uint8_t h = 0;
+      for (int j = 0; j < 8; j++) h |= (uint8_t)(((q[32 * j + l] >> 4) & 1) << j);
+      qh[l] = h;
+    }
+    for (int g = 0; g < 4; g++)
+      for (int l = 0; l < 32; l++) qs[32 * g + l] = (uint8_t)((q[64 * g + l] & 15) | ((q[64 * g + 32 + l] & 15) << 4));
+  }
+}
+
 // Q6_K: 16 sub-blocks of 16 with a signed 8-bit scale each.
 void quant_q6_k(const float* x, size_t n, uint8_t* out) {
   for (size_t b = 0; b < n / 256; b++) {
@@ -241,6 +296,7 @@ int rlh_quantize_row(uint32_t ty, const float* src, uint64_t n, void* dst) {
     case RLH_TYPE_Q8_0: if (n % 32) return -1; quant_q8_0(src, n, o); return 0;
     case RLH_TYPE_Q4_0: if (n % 32) return -1; quant_q4_0(src, n, o); return 0;
     case RLH_TYPE_Q4_K: if (n % 256) return -1; quant_q4_k(src, n, o); return 0;
+    case RLH_TYPE_Q5_K: if (n % 256) return -1; quant_q5_k(src, n, o); return 0;
     case RLH_TYPE_Q6_K: if (n % 256) return -1; quant_q6_k(src, n, o); return 0;
     default: return -2;
   }

@@ -100,6 +100,12 @@ def _q4km(tied, embd_type, out_type):
     return t
 
 
+def _q5km():
+    """Q5_K_M-like mix: Q5_K everywhere but attn_v / ffn_down in Q6_K; tied Q5_K embedding."""
+    return {T_ATTN_Q: Q5_K, T_ATTN_K: Q5_K, T_ATTN_V: Q6_K, T_ATTN_OUTPUT: Q5_K, T_FFN_GATE: Q5_K,
+            T_FFN_UP: Q5_K, T_FFN_DOWN: Q6_K, T_TOKEN_EMBD: Q5_K}
+
+
 def _all(ty, tied=True):
     t = {k: ty for k in (T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_OUTPUT, T_FFN_GATE, T_FFN_UP, T_FFN_DOWN,
                          T_TOKEN_EMBD)}
@@ -123,6 +129,8 @@ SPECS = {
     "tiny-q4_0": ModelSpec("tiny-q4_0", 2, 256, 512, 4, 4, 1000, True, _all(Q4_0), n_ctx=512),
     "small-q4km": ModelSpec("small-q4km", 4, 1024, 3072, 16, 8, 4096, False, _q4km(False, Q4_K, Q6_K), n_ctx=1024),
     # 8 query heads per KV head (the 32B grouping) and a long context window
+    # Q5_K matrices (no integer path in the reference: f32 products)
+    "tiny-q5km": ModelSpec("tiny-q5km", 2, 256, 512, 4, 2, 1000, True, _q5km(), n_ctx=512),
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
 }
 
@@ -174,6 +182,19 @@ def synth_tokens(seed, n, vocab, lib=None):
     return out
 
 
+class SamplingParams(ctypes.Structure):
+    """rlh_sampling_params = SamplingParams (src/sampler.rs:3-26)."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_uint32), ("top_p", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("repeat_last_n", ctypes.c_uint32),
+                ("seed", ctypes.c_uint64)]
+
+
+def sampling_params(temperature=0.7, top_k=40, top_p=0.95, repetition_penalty=1.1, repeat_last_n=64,
+                    seed=0x123456789ABCDEF0):
+    """Defaults of SamplingParams::default (sampler.rs:15-26)."""
+    return SamplingParams(temperature, top_k, top_p, repetition_penalty, repeat_last_n, seed)
+
+
 _lib = None
 
 
@@ -205,6 +226,12 @@ def load():
         "rlh_forward_into": (I32, [P, P, P, U64, U64, P]),
         "rlh_greedy_next": (I32, [P, P, ctypes.POINTER(U32)]),
         "rlh_generate_greedy": (I32, [P, P, U32, U64, P]),
+        "rlh_sampler_init": (U64, [U64]),
+        "rlh_sample": (I32, [P, U64, ctypes.POINTER(SamplingParams), P, U64, ctypes.POINTER(U64),
+                             ctypes.POINTER(U32)]),
+        "rlh_sample_next": (I32, [P, P, ctypes.POINTER(SamplingParams), P, U64, ctypes.POINTER(U64),
+                                  ctypes.POINTER(U32)]),
+        "rlh_generate": (I32, [P, P, P, U64, U64, ctypes.POINTER(SamplingParams), U32, P, ctypes.POINTER(U64)]),
         "rlh_cache_set_debug": (I32, [P, I32]),
         "rlh_debug_layer_hidden": (I32, [P, I32, P, U64]),
         "rlh_cache_read_kv": (I32, [P, I32, I32, U64, P]),
@@ -226,6 +253,22 @@ def load():
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+class Sampler:
+    """Sampler (src/sampler.rs:29-163) over host logits."""
+
+    def __init__(self, seed):
+        self.lib = load()
+        self.state = ctypes.c_uint64(self.lib.rlh_sampler_init(seed))
+
+    def sample(self, logits, params, recent):
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        r = np.ascontiguousarray(recent, dtype=np.uint32)
+        t = ctypes.c_uint32()
+        check(self.lib.rlh_sample(lg.ctypes.data, len(lg), ctypes.byref(params), r.ctypes.data, len(r),
+                                  ctypes.byref(self.state), ctypes.byref(t)))
+        return t.value
 
 
 class RlhError(RuntimeError):
@@ -310,6 +353,15 @@ class Cache:
         out = np.empty(n_steps + 1, dtype=np.uint32)
         check(self.lib.rlh_generate_greedy(self.model.h, self.h, first, n_steps, out.ctypes.data))
         return out
+
+    def generate(self, prompt, max_new, params, eos):
+        """Model::generate (src/model.rs:741-776) on the device."""
+        toks = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(1, max_new), dtype=np.uint32)
+        n = ctypes.c_uint64()
+        check(self.lib.rlh_generate(self.model.h, self.h, toks.ctypes.data, len(toks), max_new,
+                                    ctypes.byref(params), eos, out.ctypes.data, ctypes.byref(n)))
+        return out[: n.value].copy()
 
     def set_debug(self, on):
         check(self.lib.rlh_cache_set_debug(self.h, 1 if on else 0))

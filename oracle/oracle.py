@@ -215,6 +215,14 @@ class OracleCache:
         arr = np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_float)), shape=(n_pos * kvd,))
         return arr.reshape(n_pos, kvd).copy()
 
+    def generate(self, prompt, max_new, params, eos, mode=MODE_BATCH_INT):
+        """Model::generate (model.rs:741-776); returns the generated tokens."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(max(1, max_new), np.uint32)
+        n = self.lib.orc_generate(self.model.h, self.h, p.ctypes.data, len(p), max_new, ctypes.byref(params), eos,
+                                  out.ctypes.data, mode)
+        return out[:n].copy()
+
     def bench(self, prompt, n_gen, mode=MODE_DEFAULT, warmup=True):
         """main.rs cmd_bench protocol; returns (BenchResult, tokens)."""
         res = BenchResult()

@@ -1,7 +1,7 @@
 """Shared input generators for the parity tests."""
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
 BLOCK = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 12: (256, 144), 13: (256, 176),
          14: (256, 210), 0: (1, 4), 1: (1, 2), 30: (1, 2)}
 
@@ -35,7 +35,7 @@ def random_blocks(ty, nblocks, rng, scale_lo=0.01, scale_hi=1.0):
         raw[:, col + 1] = (h >> 8).astype(np.uint8)
 
     n = nblocks
-    if ty == Q4_K:
+    if ty in (Q4_K, Q5_K):
         put(0, rng.uniform(scale_lo, scale_hi, n) / 64)
         put(2, rng.uniform(scale_lo, scale_hi, n) / 64)
     elif ty == Q6_K:

@@ -120,6 +120,31 @@ def test_generate_greedy_matches_cpu_tokens(name):
     oc.close()
 
 
+@pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
+def test_generate_sampled_matches_cpu(name):
+    """Model::generate with temperature / top-k / top-p / repetition penalty
+    (the SamplingParams defaults, sampler.rs:15-26): same tokens as the oracle,
+    and generation stops at EOS."""
+    print(f"sampled generate {name}", flush=True)
+    spec, tensors, m, om = _get(name)
+    prompt = rlh.synth_tokens(31, 10, spec.vocab)
+    c = m.new_cache(64)
+    oc = om.new_cache(64)
+    params = rlh.sampling_params(seed=0xC0FFEE)
+    oparams = oracle.SamplingParams(0.7, 40, 0.95, 1.1, 64, 0xC0FFEE)
+    eos = spec.vocab + 7  # never sampled: full length
+    toks = c.generate(prompt, 24, params, eos)
+    ref = oc.generate(prompt, 24, oparams, eos)
+    assert list(map(int, toks)) == list(map(int, ref))
+    assert len(toks) == 24 and c.len == len(prompt) + 24
+    eos = int(toks[5])
+    first = int(np.flatnonzero(toks == eos)[0])
+    toks2 = c.generate(prompt, 24, params, eos)
+    assert list(map(int, toks2)) == list(map(int, toks[:first]))
+    c.close()
+    oc.close()
+
+
 def test_forward_errors():
     spec, tensors, m, om = _get("tiny-q4km")
     c = m.new_cache(16)

@@ -1,0 +1,73 @@
+"""The library's host sampler (rlh_sample, src/sampler.rs:29-163) against the
+oracle's sampler and the reference's own sampler tests. CPU only."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import rlh
+
+
+def rp(temp=0.0, top_k=0, top_p=1.0, pen=1.0, last_n=64, seed=1):
+    return rlh.SamplingParams(temp, top_k, top_p, pen, last_n, seed)
+
+
+def one(logits, p, recent, seed=1):
+    return rlh.Sampler(seed).sample(logits, p, recent)
+
+
+def test_repetition_penalty_applies_once_per_distinct_token():
+    """sampler.rs:181-189."""
+    assert one([10.0, 1.0], rp(pen=2.0, last_n=64), [0, 0, 0, 0]) == 0
+
+
+def test_repetition_penalty_respects_window():
+    """sampler.rs:191-199."""
+    assert one([10.0, 1.0], rp(pen=20.0, last_n=2), [7, 7, 0]) == 1
+    assert one([10.0, 1.0], rp(pen=20.0, last_n=2), [0, 7, 7]) == 0
+
+
+def test_repetition_penalty_disabled_is_identity():
+    """sampler.rs:201-206."""
+    assert one([10.0, 1.0], rp(pen=1.0, last_n=64), [0, 0, 0]) == 0
+
+
+def test_greedy_ties_and_empty():
+    assert one([1.0, 3.0, 3.0, 2.0], rp(), []) == 1
+    assert one([], rp(temp=0.7), []) == 0
+    assert rlh.load().rlh_sampler_init(6) == 7
+
+
+@pytest.mark.parametrize("temp", [0.0, 0.7, 1.3])
+@pytest.mark.parametrize("top_k", [0, 1, 40, 5000])
+@pytest.mark.parametrize("top_p", [1.0, 0.95, 0.3])
+@pytest.mark.parametrize("pen,last_n", [(1.0, 64), (1.1, 64), (0.8, 0), (1.3, 8)])
+def test_matches_oracle_sequence(temp, top_k, top_p, pen, last_n):
+    """A sequence of draws with one RNG state, against the oracle sampler on
+    distinct logits (where the reference's top-k order is fully determined)."""
+    rng = np.random.default_rng(hash((temp, top_k, top_p, pen, last_n)) % 2 ** 32)
+    n = 20000
+    lib = oracle.load()
+    op = oracle.SamplingParams(temp, top_k, top_p, pen, last_n, 99)
+    p = rp(temp, top_k, top_p, pen, last_n, 99)
+    os_ = lib.orc_sampler_create(99)
+    ours = rlh.Sampler(99)
+    recent = list(rng.integers(0, n, 100))
+    for step in range(12):
+        logits = rng.permutation(np.linspace(-12.0, 9.0, n).astype(np.float32))
+        assert len(np.unique(logits)) == n
+        r = np.asarray(recent, np.uint32)
+        want = lib.orc_sampler_sample(os_, logits.ctypes.data, n, ctypes.byref(op), r.ctypes.data, len(r))
+        got = ours.sample(logits, p, recent)
+        assert got == want, f"step {step}"
+        recent.append(got)
+    lib.orc_sampler_destroy(os_)
+
+
+def test_null_arguments_rejected():
+    lib = rlh.load()
+    t = ctypes.c_uint32()
+    st = ctypes.c_uint64(1)
+    p = rp()
+    assert lib.rlh_sample(None, 4, ctypes.byref(p), None, 0, ctypes.byref(st), ctypes.byref(t)) == rlh.RLH_EINVAL
