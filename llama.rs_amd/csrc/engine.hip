@@ -1243,7 +1243,6 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   // rather than from the 256 MB last-level cache a re-launched matrix would
   // sit in.
   std::vector<MvPlan> plans;
-  const uint64_t qd = (uint64_t)cfg.n_head * cfg.head_dim;
   for (uint32_t l = 0; l < (global ? 1u : cfg.n_layer); l++) {
     MvPlan p;
     if (global) {
@@ -1265,17 +1264,16 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
       } else {
         const DevTensor* t = find_matrix(m, kind, (int)l);
         if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
-        const uint64_t cols = t->cols;
-        if (cols == cfg.n_embd)
-          mv_plan_init_norm(p, (uint32_t)cols, c->x, L.attn_norm.p, cfg.rms_eps);
-        else if (cols == qd) {
-          mv_plan_init(p, (uint32_t)cols, c->act_q);
+        const uint32_t cols = (uint32_t)t->cols;
+        if (kind == RLH_T_ATTN_OUTPUT) {  // attention output in, as in decode
+          mv_plan_init(p, cols, c->act_q);
           mv_plan_set_f32(p, c->attn);
-        } else if (cols == cfg.n_ff) {
-          mv_plan_init(p, (uint32_t)cols, c->act_f);
+        } else if (kind == RLH_T_FFN_DOWN) {  // silu(g)*u in
+          mv_plan_init(p, cols, c->act_f);
           mv_plan_set_f32(p, c->g);
-        } else
-          return fail(RLH_EINVAL, "matrix width matches no activation buffer");
+        } else {  // rmsnorm(x) in (attn_k / attn_v alone)
+          mv_plan_init_norm(p, cols, c->x, L.attn_norm.p, cfg.rms_eps);
+        }
         mv_plan_add(p, t->dm, c->logits, nullptr);
       }
     }
