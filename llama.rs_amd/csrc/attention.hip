@@ -230,7 +230,6 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   __shared__ int s_on;
   __shared__ uint64_t tab_g[32];
   lu64* tab = (lu64*)tab_g;
-  exp_tab_to_lds(tab);
   lfloat* e = (lfloat*)lds_generic;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t t = a.pos0[0] + blockIdx.y + 1;
@@ -243,6 +242,7 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
     e[j] = s;
     mx = fmaxf(mx, s);
   }
+  exp_tab_to_lds(tab);  // after the row loads: its store waits for its load
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if (lane == 0) red[wave] = mx;
@@ -252,45 +252,8 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   if (x0 != x0) mx = x0;
   for (uint32_t j = tid; j < t; j += 256) e[j] = expf_glibc_t(e[j] - mx, tab);
   __syncthreads();
-  if (tid == 0) {  // the sequential sum of softmax_inplace, 16 values read ahead
-    float sum = 0.0f;
-    const lf32x4* e4 = (const lf32x4*)e;
-    const uint32_t nq = t / 4;
-    uint32_t q = 0;
-    if (nq >= 4) {
-      f32x4_t v[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = e4[i];
-      for (q = 4; q + 4 <= nq; q += 4) {
-        f32x4_t vn[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) vn[i] = e4[q + i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          sum = sum + v[i].x;
-          sum = sum + v[i].y;
-          sum = sum + v[i].z;
-          sum = sum + v[i].w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vn[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        sum = sum + v[i].x;
-        sum = sum + v[i].y;
-        sum = sum + v[i].z;
-        sum = sum + v[i].w;
-      }
-    }
-    for (; q < nq; q++) {
-      const f32x4_t v = e4[q];
-      sum = sum + v.x;
-      sum = sum + v.y;
-      sum = sum + v.z;
-      sum = sum + v.w;
-    }
-    for (uint32_t j = 4 * nq; j < t; j++) sum = sum + e[j];
+  if (tid == 0) {  // the sequential sum of softmax_inplace
+    const float sum = seq_sum_lds(e, t);
     s_on = sum > 0.0f;
     s_inv = 1.0f / sum;
   }
@@ -357,48 +320,9 @@ __global__ void __launch_bounds__(512) k_attn_pv_dec(AttnArgs a) {
   for (uint32_t k = 0; k < nch; k++) {
     if (k + 1 < nch) load(k + 1);
     if (chain) {
-      const lf32x4* vb = (const lf32x4*)(vs + (k & 1) * 32 * CS + dd * CS);
-      const lf32x4* pb = (const lf32x4*)(ps + (k & 1) * kAttnMaxGroup * CS + hl * CS);
       const uint32_t rem = t - k * kDecChunk;
       const uint32_t jn = rem < (uint32_t)kDecChunk ? rem : (uint32_t)kDecChunk;
-      const uint32_t nq = jn / 4;
-      uint32_t q = 0;
-      if (nq >= 4) {  // 16 positions in flight while the previous 16 are chained
-        f32x4_t v[4], p[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vb[i], p[i] = pb[i];
-        for (q = 4; q + 4 <= nq; q += 4) {
-          f32x4_t vn[4], pn[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) vn[i] = vb[q + i], pn[i] = pb[q + i];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            o = p[i].x * v[i].x + o;
-            o = p[i].y * v[i].y + o;
-            o = p[i].z * v[i].z + o;
-            o = p[i].w * v[i].w + o;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; i++) v[i] = vn[i], p[i] = pn[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          o = p[i].x * v[i].x + o;
-          o = p[i].y * v[i].y + o;
-          o = p[i].z * v[i].z + o;
-          o = p[i].w * v[i].w + o;
-        }
-      }
-      for (; q < nq; q++) {
-        const f32x4_t v = vb[q], p = pb[q];
-        o = p.x * v.x + o;
-        o = p.y * v.y + o;
-        o = p.z * v.z + o;
-        o = p.w * v.w + o;
-      }
-      const lfloat* vs1 = (const lfloat*)vb;
-      const lfloat* ps1 = (const lfloat*)pb;
-      for (uint32_t jj = 4 * nq; jj < jn; jj++) o = ps1[jj] * vs1[jj] + o;
+      o = seq_saxpy_lds(ps + (k & 1) * kAttnMaxGroup * CS + hl * CS, vs + (k & 1) * 32 * CS + dd * CS, jn, o);
     }
     if (k + 1 < nch) store(k + 1);
     __syncthreads();
@@ -428,7 +352,6 @@ __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
   __shared__ uint64_t tab_g[32];
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   lu64* tab = (lu64*)tab_g;
-  exp_tab_to_lds(tab);
   lfloat* vs = (lfloat*)vs_g;
   lfloat* e = (lfloat*)lds_generic;
   const int G = a.H / a.KVH;
@@ -473,9 +396,7 @@ __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
     }
   };
   load(0);
-  // the score copies are older than the 4 V loads: wait until at most those
-  // 4 are outstanding (vmcnt 4, expcnt and lgkmcnt not waited on)
-  __builtin_amdgcn_s_waitcnt(0x0F74);
+  exp_tab_to_lds(tab);  // after the bulk loads: its store waits for its load
   __syncthreads();
   // softmax_inplace of the G rows (ops.rs:398-419); head hg is taken by
   // TPH = 64 * floor(8 / G) threads
@@ -501,46 +422,8 @@ __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
     for (uint32_t j = lt; j < t; j += TPH) eh[j] = expf_glibc_t(eh[j] - m, tab);
   }
   __syncthreads();
-  if (tid < G) {  // the G sequential sums, one lane each, 16 values read ahead
-    const lf32x4* e4 = (const lf32x4*)(e + tid * RS);
-    float sum = 0.0f;
-    const uint32_t nq = t / 4;
-    uint32_t q = 0;
-    if (nq >= 4) {
-      f32x4_t v[4];
-#pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = e4[i];
-      for (q = 4; q + 4 <= nq; q += 4) {
-        f32x4_t vn[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) vn[i] = e4[q + i];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          sum = sum + v[i].x;
-          sum = sum + v[i].y;
-          sum = sum + v[i].z;
-          sum = sum + v[i].w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vn[i];
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        sum = sum + v[i].x;
-        sum = sum + v[i].y;
-        sum = sum + v[i].z;
-        sum = sum + v[i].w;
-      }
-    }
-    for (; q < nq; q++) {
-      const f32x4_t v = e4[q];
-      sum = sum + v.x;
-      sum = sum + v.y;
-      sum = sum + v.z;
-      sum = sum + v.w;
-    }
-    const lfloat* e1 = e + tid * RS;
-    for (uint32_t j = 4 * nq; j < t; j++) sum = sum + e1[j];
+  if (tid < G) {  // the G sequential sums side by side, one lane each
+    const float sum = seq_sum_lds(e + tid * RS, t);
     s_on[tid] = sum > 0.0f;
     s_inv[tid] = 1.0f / sum;
   }
@@ -557,48 +440,9 @@ __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
   for (uint32_t k = 0; k < nch; k++) {
     if (k + 1 < nch) load(k + 1);
     if (chain) {
-      const lf32x4* vb = (const lf32x4*)(vs + (k & 1) * 32 * CS + dd * CS);
-      const lf32x4* pb = (const lf32x4*)(e + hl * RS + k * kDecChunk);
       const uint32_t rem = t - k * kDecChunk;
       const uint32_t jn = rem < (uint32_t)kDecChunk ? rem : (uint32_t)kDecChunk;
-      const uint32_t nq = jn / 4;
-      uint32_t q = 0;
-      if (nq >= 4) {  // 16 positions in flight while the previous 16 are chained
-        f32x4_t v[4], p[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = vb[i], p[i] = pb[i];
-        for (q = 4; q + 4 <= nq; q += 4) {
-          f32x4_t vn[4], pn[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) vn[i] = vb[q + i], pn[i] = pb[q + i];
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            o = p[i].x * v[i].x + o;
-            o = p[i].y * v[i].y + o;
-            o = p[i].z * v[i].z + o;
-            o = p[i].w * v[i].w + o;
-          }
-#pragma unroll
-          for (int i = 0; i < 4; i++) v[i] = vn[i], p[i] = pn[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          o = p[i].x * v[i].x + o;
-          o = p[i].y * v[i].y + o;
-          o = p[i].z * v[i].z + o;
-          o = p[i].w * v[i].w + o;
-        }
-      }
-      for (; q < nq; q++) {
-        const f32x4_t v = vb[q], p = pb[q];
-        o = p.x * v.x + o;
-        o = p.y * v.y + o;
-        o = p.z * v.z + o;
-        o = p.w * v.w + o;
-      }
-      const lfloat* vs1 = (const lfloat*)vb;
-      const lfloat* ps1 = (const lfloat*)pb;
-      for (uint32_t jj = 4 * nq; jj < jn; jj++) o = ps1[jj] * vs1[jj] + o;
+      o = seq_saxpy_lds(e + hl * RS + k * kDecChunk, vs + (k & 1) * 32 * CS + dd * CS, jn, o);
     }
     if (k + 1 < nch) store(k + 1);
     __syncthreads();

@@ -305,26 +305,8 @@ struct MI<RLH_TYPE_Q5_K> {
   }
 };
 
-// In-order sum of n terms (the per-row f32 chain); 32 terms per batch of
-// LDS reads so that the reads overlap the dependent adds.
-__device__ __forceinline__ float chain(const lfloat* t, uint32_t n) {
-  float acc = 0.0f;
-  uint32_t k = 0;
-  for (; k + 32 <= n; k += 32) {
-    f32x4_t v[8];
-#pragma unroll
-    for (int q = 0; q < 8; q++) v[q] = *(const lf32x4*)(t + k + 4 * q);
-#pragma unroll
-    for (int q = 0; q < 8; q++) {
-      acc = acc + v[q].x;
-      acc = acc + v[q].y;
-      acc = acc + v[q].z;
-      acc = acc + v[q].w;
-    }
-  }
-  for (; k < n; k++) acc = acc + t[k];
-  return acc;
-}
+// In-order sum of n terms (the per-row f32 chain).
+__device__ __forceinline__ float chain(const lfloat* t, uint32_t n) { return seq_sum_lds(t, n); }
 
 // Asynchronous copies HBM -> LDS with global_load_lds (no registers
 // involved, so they overlap the weight loads already in flight). lds_dma4:
@@ -374,18 +356,30 @@ __device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& 
 // written) for the 32 FMA chains of the sum of squares, and each group of 8
 // threads quantizes one 32-value block straight into the LDS activation.
 // Needs blockDim.x >= 256 (at most kV float4 per thread).
-__device__ __forceinline__ void stage_norm(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* misc) {
-  constexpr int kV = kMvMaxNormCols / 4 / 256;
+constexpr int kNormV = kMvMaxNormCols / 4 / 256;  // float4 of the row per thread
+struct NormRegs {
+  float4 xr[kNormV], wr[kNormV];
+};
+
+// The row and norm weight loads, issued before the first weight tiles so
+// that they are not queued behind them. Unconditional (index clamped into
+// the row): a load under a branch gets a wait for every load before it.
+__device__ __forceinline__ void norm_load(const MvLaunch& L, NormRegs& r) {
   const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
-  // unconditional loads (index clamped into the row): a load under a branch
-  // gets a wait for every load before it
-  float4 xr[kV], wr[kV];
 #pragma unroll
-  for (int k = 0; k < kV; k++) {
+  for (int k = 0; k < kNormV; k++) {
     const uint32_t i = min(tid + NT * k, n4 - 1);
-    xr[k] = ld_gf4(L.nx + 4 * i);
-    wr[k] = ld_gf4(L.nw + 4 * i);
+    r.xr[k] = ld_gf4(L.nx + 4 * i);
+    r.wr[k] = ld_gf4(L.nw + 4 * i);
   }
+}
+
+__device__ __forceinline__ void stage_norm(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* misc,
+                                           const NormRegs& nr) {
+  constexpr int kV = kNormV;
+  const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
+  const float4* xr = nr.xr;
+  const float4* wr = nr.wr;
 #pragma unroll
   for (int k = 0; k < kV; k++) {
     const uint32_t i = tid + NT * k;
@@ -440,7 +434,7 @@ __device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
 // up share type and tiling).
 template <uint32_t TY, int NM>
 __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc,
-                                         const lu64* exp_tab) {
+                                         lu64* exp_tab) {
   using I = MI<TY>;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
@@ -483,8 +477,14 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   if (NM == 1 && g.resid && wave == 0) rsd = ld_gf(g.resid + row0 + min(lane, nrows - 1));
   typename I::W wa[NM], wb[kPP ? NM : 1];
   uint32_t t = wave;
+  NormRegs nr;
+  if (L.nx) norm_load(L, nr);
+  __builtin_amdgcn_sched_barrier(0);  // keep the row loads ahead of the weight tiles
   if (t < ntiles) load(wa, t);
-  if (L.nx) stage_norm(L, la, region, misc);
+  // silu's expf table to LDS, after the bulk loads are issued (its store
+  // waits for its load); read after the prologue's barriers
+  if (NM == 2) exp_tab_to_lds(exp_tab);
+  if (L.nx) stage_norm(L, la, region, misc, nr);
   else stage_activation(L, la);
   if (kPP) {
     for (; t < ntiles; t += 2 * nwaves) {
@@ -551,7 +551,6 @@ __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
   __shared__ uint64_t tab_g[NM == 2 ? 32 : 1];
   lfloat* lds = (lfloat*)lds_generic;
   lfloat* misc = (lfloat*)misc_generic;
-  if (NM == 2) exp_tab_to_lds((lu64*)tab_g);  // silu's expf table (read after the prologue's barriers)
   // segment of this block, selected without indexing the argument array
   // (a dynamic index would copy the kernel argument to private memory)
   MvSeg g = L.seg[0];

@@ -79,6 +79,105 @@ __device__ __forceinline__ float expf_glibc_t(float x, Tab tab) {
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
 
+// ---------------------------------------------------------------------------
+// Ordered f32 chains over LDS data, the reference's sequential loops:
+//   seq_sum_lds   s = ((0 + x0) + x1) + ...            (the softmax sum,
+//                 ops.rs:408-412; the per-row term chain of the matvec)
+//   seq_saxpy_lds o = p_j * v_j + o for j in order     (saxpy, simd.rs:674-691)
+// The chain is latency bound (one dependent add per element), so the LDS
+// reads run one batch ahead in two register sets used alternately; no set
+// is copied into the other, which would make every batch wait for the reads
+// just issued. x, p and v are 16-byte aligned.
+// ---------------------------------------------------------------------------
+typedef float f32x4d_t __attribute__((ext_vector_type(4)));
+typedef RLH_LDS f32x4d_t lf32x4d;
+
+__device__ __forceinline__ float seq_sum_lds(const RLH_LDS float* x, uint32_t n) {
+  const lf32x4d* x4 = (const lf32x4d*)x;
+  const uint32_t nq = n / 4, nb = nq / 8;  // float4s, full batches of 8
+  float s = 0.0f;
+  if (nb) {
+    // the next batch's reads are unconditional (index clamped to the last
+    // full batch): with a branch around them the compiler assumes either
+    // path and waits for the newest reads before using the older ones
+    f32x4d_t a[8], b[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) a[i] = x4[i];
+    for (uint32_t bi = 0;; bi += 2) {
+      const uint32_t q1 = 8 * min(bi + 1, nb - 1);
+#pragma unroll
+      for (int i = 0; i < 8; i++) b[i] = x4[q1 + i];
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the adds
+#pragma unroll
+      for (int i = 0; i < 8; i++) s = (((s + a[i].x) + a[i].y) + a[i].z) + a[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+      if (bi + 1 >= nb) break;
+      const uint32_t q2 = 8 * min(bi + 2, nb - 1);
+#pragma unroll
+      for (int i = 0; i < 8; i++) a[i] = x4[q2 + i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) s = (((s + b[i].x) + b[i].y) + b[i].z) + b[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+      if (bi + 2 >= nb) break;
+    }
+  }
+  for (uint32_t q = 8 * nb; q < nq; q++) {
+    const f32x4d_t v = x4[q];
+    s = (((s + v.x) + v.y) + v.z) + v.w;
+  }
+  for (uint32_t j = 4 * nq; j < n; j++) s = s + x[j];
+  return s;
+}
+
+__device__ __forceinline__ float seq_saxpy_lds(const RLH_LDS float* p, const RLH_LDS float* v, uint32_t n, float o) {
+  const lf32x4d* p4 = (const lf32x4d*)p;
+  const lf32x4d* v4 = (const lf32x4d*)v;
+  const uint32_t nq = n / 4, nb = nq / 4;  // float4s, full batches of 4 (16 positions)
+  if (nb) {
+    f32x4d_t pa[4], va[4], pb[4], vb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pa[i] = p4[i], va[i] = v4[i];
+    for (uint32_t bi = 0;; bi += 2) {
+      const uint32_t q1 = 4 * min(bi + 1, nb - 1);
+#pragma unroll
+      for (int i = 0; i < 4; i++) pb[i] = p4[q1 + i], vb[i] = v4[q1 + i];
+      __builtin_amdgcn_sched_barrier(0);  // the reads stay ahead of the chain
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o = pa[i].x * va[i].x + o;
+        o = pa[i].y * va[i].y + o;
+        o = pa[i].z * va[i].z + o;
+        o = pa[i].w * va[i].w + o;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (bi + 1 >= nb) break;
+      const uint32_t q2 = 4 * min(bi + 2, nb - 1);
+#pragma unroll
+      for (int i = 0; i < 4; i++) pa[i] = p4[q2 + i], va[i] = v4[q2 + i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        o = pb[i].x * vb[i].x + o;
+        o = pb[i].y * vb[i].y + o;
+        o = pb[i].z * vb[i].z + o;
+        o = pb[i].w * vb[i].w + o;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (bi + 2 >= nb) break;
+    }
+  }
+  for (uint32_t q = 4 * nb; q < nq; q++) {
+    const f32x4d_t a = p4[q], b = v4[q];
+    o = a.x * b.x + o;
+    o = a.y * b.y + o;
+    o = a.z * b.z + o;
+    o = a.w * b.w + o;
+  }
+  for (uint32_t j = 4 * nq; j < n; j++) o = p[j] * v[j] + o;
+  return o;
+}
+
 // LDS copy of kExp2Tab: every thread of the block calls it; visible to the
 // block after the next barrier.
 typedef RLH_LDS uint64_t lu64;
