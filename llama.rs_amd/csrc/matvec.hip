@@ -14,7 +14,7 @@
 //    every load instruction reads 1 KB of HBM while the scale unpacking and
 //    address arithmetic are paid once per 256 weights.
 //  * The activation is a Q8 row in HBM (Q8Row, simd.rs:88-101), staged into
-//    LDS with global_load_lds while the first weights are already in flight.
+//    LDS with global_load_lds issued ahead of the first weights.
 //    Q8 super-blocks are stored in LDS with a 16-byte pad so that lanes on
 //    different super-blocks hit different banks.
 //  * Every item writes its terms into the block's LDS tile [row][term]; after
@@ -59,13 +59,29 @@ __device__ __forceinline__ const RLH_LDS int8_t* qblk(const LAct& a, uint32_t b)
   return a.qs + (b >> 3) * kSbStride + (b & 7) * 32;
 }
 __device__ __forceinline__ u32x4_t lds_u4(const RLH_LDS int8_t* p) { return *(const lu32x4*)p; }
-__device__ __forceinline__ u32x4_t gl_u4(const void* p) { return *(const RLH_GLOBAL u32x4_t*)p; }
+// Weight loads: every weight is read once per token, so the loads carry the
+// non-temporal hint (nt); measured faster than ordinary loads on every shape.
+__device__ __forceinline__ u32x4_t gl_u4(const void* p) {
+  return __builtin_nontemporal_load((const RLH_GLOBAL u32x4_t*)p);
+}
 
 __device__ __forceinline__ int dot16(u32x4_t w, u32x4_t a, int acc) {
   acc = sdot4(w.x, a.x, acc);
   acc = sdot4(w.y, a.y, acc);
   acc = sdot4(w.z, a.z, acc);
   return sdot4(w.w, a.w, acc);
+}
+
+// Makes a tile's weight registers opaque at the start of its terms: the
+// unpacking (nibble masks, scale shifts) depends only on the weights, and
+// without this the compiler may move it next to the loads of the tile, where
+// it waits for the data that was meant to stream in behind other work.
+template <class W>
+__device__ __forceinline__ void weights_ready(W& r) {
+  static_assert(sizeof(W) % 16 == 0, "item registers are whole 16-byte loads");
+  u32x4_t* p = reinterpret_cast<u32x4_t*>(&r);
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(W) / 16); i++) asm volatile("" : "+v"(p[i]));
 }
 
 // ---- work items: one super-block of one row ---------------------------------
@@ -75,6 +91,7 @@ struct MI;
 template <>
 struct MI<RLH_TYPE_Q4_K> {
   static constexpr uint32_t kT = 4;
+  static constexpr int kLoads = 9;  // vector-memory loads per item
   struct W {
     u32x4_t hdr, q[8];
   };
@@ -130,9 +147,10 @@ struct MI<RLH_TYPE_Q4_K> {
 template <>
 struct MI<RLH_TYPE_Q6_K> {
   static constexpr uint32_t kT = 16;
+  static constexpr int kLoads = 14;
   struct W {
     u32x4_t ql[8], qh[4], sc;
-    uint32_t d;
+    u32x4_t d;  // .x = the f16 scale (the other lanes unused)
   };
   __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
 #pragma unroll
@@ -140,11 +158,11 @@ struct MI<RLH_TYPE_Q6_K> {
 #pragma unroll
     for (int k = 0; k < 4; k++) r.qh[k] = gl_u4(tile + (8 + k) * 1024 + lane * 16);
     r.sc = gl_u4(tile + 12 * 1024 + lane * 16);
-    r.d = ld_g2(tile + 13 * 1024 + lane * 2);
+    r.d = u32x4_t{ld_g2(tile + 13 * 1024 + lane * 2), 0u, 0u, 0u};
   }
   __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
     const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
-    const float d = f16_to_f32(r.d);
+    const float d = f16_to_f32(r.d.x);
 #pragma unroll
     for (int h = 0; h < 2; h++) {
       const uint32_t wlo = h ? r.sc.z : r.sc.x, whi = h ? r.sc.w : r.sc.y;  // the half's 8 scale bytes
@@ -185,6 +203,7 @@ struct MI<RLH_TYPE_Q6_K> {
 template <>
 struct MI<RLH_TYPE_Q8_0> {
   static constexpr uint32_t kT = 8;
+  static constexpr int kLoads = 17;
   struct W {
     u32x4_t q[16], dv;
   };
@@ -213,6 +232,7 @@ struct MI<RLH_TYPE_Q8_0> {
 template <>
 struct MI<RLH_TYPE_Q4_0> {
   static constexpr uint32_t kT = 8;
+  static constexpr int kLoads = 9;
   struct W {
     u32x4_t q[8], dv;
   };
@@ -249,6 +269,7 @@ struct MI<RLH_TYPE_Q4_0> {
 template <>
 struct MI<RLH_TYPE_Q5_K> {
   static constexpr uint32_t kT = 1;
+  static constexpr int kLoads = 11;
   struct W {
     u32x4_t hdr, qh[2], q[8];
   };
@@ -321,11 +342,12 @@ __device__ __forceinline__ void lds_dma4(RLH_LDS void* dst, const void* src, uin
   }
 }
 
-// Stages the Q8 activation row (HBM, Q8Row layout) into LDS. The quants go
-// to the padded layout (17 slots of 16 bytes per 256 values, the 17th empty):
-// lane i of a copy fills slot s0 + i, so its source is chosen per slot and
-// the pad slots are simply masked off.
-__device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& la) {
+// Stages the Q8 activation row (HBM, Q8Row layout) into LDS by DMA. The
+// quants go to the padded layout (17 slots of 16 bytes per 256 values, the
+// 17th empty): lane i of a copy fills slot s0 + i, so its source is chosen per
+// slot and the pad slots are simply masked off. act_finish runs after the
+// copies have landed (wait_vmcnt) and turns the 16-value sums into floats.
+__device__ __forceinline__ void act_dma(const MvLaunch& L, const LAct& la) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const uint32_t cols = L.cols, nsb = cols >> 8, nb = cols >> 5, nslots = nsb * 17;
   for (uint32_t s0 = wave * 64; s0 < nslots; s0 += nw * 64) {
@@ -341,77 +363,65 @@ __device__ __forceinline__ void stage_activation(const MvLaunch& L, const LAct& 
     for (uint32_t sb = wave; sb < nsb; sb += nw)
       __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.xf + sb * 256 + lane * 4),
                                        (RLH_LDS void*)(la.xf + sb * kXfStride), 16, 0, 0);
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's copies (and first weights) have landed
-  __syncthreads();
-  for (uint32_t i = tid; i < 2 * nb; i += blockDim.x) {
+}
+
+__device__ __forceinline__ void act_finish(const MvLaunch& L, const LAct& la) {
+  const uint32_t nb = L.cols >> 5;
+  lds_barrier();
+  for (uint32_t i = threadIdx.x; i < 2 * nb; i += blockDim.x) {
     const int v = ((RLH_LDS int32_t*)la.s16x32)[i];
     la.s16x32[i] = 32.0f * (float)v;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // Norm input: every block computes quantize_q8(rmsnorm(x, w)) itself
-// (k_rmsnorm_q8's arithmetic): the row and the weights go to registers in
-// one batch of loads, the row to LDS (`xs`, free until the terms are
-// written) for the 32 FMA chains of the sum of squares, and each group of 8
-// threads quantizes one 32-value block straight into the LDS activation.
-// Needs blockDim.x >= 256 (at most kV float4 per thread).
-constexpr int kNormV = kMvMaxNormCols / 4 / 256;  // float4 of the row per thread
-struct NormRegs {
-  float4 xr[kNormV], wr[kNormV];
-};
-
-// The row and norm weight loads, issued before the first weight tiles so
-// that they are not queued behind them. Unconditional (index clamped into
-// the row): a load under a branch gets a wait for every load before it.
-__device__ __forceinline__ void norm_load(const MvLaunch& L, NormRegs& r) {
-  const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
-#pragma unroll
-  for (int k = 0; k < kNormV; k++) {
-    const uint32_t i = min(tid + NT * k, n4 - 1);
-    r.xr[k] = ld_gf4(L.nx + 4 * i);
-    r.wr[k] = ld_gf4(L.nw + 4 * i);
+// (k_rmsnorm_q8's arithmetic). norm_dma copies the row and the norm weights
+// into LDS (xs, ws: the term tiles, free until the terms are written);
+// norm_finish, after the copies have landed, runs the 32 FMA chains of the
+// sum of squares in wave 0, then each group of 8 threads quantizes one
+// 32-value block straight into the LDS activation.
+__device__ __forceinline__ void norm_dma(const MvLaunch& L, lfloat* xs, lfloat* ws) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const uint32_t nbytes = L.cols * 4;  // a multiple of 1024
+  for (uint32_t off = wave * 1024; off < nbytes; off += nw * 1024) {
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)L.nx + off + lane * 16),
+                                     (RLH_LDS void*)((RLH_LDS uint8_t*)xs + off), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)L.nw + off + lane * 16),
+                                     (RLH_LDS void*)((RLH_LDS uint8_t*)ws + off), 16, 0, 0);
   }
 }
 
-__device__ __forceinline__ void stage_norm(const MvLaunch& L, const LAct& la, lfloat* xs, lfloat* misc,
-                                           const NormRegs& nr) {
-  constexpr int kV = kNormV;
+__device__ __forceinline__ void norm_finish(const MvLaunch& L, const LAct& la, const lfloat* xs, const lfloat* ws,
+                                            lfloat* misc) {
   const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
-  const float4* xr = nr.xr;
-  const float4* wr = nr.wr;
-#pragma unroll
-  for (int k = 0; k < kV; k++) {
-    const uint32_t i = tid + NT * k;
-    if (i < n4) *(lf32x4*)(xs + 4 * i) = f32x4_t{xr[k].x, xr[k].y, xr[k].z, xr[k].w};
-  }
-  __syncthreads();
+  lds_barrier();
   if (tid < 64) {
     const float ss = rms_sumsq_lds(xs, (int)L.cols);
     if (tid == 0) misc[0] = 1.0f / sqrtf(ss / (float)L.cols + L.eps);
   }
-  __syncthreads();
+  lds_barrier();
   const float s = misc[0];
-#pragma unroll
-  for (int k = 0; k < kV; k++) {
-    const uint32_t i = tid + NT * k;
-    if (i < n4) {  // n4 and NT are multiples of 8: whole 8-lane groups
-      const float v0 = (xr[k].x * s) * wr[k].x, v1 = (xr[k].y * s) * wr[k].y;
-      const float v2 = (xr[k].z * s) * wr[k].z, v3 = (xr[k].w * s) * wr[k].w;
-      if (L.need_xf) *(lf32x4*)(la.xf + (i >> 6) * kXfStride + 4 * (i & 63)) = f32x4_t{v0, v1, v2, v3};
-      const Q8Blk8x4 r = q8_block8x4(v0, v1, v2, v3);
-      const uint32_t blk = i / 8, l = i & 7;
-      *(RLH_LDS uint32_t*)(la.qs + (blk >> 3) * kSbStride + (blk & 7) * 32 + 4 * l) = r.packed;
-      if (l == 0) {
-        la.d[blk] = r.d;
-        la.s[blk] = r.tot;
-        la.s16x32[2 * blk] = 32.0f * (float)r.s;
-      } else if (l == 4) {
-        la.s16x32[2 * blk + 1] = 32.0f * (float)r.s;
-      }
+  const lf32x4* x4 = (const lf32x4*)xs;
+  const lf32x4* w4 = (const lf32x4*)ws;
+  // n4 and NT are multiples of 8: whole 8-lane groups stay active together
+  for (uint32_t i = tid; i < n4; i += NT) {
+    const f32x4_t xr = x4[i], wr = w4[i];
+    const float v0 = (xr.x * s) * wr.x, v1 = (xr.y * s) * wr.y;
+    const float v2 = (xr.z * s) * wr.z, v3 = (xr.w * s) * wr.w;
+    if (L.need_xf) *(lf32x4*)(la.xf + (i >> 6) * kXfStride + 4 * (i & 63)) = f32x4_t{v0, v1, v2, v3};
+    const Q8Blk8x4 r = q8_block8x4(v0, v1, v2, v3);
+    const uint32_t blk = i / 8, l = i & 7;
+    *(RLH_LDS uint32_t*)(la.qs + (blk >> 3) * kSbStride + (blk & 7) * 32 + 4 * l) = r.packed;
+    if (l == 0) {
+      la.d[blk] = r.d;
+      la.s[blk] = r.tot;
+      la.s16x32[2 * blk] = 32.0f * (float)r.s;
+    } else if (l == 4) {
+      la.s16x32[2 * blk + 1] = 32.0f * (float)r.s;
     }
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 __device__ __forceinline__ void argmax_merge(float& bv, uint32_t& bi, float v, uint32_t i) {
@@ -454,52 +464,49 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   la.xf = (RLH_LDS float*)((RLH_LDS int8_t*)lds + L.xf_off);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
 
-  // two tiles per wave in flight: the next tile's weights load while the
-  // current tile's terms are computed; the first tile's weights are in
-  // flight while the activation is staged
+  // One tile per wave in flight (the next tile's loads are issued after the
+  // current tile's terms): with a second register set in flight the
+  // requests of the whole chip queue up and every wave's data lands late,
+  // which measured slower than spreading the tiles over more waves. The
+  // staging copies (activation row or norm inputs, silu's table) are issued
+  // first and the wave's first tile right after them, so the prologue waits
+  // for the copies alone while the weights stream in. The first load is
+  // unconditional (tile index clamped; a wave without a tile reloads the last
+  // one and never uses it): a load under a branch lets the compiler move the
+  // unpacking of its data next to it, which then waits for the data.
   auto load = [&](typename I::W* w, uint32_t t) {
     const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
     I::load(w[0], g.w.a + off, lane);
     if (NM == 2) I::load(w[NM - 1], g.w2.a + off, lane);
   };
-  auto terms = [&](const typename I::W* w, uint32_t t) {
+  auto terms = [&](typename I::W* w, uint32_t t) {
+    weights_ready(w[0]);
+    if (NM == 2) weights_ready(w[NM - 1]);
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
     I::terms(w[0], la, j, region + rl * stride + j * I::kT);
     if (NM == 2) I::terms(w[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
   };
-  // ping-pong over two register sets, except for PAIR launches of the
-  // larger item types and for Q5_K, whose second set would not fit the
-  // register budget
-  constexpr bool kPP = (NM == 1 && TY != RLH_TYPE_Q5_K) || sizeof(typename I::W) <= 9 * 16;
   // the residual of the chain lane's row, read now so that the epilogue
   // does not wait for it
   float rsd = 0.0f;
   if (NM == 1 && g.resid && wave == 0) rsd = ld_gf(g.resid + row0 + min(lane, nrows - 1));
-  typename I::W wa[NM], wb[kPP ? NM : 1];
+  lfloat* xs = region;
+  lfloat* ws = region + cols;
+  if (NM == 2 && wave == 0) exp_tab_dma(exp_tab);
+  if (L.nx) norm_dma(L, xs, ws);
+  else act_dma(L, la);
+  __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads
+  typename I::W wa[NM];
   uint32_t t = wave;
-  NormRegs nr;
-  if (L.nx) norm_load(L, nr);
-  __builtin_amdgcn_sched_barrier(0);  // keep the row loads ahead of the weight tiles
-  if (t < ntiles) load(wa, t);
-  // silu's expf table to LDS, after the bulk loads are issued (its store
-  // waits for its load); read after the prologue's barriers
-  if (NM == 2) exp_tab_to_lds(exp_tab);
-  if (L.nx) stage_norm(L, la, region, misc, nr);
-  else stage_activation(L, la);
-  if (kPP) {
-    for (; t < ntiles; t += 2 * nwaves) {
-      const uint32_t t2 = t + nwaves;
-      if (t2 < ntiles) load(wb, t2);
-      terms(wa, t);
-      if (t2 >= ntiles) break;
-      if (t2 + nwaves < ntiles) load(wa, t2 + nwaves);
-      terms(wb, t2);
-    }
-  } else {
-    for (; t < ntiles; t += nwaves) {
-      terms(wa, t);
-      if (t + nwaves < ntiles) load(wa, t + nwaves);
-    }
+  load(wa, min(t, ntiles - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<I::kLoads * NM>();  // this wave's copies have landed (the tile's loads may not)
+  if (L.nx) norm_finish(L, la, xs, ws, misc);
+  else act_finish(L, la);
+  for (; t < ntiles; t += nwaves) {
+    __builtin_amdgcn_sched_barrier(0);
+    terms(wa, t);
+    if (t + nwaves < ntiles) load(wa, t + nwaves);
   }
   __syncthreads();
 
@@ -587,11 +594,9 @@ MvKernel mv_kernel(uint32_t ty) {
 
 constexpr uint32_t kMaxLds = 150u * 1024u;
 
-// LDS bytes of a plan with R rows per block: the padded Q8 activation row,
-// then the term tiles.
 // LDS of a plan with R rows per block: the padded Q8 activation row, the
 // padded f32 row when a segment is Q5_K, then the term tiles (which the norm
-// prologue borrows for the unpadded f32 input row).
+// prologue borrows for the f32 input row and the norm weights).
 uint32_t plan_act_bytes(const MvPlan& p) {
   const uint32_t nsb = p.L.cols / 256, nb = p.L.cols / 32;
   return (nsb * kSbStride + nb * 16 + 15) & ~15u;
@@ -601,7 +606,7 @@ uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   const uint32_t cols = p.L.cols, nsb = cols / 256;
   const uint32_t stride = nsb * p.max_terms + 4;
   const uint32_t tile = nm * R * stride * 4;
-  return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? cols * 4 : 0u);
+  return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? 2 * cols * 4 : 0u);
 }
 
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
@@ -656,10 +661,12 @@ void mv_plan_argmax(MvPlan& p, const MvArgmax& am) {
   p.L.am = am;
 }
 
-// Block shape: R rows = whole row-tiles. Small blocks spread the rows over
-// every CU with high occupancy (R = one row-tile); a PAIR launch needs R to
-// be a multiple of 32 (its epilogue emits whole Q8 blocks of h). One wave
-// per tile of the block, at most 16.
+// Block shape: R rows = whole row-tiles, one wave per tile (at most 8
+// waves; a block with more tiles loops). Single launches take one row-tile
+// per block, launches with the norm prologue two (half the blocks repeat
+// it); a PAIR launch takes 64 rows (its epilogue emits whole Q8 blocks of h,
+// one row per lane). Measured on Qwen3-8B shapes against 1-4 tiles per wave
+// and 16-64 rows per block.
 bool mv_plan_finish(MvPlan& p) {
   const uint32_t nm = (p.L.nseg == 1 && p.L.seg[0].pair) ? 2u : 1u;
   const uint32_t nsb = p.L.cols / 256;
@@ -670,7 +677,8 @@ bool mv_plan_finish(MvPlan& p) {
   if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows ||
                   p.L.seg[0].w.rows % 32 != 0))
     return false;
-  const uint32_t R = nm == 2 ? std::max<uint32_t>(tr, 32) : tr;
+  // the epilogue runs one row per lane: R <= 64
+  const uint32_t R = nm == 2 ? 64u : std::min<uint32_t>(p.norm ? 2 * tr : tr, 64);
   p.L.need_xf = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty == RLH_TYPE_Q5_K || (p.L.seg[s].pair && p.L.seg[s].w2.ty == RLH_TYPE_Q5_K)) p.L.need_xf = 1;
@@ -682,10 +690,8 @@ bool mv_plan_finish(MvPlan& p) {
   p.L.xf_off = plan_act_bytes(p);
   p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
   p.lds = plan_lds(p, R, nm);
-  // two tiles per wave (the load/compute ping-pong); the norm prologue
-  // needs at least 4 waves
   const uint32_t ntiles = (R / tr) * ntj;
-  p.waves = std::max<uint32_t>(std::max<uint32_t>(nm, p.norm ? 4u : 1u), std::min<uint32_t>(8, (ntiles + 1) / 2));
+  p.waves = std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;

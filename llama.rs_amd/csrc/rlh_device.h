@@ -185,6 +185,40 @@ __device__ __forceinline__ void exp_tab_to_lds(lu64* tab) {
   if (threadIdx.x < 32) tab[threadIdx.x] = kExp2Tab[threadIdx.x];
 }
 
+// The same copy as one wave's LDS DMA (global_load_lds, 4 bytes per lane): no
+// register round trip, so nothing waits for it until the wave's vector-memory
+// count says it has landed (wait_vmcnt), and the block's barrier after that.
+__device__ __forceinline__ void exp_tab_dma(lu64* tab) {
+  const uint32_t lane = threadIdx.x & 63;
+  __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint32_t*)(const void*)kExp2Tab + lane),
+                                   (RLH_LDS void*)tab, 4, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Waits and barriers that leave the wave's global loads in flight.
+//
+// __syncthreads() is a release/acquire fence plus s_barrier; in a kernel that
+// copies HBM -> LDS with global_load_lds the fence waits for every
+// outstanding vector-memory operation (vmcnt(0)), including register loads of
+// weights meant to stay in flight. A prologue that stages its inputs by DMA
+// therefore issues the DMA first, then the weight loads, then waits with
+// wait_vmcnt<n> (n = loads issued after the DMA: the counter retires in
+// issue order) and meets the other waves at lds_barrier().
+// ---------------------------------------------------------------------------
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  // gfx9 s_waitcnt: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// Block barrier for LDS traffic: this wave's LDS accesses have completed
+// (lgkmcnt(0)); vector-memory operations are not waited for. The asm's memory
+// clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));
+  asm volatile("s_barrier" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Exact AVX2 reduction tree over 32 "slot" accumulators held in lanes 0..31
 // of a wave: slot 8k+l is lane l of the reference's accumulator a_k.
