@@ -85,30 +85,37 @@ __device__ __forceinline__ void weights_ready(W& r) {
 }
 
 // ---- work items: one super-block of one row ---------------------------------
+// An item is streamed in kParts parts (halves of its super-block, each with
+// the item's small scale words again), so that a wave keeps one part in
+// flight while it computes the previous one. Part h of kParts writes the
+// item's terms [h * kT / kParts, (h + 1) * kT / kParts).
 template <uint32_t TY>
 struct MI;
 
 template <>
 struct MI<RLH_TYPE_Q4_K> {
   static constexpr uint32_t kT = 4;
-  static constexpr int kLoads = 9;  // vector-memory loads per item
-  struct W {
-    u32x4_t hdr, q[8];
+  static constexpr int kParts = 2;
+  static constexpr int kQ = 8 / kParts;  // 16-byte quant chunks per part
+  static constexpr int kLoads = kQ + 1;  // vector-memory loads per part
+  struct P {
+    u32x4_t hdr, q[kQ];
   };
-  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int h) {
     r.hdr = gl_u4(tile + lane * 16);
 #pragma unroll
-    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + (k + 1) * 1024 + lane * 16);
+    for (int k = 0; k < kQ; k++) r.q[k] = gl_u4(tile + (h * kQ + k + 1) * 1024 + lane * 16);
   }
   // Group g: low nibbles of q[2g], q[2g+1] = sub-block 2g, high = 2g+1.
-  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int h) {
     const uint32_t m4 = 0x0F0F0F0Fu;
     const float d = f16_to_f32(r.hdr.x & 0xffff);
     const float dmin = f16_to_f32(r.hdr.x >> 16);
     const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;  // the 12 scale bytes
-    float out[4];
+    float out[kQ / 2];
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
+    for (int gl = 0; gl < kQ / 2; gl++) {
+      const int g = h * (kQ / 2) + gl;
       // get_scale_min_k4 (quant.rs:176-185) for sub-blocks 2g and 2g+1
       uint32_t sc1, m1, sc2, m2;
       if (g < 2) {
@@ -127,7 +134,7 @@ struct MI<RLH_TYPE_Q4_K> {
       const uint32_t ab = j * 8 + 2 * g;
       const RLH_LDS int8_t* pa = qblk(act, ab);
       const u32x4_t a0 = lds_u4(pa), a1 = lds_u4(pa + 16), b0 = lds_u4(pa + 32), b1 = lds_u4(pa + 48);
-      const u32x4_t q0 = r.q[2 * g], q1 = r.q[2 * g + 1];
+      const u32x4_t q0 = r.q[2 * gl], q1 = r.q[2 * gl + 1];
       int i1 = dot16(q0 & m4, a0, 0);
       i1 = dot16(q1 & m4, a1, i1);
       int i2 = dot16((q0 >> 4) & m4, b0, 0);
@@ -136,126 +143,128 @@ struct MI<RLH_TYPE_Q4_K> {
       const float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
       const float da = act.d[ab], db = act.d[ab + 1];
       const float sa = (float)act.s[ab], sb = (float)act.s[ab + 1];
-      out[g] = da * (d1 * (float)i1 - mm1 * sa) + db * (d2 * (float)i2 - mm2 * sb);
+      out[gl] = da * (d1 * (float)i1 - mm1 * sa) + db * (d2 * (float)i2 - mm2 * sb);
     }
-    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
+#pragma unroll
+    for (int gl = 0; gl < kQ / 2; gl++) t[h * (kQ / 2) + gl] = out[gl];
   }
 };
 
 // Q6_K terms in the reference order: for half { for sub { for c } }
-// (simd.rs:611-666), 16 per super-block.
+// (simd.rs:611-666), 16 per super-block; part h = half h.
 template <>
 struct MI<RLH_TYPE_Q6_K> {
   static constexpr uint32_t kT = 16;
-  static constexpr int kLoads = 14;
-  struct W {
-    u32x4_t ql[8], qh[4], sc;
+  static constexpr int kParts = 2;
+  static constexpr int kLoads = 8;
+  struct P {
+    u32x4_t ql[4], qh[2], sc;
     u32x4_t d;  // .x = the f16 scale (the other lanes unused)
   };
-  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int h) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) r.ql[k] = gl_u4(tile + k * 1024 + lane * 16);
+    for (int k = 0; k < 4; k++) r.ql[k] = gl_u4(tile + (4 * h + k) * 1024 + lane * 16);
 #pragma unroll
-    for (int k = 0; k < 4; k++) r.qh[k] = gl_u4(tile + (8 + k) * 1024 + lane * 16);
+    for (int k = 0; k < 2; k++) r.qh[k] = gl_u4(tile + (8 + 2 * h + k) * 1024 + lane * 16);
     r.sc = gl_u4(tile + 12 * 1024 + lane * 16);
     r.d = u32x4_t{ld_g2(tile + 13 * 1024 + lane * 2), 0u, 0u, 0u};
   }
-  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int h) {
     const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
     const float d = f16_to_f32(r.d.x);
+    const uint32_t wlo = h ? r.sc.z : r.sc.x, whi = h ? r.sc.w : r.sc.y;  // the half's 8 scale bytes
+    const uint32_t ab = j * 8 + 4 * h;
+    // the half's 128 activation bytes, scales and 16-value sums, read in
+    // one batch so the LDS latency is paid once per half
+    u32x4_t av[4][2];
+    float da[4], sa[4][2];
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-      const uint32_t wlo = h ? r.sc.z : r.sc.x, whi = h ? r.sc.w : r.sc.y;  // the half's 8 scale bytes
-      const uint32_t ab = j * 8 + 4 * h;
-      // the half's 128 activation bytes, scales and 16-value sums, read in
-      // one batch so the LDS latency is paid once per half
-      u32x4_t av[4][2];
-      float da[4], sa[4][2];
+    for (int c = 0; c < 4; c++) {
+      av[c][0] = lds_u4(qblk(act, ab + c));
+      av[c][1] = lds_u4(qblk(act, ab + c) + 16);
+      da[c] = act.d[ab + c];
+      sa[c][0] = act.s16x32[(ab + c) * 2];
+      sa[c][1] = act.s16x32[(ab + c) * 2 + 1];
+    }
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+      const u32x4_t ql0 = r.ql[s], ql1 = r.ql[2 + s], qh = r.qh[s];
+      float out[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        av[c][0] = lds_u4(qblk(act, ab + c));
-        av[c][1] = lds_u4(qblk(act, ab + c) + 16);
-        da[c] = act.d[ab + c];
-        sa[c][0] = act.s16x32[(ab + c) * 2];
-        sa[c][1] = act.s16x32[(ab + c) * 2 + 1];
+        const u32x4_t lo = (c & 1) ? ql1 : ql0;
+        const u32x4_t nib = (c < 2) ? (lo & m4) : ((lo >> 4) & m4);
+        const u32x4_t uu = nib | (((qh >> (2 * c)) & m2) << 4);
+        const int ss = dot16(uu, av[c][s], 0);
+        const uint32_t bi = s + 2 * c;  // sc[sub + 2c] (simd.rs:626-629)
+        const float scf = (float)(int8_t)(((bi < 4 ? wlo : whi) >> (8 * (bi & 3))) & 0xff);
+        out[c] = d * scf * ((float)ss - sa[c][s]) * da[c];
       }
-#pragma unroll
-      for (int s = 0; s < 2; s++) {
-        const u32x4_t ql0 = r.ql[4 * h + s], ql1 = r.ql[4 * h + 2 + s], qh = r.qh[2 * h + s];
-        float out[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const u32x4_t lo = (c & 1) ? ql1 : ql0;
-          const u32x4_t nib = (c < 2) ? (lo & m4) : ((lo >> 4) & m4);
-          const u32x4_t uu = nib | (((qh >> (2 * c)) & m2) << 4);
-          const int ss = dot16(uu, av[c][s], 0);
-          const uint32_t bi = s + 2 * c;  // sc[sub + 2c] (simd.rs:626-629)
-          const float scf = (float)(int8_t)(((bi < 4 ? wlo : whi) >> (8 * (bi & 3))) & 0xff);
-          out[c] = d * scf * ((float)ss - sa[c][s]) * da[c];
-        }
-        *(lf32x4*)(t + 8 * h + 4 * s) = f32x4_t{out[0], out[1], out[2], out[3]};
-      }
+      *(lf32x4*)(t + 8 * h + 4 * s) = f32x4_t{out[0], out[1], out[2], out[3]};
     }
   }
 };
 
-// Q8_0: item = 8 consecutive 32-value blocks (256 values).
+// Q8_0: item = 8 consecutive 32-value blocks (256 values); part h = blocks
+// 4h .. 4h+3.
 template <>
 struct MI<RLH_TYPE_Q8_0> {
   static constexpr uint32_t kT = 8;
-  static constexpr int kLoads = 17;
-  struct W {
-    u32x4_t q[16], dv;
+  static constexpr int kParts = 2;
+  static constexpr int kLoads = 9;
+  struct P {
+    u32x4_t q[8], dv;
   };
-  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int h) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) r.q[k] = gl_u4(tile + k * 1024 + lane * 16);
+    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + (8 * h + k) * 1024 + lane * 16);
     r.dv = gl_u4(tile + 16 * 1024 + lane * 16);
   }
-  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int h) {
     const uint32_t dw[4] = {r.dv.x, r.dv.y, r.dv.z, r.dv.w};
-    float out[8];
+    float out[4];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int kl = 0; kl < 4; kl++) {
+      const int k = 4 * h + kl;
       const uint32_t b = j * 8 + k;
       const RLH_LDS int8_t* pa = qblk(act, b);
-      const int i = dot16(r.q[2 * k + 1], lds_u4(pa + 16), dot16(r.q[2 * k], lds_u4(pa), 0));
+      const int i = dot16(r.q[2 * kl + 1], lds_u4(pa + 16), dot16(r.q[2 * kl], lds_u4(pa), 0));
       const float dk = f16_to_f32((dw[k >> 1] >> (16 * (k & 1))) & 0xffff);
-      out[k] = dk * (float)i * act.d[b];  // simd.rs:891
+      out[kl] = dk * (float)i * act.d[b];  // simd.rs:891
     }
-    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
-    *(lf32x4*)(t + 4) = f32x4_t{out[4], out[5], out[6], out[7]};
+    *(lf32x4*)(t + 4 * h) = f32x4_t{out[0], out[1], out[2], out[3]};
   }
 };
 
-// Q4_0: item = 8 consecutive 32-value blocks.
+// Q4_0: item = 8 consecutive 32-value blocks; part h = blocks 4h .. 4h+3.
 template <>
 struct MI<RLH_TYPE_Q4_0> {
   static constexpr uint32_t kT = 8;
-  static constexpr int kLoads = 9;
-  struct W {
-    u32x4_t q[8], dv;
+  static constexpr int kParts = 2;
+  static constexpr int kLoads = 5;
+  struct P {
+    u32x4_t q[4], dv;
   };
-  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int h) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + k * 1024 + lane * 16);
+    for (int k = 0; k < 4; k++) r.q[k] = gl_u4(tile + (4 * h + k) * 1024 + lane * 16);
     r.dv = gl_u4(tile + 8 * 1024 + lane * 16);
   }
-  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int h) {
     const uint32_t m4 = 0x0F0F0F0Fu;
     const uint32_t dw[4] = {r.dv.x, r.dv.y, r.dv.z, r.dv.w};
-    float out[8];
+    float out[4];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int kl = 0; kl < 4; kl++) {
+      const int k = 4 * h + kl;
       const uint32_t b = j * 8 + k;
       const RLH_LDS int8_t* pa = qblk(act, b);
-      const int i0 = dot16(r.q[k] & m4, lds_u4(pa), 0);
-      const int i1 = dot16((r.q[k] >> 4) & m4, lds_u4(pa + 16), 0);
+      const int i0 = dot16(r.q[kl] & m4, lds_u4(pa), 0);
+      const int i1 = dot16((r.q[kl] >> 4) & m4, lds_u4(pa + 16), 0);
       const float dk = f16_to_f32((dw[k >> 1] >> (16 * (k & 1))) & 0xffff);
-      out[k] = dk * (float)(i0 + i1 - 8 * act.s[b]) * act.d[b];  // simd.rs:863
+      out[kl] = dk * (float)(i0 + i1 - 8 * act.s[b]) * act.d[b];  // simd.rs:863
     }
-    *(lf32x4*)t = f32x4_t{out[0], out[1], out[2], out[3]};
-    *(lf32x4*)(t + 4) = f32x4_t{out[4], out[5], out[6], out[7]};
+    *(lf32x4*)(t + 4 * h) = f32x4_t{out[0], out[1], out[2], out[3]};
   }
 };
 
@@ -265,22 +274,23 @@ struct MI<RLH_TYPE_Q4_0> {
 // simd.rs:328-377 for 256 values): slot (m, l) is the FMA chain over the
 // eight 32-value chunks c of element 32c + 8m + l, A_l = (a0+a1)+(a2+a3),
 // then the AVX2 tree. Dequant (quant.rs:313-349): d1 * (q + 16*hbit) - mm1.
-// One term per super-block.
+// One term per super-block, one part (the chains run through all chunks).
 template <>
 struct MI<RLH_TYPE_Q5_K> {
   static constexpr uint32_t kT = 1;
+  static constexpr int kParts = 1;
   static constexpr int kLoads = 11;
-  struct W {
+  struct P {
     u32x4_t hdr, qh[2], q[8];
   };
-  __device__ __forceinline__ static void load(W& r, const uint8_t* tile, uint32_t lane) {
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int) {
     r.hdr = gl_u4(tile + lane * 16);
     r.qh[0] = gl_u4(tile + 1024 + lane * 16);
     r.qh[1] = gl_u4(tile + 2048 + lane * 16);
 #pragma unroll
     for (int k = 0; k < 8; k++) r.q[k] = gl_u4(tile + (k + 3) * 1024 + lane * 16);
   }
-  __device__ __forceinline__ static void terms(const W& r, const LAct& act, uint32_t j, lfloat* t) {
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int) {
     const float d = f16_to_f32(r.hdr.x & 0xffff);
     const float dmin = f16_to_f32(r.hdr.x >> 16);
     const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
@@ -464,27 +474,32 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   la.xf = (RLH_LDS float*)((RLH_LDS int8_t*)lds + L.xf_off);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
 
-  // One tile per wave in flight (the next tile's loads are issued after the
-  // current tile's terms): with a second register set in flight the
-  // requests of the whole chip queue up and every wave's data lands late,
-  // which measured slower than spreading the tiles over more waves. The
-  // staging copies (activation row or norm inputs, silu's table) are issued
-  // first and the wave's first tile right after them, so the prologue waits
-  // for the copies alone while the weights stream in. The first load is
-  // unconditional (tile index clamped; a wave without a tile reloads the last
-  // one and never uses it): a load under a branch lets the compiler move the
-  // unpacking of its data next to it, which then waits for the data.
-  auto load = [&](typename I::W* w, uint32_t t) {
-    const size_t off = ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes;
-    I::load(w[0], g.w.a + off, lane);
-    if (NM == 2) I::load(w[NM - 1], g.w2.a + off, lane);
+  // The wave streams its work as units (tile t, matrix m, part h), one
+  // unit in flight: when a unit's data has arrived the next unit's loads are
+  // issued, then the arrived unit's terms are computed. More data in flight
+  // per wave queues up the requests of the whole chip and every wave's data
+  // lands late; measured slower. The staging copies (activation row or norm
+  // inputs, silu's table) are issued first and the first unit right after
+  // them, so the prologue waits for the copies alone while the weights
+  // stream in. The first unit is loaded unconditionally (a wave without a
+  // tile loads the last one and never uses it); weights_ready() keeps the
+  // compiler from moving a unit's unpacking next to its loads, where it
+  // would wait for the data.
+  using P = typename I::P;
+  constexpr int kP = I::kParts;
+  constexpr int kH1 = kP == 2 ? 1 : 0;  // part of the odd units
+  const uint32_t my_tiles = wave < ntiles ? (ntiles - 1 - wave) / nwaves + 1 : 0;
+  const uint32_t nunits = my_tiles * NM * kP;
+  auto tile_off = [&](uint32_t t) { return ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes; };
+  auto issue = [&](P& r, uint32_t u, int h) {
+    const uint32_t t = min(wave + (u / (NM * kP)) * nwaves, ntiles - 1);
+    const uint8_t* base = (NM == 2 && (u / kP) % NM == 1) ? g.w2.a : g.w.a;
+    I::load(r, base + tile_off(t), lane, h);
   };
-  auto terms = [&](typename I::W* w, uint32_t t) {
-    weights_ready(w[0]);
-    if (NM == 2) weights_ready(w[NM - 1]);
+  auto work = [&](const P& r, uint32_t u, int h) {
+    const uint32_t t = wave + (u / (NM * kP)) * nwaves, m = (u / kP) % NM;
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
-    I::terms(w[0], la, j, region + rl * stride + j * I::kT);
-    if (NM == 2) I::terms(w[NM - 1], la, j, region + (R + rl) * stride + j * I::kT);
+    I::terms(r, la, j, region + (m * R + rl) * stride + j * I::kT, h);
   };
   // the residual of the chain lane's row, read now so that the epilogue
   // does not wait for it
@@ -496,17 +511,22 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   if (L.nx) norm_dma(L, xs, ws);
   else act_dma(L, la);
   __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads
-  typename I::W wa[NM];
-  uint32_t t = wave;
-  load(wa, min(t, ntiles - 1));
+  P ua, ub;
+  issue(ua, 0, 0);
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<I::kLoads * NM>();  // this wave's copies have landed (the tile's loads may not)
+  wait_vmcnt<I::kLoads>();  // this wave's copies have landed (the unit's loads may not)
   if (L.nx) norm_finish(L, la, xs, ws, misc);
   else act_finish(L, la);
-  for (; t < ntiles; t += nwaves) {
+  for (uint32_t u = 0; u < nunits; u += 2) {
+    weights_ready(ua);
+    if (u + 1 < nunits) issue(ub, u + 1, kH1);
     __builtin_amdgcn_sched_barrier(0);
-    terms(wa, t);
-    if (t + nwaves < ntiles) load(wa, t + nwaves);
+    work(ua, u, 0);
+    if (u + 1 >= nunits) break;
+    weights_ready(ub);
+    if (u + 2 < nunits) issue(ua, u + 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    work(ub, u + 1, kH1);
   }
   __syncthreads();
 
