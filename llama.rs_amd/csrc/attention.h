@@ -43,9 +43,14 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused);
 // softmax_inplace of every score row (probabilities overwrite the scores).
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a);
 // Decode (one token) after the scores: softmax and the ordered V
-// accumulation in one kernel when the group's score rows fit its LDS,
-// otherwise launch_attn_softmax + the decode PV kernel.
-void launch_attn_decode(hipStream_t st, const AttnArgs& a);
+// accumulation in one kernel, otherwise launch_attn_softmax + the decode PV
+// kernel. resident (when attn_dec_v_lds is nonzero): the kernel that keeps
+// its V slice in LDS, which writes out in f32 only; the other variants
+// also write the Q8 blocks out_q8.
+void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool resident);
+// LDS of the resident-V decode kernel (0 when it does not apply: more than 4
+// query heads per KV head or too many positions).
+size_t attn_dec_v_lds(uint32_t t_max, uint32_t group);
 // LDS of the fused decode kernel for t_max positions and `group` query heads
 // per KV head (0 when the rows do not fit).
 size_t attn_dec_fused_lds(uint32_t t_max, uint32_t group);

@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "attention.h"
 #include "rlh_device.h"
 
@@ -454,6 +456,204 @@ __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
   }
 }
 
+// Max over the 64 lanes of a wave (order-free) with DPP row shifts and row
+// broadcasts: a lane whose DPP source is outside its row keeps its own value.
+__device__ __forceinline__ float wave_max(float x) {
+  auto dpp = [](float v, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), decltype(ctrl)::value, 0xf,
+                                                      0xf, false));
+  };
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x111>{}));  // row_shr:1
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x112>{}));  // row_shr:2
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x114>{}));  // row_shr:4
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x118>{}));  // row_shr:8
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x142>{}));  // row_bcast:15
+  x = fmaxf(x, dpp(x, std::integral_constant<int, 0x143>{}));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
+// Decode softmax + PV with the block's V slice resident in LDS.
+// grid (KVH, 8 slices of 16 dimensions), block 512 (8 waves); G <= 4.
+// Dynamic LDS: score rows e[G][RS] | V slice vs[RS][16] | product ring
+// pr[3][64 chain lanes][kPrStride].
+// * At entry every wave issues its DMA copies: the G score rows, then exactly
+//   kVDma 1 KB pieces of the V slice (16 rows x 64 B each; a piece index
+//   past the last is clamped, so a repeated piece rewrites the same bytes).
+//   The softmax runs while the V slice lands.
+// * softmax_inplace of the G rows as in k_attn_smpv_dec.
+// * PV: chain lane l < G*16 of wave 0 owns (head l / 16, dimension l % 16)
+//   and adds its products in position order, o = prod_j + o (the saxpy's
+//   add); the products prod_j = p_j * v_j[d] are formed by waves 1..7 one
+//   64-position chunk ahead into a ring of three chunk slots, so the chain
+//   wave issues one add per position and a 16-byte LDS read per four (a
+//   multiply on the chain wave would cost an issue slot per position).
+//   One block barrier per chunk: at chunk c the chain reads slot c % 3 while
+//   the producers fill slot (c + 2) % 3.
+// The output is written in f32; its Q8 blocks are made by the attn_output
+// matvec's prologue.
+constexpr int kVsW = 16;              // dimensions per block
+constexpr int kPrC = 64;              // positions per product chunk
+constexpr int kPrStride = kPrC + 4;   // floats per chain lane in a chunk slot
+constexpr int kPrSlots = 3;
+constexpr int kVDma = 12;             // V-slice DMA pieces per wave (16 rows each)
+constexpr uint32_t kDecVMaxCtx = 8u * kVDma * 16u;  // 1536 positions
+constexpr size_t kDecVLdsMax = 150u * 1024u;
+
+__global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
+  __shared__ float red[8 * kAttnMaxGroup];
+  __shared__ float s_mx[kAttnMaxGroup], s_inv[kAttnMaxGroup];
+  __shared__ int s_on[kAttnMaxGroup];
+  __shared__ uint64_t tab_g[32];
+  extern __shared__ __attribute__((aligned(16))) float lds_generic[];
+  lu64* tab = (lu64*)tab_g;
+  const int G = a.H / a.KVH;
+  const uint32_t RS = dec_row_stride(a.t_max);
+  lfloat* e = (lfloat*)lds_generic;
+  lfloat* vs = e + (size_t)G * RS;
+  lfloat* pr = vs + (size_t)RS * kVsW;
+  const uint32_t g = blockIdx.x, d0 = blockIdx.y * kVsW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvd = a.KVH * kHd;
+  const uint32_t t = a.pos0[0] + 1;
+  const float* srow = a.scores + (size_t)g * G * a.t_stride;
+  // score rows -> LDS (positions past t repeat the last score; their slots
+  // lie inside the row stride), the exp table, then the V slice
+  const uint32_t pieces = (t + 63) / 64;
+  for (uint32_t pc = wave; pc < (uint32_t)G * pieces; pc += 8) {
+    const uint32_t h = pc / pieces, j0 = (pc % pieces) * 64;
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(srow + (size_t)h * a.t_stride + min(j0 + lane, t - 1)),
+                                     (RLH_LDS void*)(e + h * RS + j0), 4, 0, 0);
+  }
+  if (wave == 0) exp_tab_dma(tab);
+  {
+    const uint32_t nvp = (t + 15) / 16;
+    const float* vsrc = a.vcache + g * kHd + d0 + (lane & 3) * 4;
+#pragma unroll
+    for (int i = 0; i < kVDma; i++) {
+      const uint32_t pc = min((uint32_t)(wave + 8 * i), nvp - 1);
+      const uint32_t row = min(pc * 16 + (uint32_t)(lane >> 2), t - 1);
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(vsrc + (size_t)row * kvd),
+                                       (RLH_LDS void*)(vs + pc * 16 * kVsW), 16, 0, 0);
+    }
+  }
+  wait_vmcnt<kVDma>();  // this wave's score rows (and table) have landed
+  lds_barrier();
+  // softmax_inplace of the G rows (ops.rs:398-419); head hg is taken by
+  // TPH = 64 * floor(8 / G) threads, four consecutive positions at a time
+  // (the positions from t to the next multiple of 4 hold copies of the last
+  // score: they leave the max unchanged and are never summed)
+  const uint32_t TPH = 64u * (8u / (uint32_t)G), WPH = TPH / 64;
+  const uint32_t hg = tid / TPH, lt = tid % TPH;
+  const bool hon = hg < (uint32_t)G;
+  lfloat* eh = e + min(hg, (uint32_t)G - 1) * RS;
+  const uint32_t nq4 = (t + 3) / 4;
+  float mx = -__int_as_float(0x7f800000), my = mx;
+  if (hon)
+    for (uint32_t q = lt; q < nq4; q += 2 * TPH) {
+      const f32x4_t x = *(const lf32x4*)(eh + 4 * q);
+      const f32x4_t y = *(const lf32x4*)(eh + 4 * min(q + TPH, nq4 - 1));
+      mx = fmaxf(fmaxf(mx, x.x), fmaxf(x.y, fmaxf(x.z, x.w)));
+      my = fmaxf(fmaxf(my, y.x), fmaxf(y.y, fmaxf(y.z, y.w)));
+    }
+  mx = wave_max(fmaxf(mx, my));
+  if (lane == 0) red[wave] = mx;
+  lds_barrier();
+  if (tid < G) {  // NaN first score: the reference's max stays NaN
+    float m = red[tid * WPH];
+    for (uint32_t w = 1; w < WPH; w++) m = fmaxf(m, red[tid * WPH + w]);
+    const float x0 = e[tid * RS];
+    s_mx[tid] = x0 != x0 ? x0 : m;
+  }
+  lds_barrier();
+  if (hon) {
+    const float m = s_mx[hg];
+    for (uint32_t q = lt; q < nq4; q += TPH) {
+      const f32x4_t x = *(const lf32x4*)(eh + 4 * q);
+      *(lf32x4*)(eh + 4 * q) = f32x4_t{expf_glibc_t(x.x - m, tab), expf_glibc_t(x.y - m, tab),
+                                       expf_glibc_t(x.z - m, tab), expf_glibc_t(x.w - m, tab)};
+    }
+  }
+  lds_barrier();
+  if (tid < G) {  // the G sequential sums side by side, one lane each
+    const float sum = seq_sum_lds(e + tid * RS, t);
+    s_on[tid] = sum > 0.0f;
+    s_inv[tid] = 1.0f / sum;
+  }
+  wait_vmcnt<0>();  // this wave's V pieces have landed
+  lds_barrier();
+  // PV. Producer wave w = 1..7, lane l < NL (chain lane l: head h = l / 16,
+  // dimension l % 16) forms the products of the position quads w - 1,
+  // w + 6, w + 13 of a chunk, one quad at a time (more reads in flight per
+  // wave crowd the LDS the chain reads from): p_j = e_j * (1 / sum) when
+  // sum > 0 (softmax_inplace's last loop), then p_j * v_j[d], both rounded
+  // as the reference rounds them.
+  const uint32_t NL = (uint32_t)G * kVsW;  // chain lanes
+  const uint32_t nch = (t + kPrC - 1) / kPrC;
+  const uint32_t ph = min((uint32_t)lane, NL - 1) / kVsW;
+  const bool pon = s_on[ph];
+  const float pinv = s_inv[ph];
+  auto produce = [&](uint32_t c) {
+    if ((uint32_t)lane >= NL) return;
+    lfloat* slot = pr + (c % kPrSlots) * (64 * kPrStride) + lane * kPrStride;
+    const lfloat* ec = e + ph * RS + c * kPrC;  // < RS: chunks never pass the row stride
+    const lfloat* vc = vs + c * kPrC * kVsW + lane % kVsW;
+    for (uint32_t q = wave - 1; q < (uint32_t)kPrC / 4; q += 7) {
+      f32x4_t x = *(const lf32x4*)(ec + 4 * q);
+      if (pon) x = f32x4_t{x.x * pinv, x.y * pinv, x.z * pinv, x.w * pinv};
+      const lfloat* v = vc + 4 * q * kVsW;
+      *(lf32x4*)(slot + 4 * q) = f32x4_t{x.x * v[0], x.y * v[kVsW], x.z * v[2 * kVsW], x.w * v[3 * kVsW]};
+    }
+  };
+  if (wave != 0) {
+    produce(0);
+    if (nch > 1) produce(1);
+  }
+  lds_barrier();
+  if (wave != 0) {
+    for (uint32_t c = 0; c < nch; c++) {
+      if (c + 2 < nch) produce(c + 2);
+      lds_barrier();
+    }
+    return;
+  }
+  // the chain wave: o = prod_j + o in position order. Chunk c + 1 is complete
+  // while chunk c is added (it was made before the previous barrier), so the
+  // reads run one 32-position batch ahead across chunk boundaries; the
+  // chain wave writes no LDS and meets the producers at a plain s_barrier.
+  // Lanes past NL run a copy of the last chain (uniform control flow).
+  const uint32_t lc = min((uint32_t)lane, NL - 1);
+  const lfloat* base = pr + lc * kPrStride;
+  auto slotp = [&](uint32_t c) { return (const lf32x4d*)(base + (c % kPrSlots) * (64 * kPrStride)); };
+  float o = 0.0f;
+  f32x4d_t xa[8], xb[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) xa[i] = slotp(0)[i];
+  for (uint32_t c = 0; c < nch; c++) {
+    const lf32x4d* sc = slotp(c);
+    const lf32x4d* sn = slotp(c + 1);  // past the last chunk: read, never added
+    const uint32_t n = t - c * kPrC;
+    if (n >= (uint32_t)kPrC) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xb[i] = sc[8 + i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o = (((o + xa[i].x) + xa[i].y) + xa[i].z) + xa[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) xa[i] = sn[i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o = (((o + xb[i].x) + xb[i].y) + xb[i].z) + xb[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      o = seq_sum_lds((const lfloat*)sc, n, o);
+    }
+    asm volatile("s_barrier" ::: "memory");
+  }
+  if ((uint32_t)lane < NL)
+    ((RLH_GLOBAL float*)a.out)[(g * G + lane / kVsW) * kHd + d0 + lane % kVsW] = o;
+}
+
 // grid: (KVH, ceil(n_tok / TT)), TT = 32 / G tokens per block, latest (most
 // positions) token tiles first; block 512: thread (d = tid % 128, quarter
 // tid / 128) runs the chains of combinations quarter + 4i.
@@ -583,7 +783,19 @@ size_t attn_dec_fused_lds(uint32_t t_max, uint32_t group) {
   return b <= kDecFusedLds ? b : 0;
 }
 
-void launch_attn_decode(hipStream_t st, const AttnArgs& a) {
+size_t attn_dec_v_lds(uint32_t t_max, uint32_t group) {
+  if (group < 1 || group > 4 || t_max > kDecVMaxCtx) return 0;
+  const size_t rs = dec_row_stride(t_max);
+  const size_t b = (size_t)group * rs * 4 + rs * kVsW * 4 + (size_t)kPrSlots * 64 * kPrStride * 4;
+  return b <= kDecVLdsMax ? b : 0;
+}
+
+void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool resident) {
+  const size_t lv = resident ? attn_dec_v_lds(a.t_max, (uint32_t)(a.H / a.KVH)) : 0;
+  if (lv) {
+    hipLaunchKernelGGL(k_attn_dec_v, dim3(a.KVH, kHd / kVsW), dim3(512), lv, st, a);
+    return;
+  }
   const size_t lds = attn_dec_fused_lds(a.t_max, (uint32_t)(a.H / a.KVH));
   if (lds) {
     hipLaunchKernelGGL(k_attn_smpv_dec, dim3(a.KVH, 4), dim3(512), lds, st, a);
@@ -607,7 +819,9 @@ bool attn_init(uint32_t max_ctx) {
   return hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_smpv_dec, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)kDecFusedLds) == hipSuccess;
+                             (int)kDecFusedLds) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_dec_v, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kDecVLdsMax) == hipSuccess;
 }
 
 }  // namespace rlh

@@ -318,6 +318,25 @@ float* layer_v(rlh_cache* c, uint32_t l) {
 
 enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
 
+// Decode attention keeps its V slices in LDS (and writes only f32) when the
+// cache's positions fit; attn_output then quantizes that f32 row itself.
+bool attn_resident(const rlh_cache* c) {
+  const rlh_config& cfg = c->m->cfg;
+  const uint32_t qd = cfg.n_head * cfg.head_dim;
+  return qd <= kMvMaxNormCols && attn_dec_v_lds((uint32_t)c->max_ctx, cfg.n_head / cfg.n_head_kv) != 0;
+}
+
+// The attn_output plan of a decode step: its Q8 activation from the f32
+// attention output (resident attention) or the attention kernel's Q8 blocks.
+void plan_attn_output(MvPlan& p, rlh_cache* c, uint32_t qd) {
+  if (attn_resident(c)) {
+    mv_plan_init_quant(p, qd, c->attn);
+  } else {
+    mv_plan_init(p, qd, c->act_q);
+    mv_plan_set_f32(p, c->attn);
+  }
+}
+
 // Enqueues one decode step (model.rs:585-738) reading tok = st_dev[0] and
 // pos = st_dev[1]. dbg_slot >= 0 copies the residual after each layer.
 void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
@@ -370,12 +389,11 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       a.out = c->attn;
       a.out_q8 = c->act_q;
       launch_attn_scores(st, a, true);
-      launch_attn_decode(st, a);
+      launch_attn_decode(st, a, attn_resident(c));
     }
     {  // attn_output, x += (model.rs:713-716)
       MvPlan p;
-      mv_plan_init(p, qd, c->act_q);
-      mv_plan_set_f32(p, c->attn);
+      plan_attn_output(p, c, qd);
       mv_plan_add(p, L.o.dm, nullptr, c->x);
       mv_plan_finish(p);
       mv_launch(st, p);
@@ -1266,8 +1284,7 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
         if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
         const uint32_t cols = (uint32_t)t->cols;
         if (kind == RLH_T_ATTN_OUTPUT) {  // attention output in, as in decode
-          mv_plan_init(p, cols, c->act_q);
-          mv_plan_set_f32(p, c->attn);
+          plan_attn_output(p, c, cols);
         } else if (kind == RLH_T_FFN_DOWN) {  // silu(g)*u in
           mv_plan_init(p, cols, c->act_f);
           mv_plan_set_f32(p, c->g);

@@ -67,6 +67,7 @@ struct MvPlan {
   uint32_t max_terms = 0;
   uint32_t rows = 0;   // rows over all segments
   bool norm = false;   // activation from the norm prologue
+  bool quant = false;  // ... without the norm (quantize_q8 of the f32 row only)
 };
 
 // Terms (float summands of the reference's per-row chain) per 256-value
@@ -85,6 +86,9 @@ void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act);
 // the rmsnorm weight w (cols <= kMvMaxNormCols).
 void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w, float eps);
 constexpr uint32_t kMvMaxNormCols = 7168;
+// Same, with the activation quantize_q8(x) of the f32 row x computed in the
+// kernel (no norm; cols <= kMvMaxNormCols).
+void mv_plan_init_quant(MvPlan& p, uint32_t cols, const float* x);
 // The f32 form of a Q8 launch's activation (used when a segment is Q5_K).
 void mv_plan_set_f32(MvPlan& p, const float* xf);
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);

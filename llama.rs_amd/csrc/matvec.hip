@@ -386,37 +386,41 @@ __device__ __forceinline__ void act_finish(const MvLaunch& L, const LAct& la) {
 }
 
 // Norm input: every block computes quantize_q8(rmsnorm(x, w)) itself
-// (k_rmsnorm_q8's arithmetic). norm_dma copies the row and the norm weights
-// into LDS (xs, ws: the term tiles, free until the terms are written);
-// norm_finish, after the copies have landed, runs the 32 FMA chains of the
-// sum of squares in wave 0, then each group of 8 threads quantizes one
-// 32-value block straight into the LDS activation.
+// (k_rmsnorm_q8's arithmetic), or quantize_q8(x) when there is no norm
+// weight (nw null: the attention output entering attn_output). norm_dma
+// copies the row and the norm weights into LDS (xs, ws: the term tiles, free
+// until the terms are written); norm_finish, after the copies have landed,
+// runs the 32 FMA chains of the sum of squares in wave 0, then each group of
+// 8 threads quantizes one 32-value block straight into the LDS activation.
 __device__ __forceinline__ void norm_dma(const MvLaunch& L, lfloat* xs, lfloat* ws) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const uint32_t nbytes = L.cols * 4;  // a multiple of 1024
   for (uint32_t off = wave * 1024; off < nbytes; off += nw * 1024) {
     __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)L.nx + off + lane * 16),
                                      (RLH_LDS void*)((RLH_LDS uint8_t*)xs + off), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)L.nw + off + lane * 16),
-                                     (RLH_LDS void*)((RLH_LDS uint8_t*)ws + off), 16, 0, 0);
+    if (L.nw)
+      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)((const uint8_t*)L.nw + off + lane * 16),
+                                       (RLH_LDS void*)((RLH_LDS uint8_t*)ws + off), 16, 0, 0);
   }
 }
 
 __device__ __forceinline__ void norm_finish(const MvLaunch& L, const LAct& la, const lfloat* xs, const lfloat* ws,
                                             lfloat* misc) {
   const uint32_t tid = threadIdx.x, NT = blockDim.x, n4 = L.cols / 4;
+  const bool nrm = L.nw != nullptr;
   lds_barrier();
-  if (tid < 64) {
+  if (nrm && tid < 64) {
     const float ss = rms_sumsq_lds(xs, (int)L.cols);
     if (tid == 0) misc[0] = 1.0f / sqrtf(ss / (float)L.cols + L.eps);
   }
   lds_barrier();
-  const float s = misc[0];
+  const float s = nrm ? misc[0] : 1.0f;
   const lf32x4* x4 = (const lf32x4*)xs;
   const lf32x4* w4 = (const lf32x4*)ws;
   // n4 and NT are multiples of 8: whole 8-lane groups stay active together
   for (uint32_t i = tid; i < n4; i += NT) {
-    const f32x4_t xr = x4[i], wr = w4[i];
+    const f32x4_t xr = x4[i], wr = nrm ? w4[i] : f32x4_t{1.0f, 1.0f, 1.0f, 1.0f};
+    // without a norm weight (x * 1) * 1 == x exactly: the plain quantize_q8
     const float v0 = (xr.x * s) * wr.x, v1 = (xr.y * s) * wr.y;
     const float v2 = (xr.z * s) * wr.z, v3 = (xr.w * s) * wr.w;
     if (L.need_xf) *(lf32x4*)(la.xf + (i >> 6) * kXfStride + 4 * (i & 63)) = f32x4_t{v0, v1, v2, v3};
@@ -652,6 +656,15 @@ void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w,
   p.norm = true;
 }
 
+void mv_plan_init_quant(MvPlan& p, uint32_t cols, const float* x) {
+  p = MvPlan{};
+  p.L.cols = cols;
+  p.L.nx = x;
+  p.L.nw = nullptr;
+  p.norm = true;
+  p.quant = true;
+}
+
 void mv_plan_set_f32(MvPlan& p, const float* xf) { p.L.xf = xf; }
 
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid) {
@@ -684,7 +697,7 @@ void mv_plan_argmax(MvPlan& p, const MvArgmax& am) {
 // Block shape: R rows = whole row-tiles, one wave per tile (at most 8
 // waves; a block with more tiles loops). Single launches take one row-tile
 // per block, launches with the norm prologue two (half the blocks repeat
-// it); a PAIR launch takes 64 rows (its epilogue emits whole Q8 blocks of h,
+// it; the quantize-only prologue is cheap and keeps one); a PAIR launch takes 64 rows (its epilogue emits whole Q8 blocks of h,
 // one row per lane). Measured on Qwen3-8B shapes against 1-4 tiles per wave
 // and 16-64 rows per block.
 bool mv_plan_finish(MvPlan& p) {
@@ -698,7 +711,7 @@ bool mv_plan_finish(MvPlan& p) {
                   p.L.seg[0].w.rows % 32 != 0))
     return false;
   // the epilogue runs one row per lane: R <= 64
-  const uint32_t R = nm == 2 ? 64u : std::min<uint32_t>(p.norm ? 2 * tr : tr, 64);
+  const uint32_t R = nm == 2 ? 64u : std::min<uint32_t>(p.norm && !p.quant ? 2 * tr : tr, 64);
   p.L.need_xf = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty == RLH_TYPE_Q5_K || (p.L.seg[s].pair && p.L.seg[s].w2.ty == RLH_TYPE_Q5_K)) p.L.need_xf = 1;

@@ -81,7 +81,7 @@ __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kE
 
 // ---------------------------------------------------------------------------
 // Ordered f32 chains over LDS data, the reference's sequential loops:
-//   seq_sum_lds   s = ((0 + x0) + x1) + ...            (the softmax sum,
+//   seq_sum_lds   s = ((s0 + x0) + x1) + ...  s0 = 0 (the softmax sum,
 //                 ops.rs:408-412; the per-row term chain of the matvec)
 //   seq_saxpy_lds o = p_j * v_j + o for j in order     (saxpy, simd.rs:674-691)
 // The chain is latency bound (one dependent add per element), so the LDS
@@ -92,10 +92,9 @@ __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kE
 typedef float f32x4d_t __attribute__((ext_vector_type(4)));
 typedef RLH_LDS f32x4d_t lf32x4d;
 
-__device__ __forceinline__ float seq_sum_lds(const RLH_LDS float* x, uint32_t n) {
+__device__ __forceinline__ float seq_sum_lds(const RLH_LDS float* x, uint32_t n, float s = 0.0f) {
   const lf32x4d* x4 = (const lf32x4d*)x;
   const uint32_t nq = n / 4, nb = nq / 8;  // float4s, full batches of 8
-  float s = 0.0f;
   if (nb) {
     // the next batch's reads are unconditional (index clamped to the last
     // full batch): with a branch around them the compiler assumes either

@@ -132,6 +132,8 @@ SPECS = {
     # Q5_K matrices (no integer path in the reference: f32 products)
     "tiny-q5km": ModelSpec("tiny-q5km", 2, 256, 512, 4, 2, 1000, True, _q5km(), n_ctx=512),
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
+    # 4 query heads per KV head (the 4B / 8B grouping) and a long context window
+    "tiny-g4-q4km": ModelSpec("tiny-g4-q4km", 2, 256, 512, 8, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
 }
 
 

@@ -103,6 +103,33 @@ def test_decode_attention_paths(max_ctx):
     oc.close()
 
 
+@pytest.mark.parametrize("max_ctx,n_prompt", [(300, 62), (1200, 250), (4096, 130), (8000, 70)])
+def test_decode_attention_g4_paths(max_ctx, n_prompt):
+    """Decode attention with 4 query heads per KV head. Caches up to about
+    1200 positions take the kernel that keeps its V slices in LDS (the
+    products run one 64-position chunk ahead of the ordered adds: the steps
+    cross chunk boundaries and end on ragged chunks), 4096 positions the
+    streamed fused kernel, 8000 the separate softmax and V kernels. Logits
+    bit-exact in every step."""
+    print(f"decode attention g4 max_ctx {max_ctx} prompt {n_prompt}", flush=True)
+    spec, tensors, m, om = _get("tiny-g4-q4km")
+    prompt = rlh.synth_tokens(55, n_prompt, spec.vocab)
+    c = m.new_cache(max_ctx)
+    oc = om.new_cache(max_ctx)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg), bits(rg))
+    lib = oracle.load()
+    tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    for i in range(6):
+        lg = c.forward_into(np.array([tok], np.uint32), n_prompt + i)
+        rg = oc.forward_into(np.array([tok], np.uint32), n_prompt + i, oracle.MODE_DEFAULT)
+        assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ (rel {rel_l2(lg, rg):.2e})"
+        tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    c.close()
+    oc.close()
+
+
 @pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
 def test_generate_greedy_matches_cpu_tokens(name):
     spec, tensors, m, om = _get(name)
