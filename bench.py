@@ -9,7 +9,17 @@ tokens per second. Prefill tok/s, the per-token HBM roofline and the
 dominant kernel's roofline are reported alongside, plus the CPU reference
 (oracle) timed on a bounded sample of the same workload.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 1..5]
+
+Workloads (the five benchmark configurations; 4 is the default and the
+headline):
+  1  Qwen3-0.6B Q4_K_M   48-token prompt,   32 greedy tokens
+  2  Qwen3-0.6B Q8_0     48-token prompt,  128 greedy tokens (KV up to 176)
+  3  Qwen3-4B  Q4_K_M   256-token prompt,  256 greedy tokens
+  4  Qwen3-8B  Q4_K_M   512-token prompt,  512 greedy tokens
+  5  Qwen3-32B Q4_K_M  4096-token prompt,  256 sampled tokens (temperature 0.7,
+     top-k 40, top-p 0.95, repetition penalty 1.1 over the last 64, the
+     CLI's fixed seed; src/main.rs:44-52)
 """
 import argparse
 import json
@@ -26,6 +36,16 @@ import rlh  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
+
+
+# workload -> (model, prompt tokens, decode tokens, sampled)
+WORKLOADS = {
+    1: ("qwen3-0.6b-q4km", 48, 32, False),
+    2: ("qwen3-0.6b-q8_0", 48, 128, False),
+    3: ("qwen3-4b-q4km", 256, 256, False),
+    4: ("qwen3-8b-q4km", 512, 512, False),
+    5: ("qwen3-32b-q4km", 4096, 256, True),
+}
 
 
 def log(msg):
@@ -90,10 +110,11 @@ def calibration_copy(mb):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=512, help="timed decode tokens")
+    ap.add_argument("--workload", type=int, default=4, choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: the workload's)")
     ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens after the warm-up prefill")
-    ap.add_argument("--config", default="qwen3-8b-q4km")
-    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--config", default=None, help="model shape (default: the workload's)")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
     ap.add_argument("--seed", type=int, default=20260)
     ap.add_argument("--cpu-decode", type=int, default=6, help="CPU baseline decode tokens (0 = skip)")
     ap.add_argument("--cpu-prompt", type=int, default=8, help="CPU baseline prompt tokens")
@@ -106,6 +127,10 @@ def main():
               "--gpus must be 1", file=sys.stderr)
         sys.exit(2)
 
+    wl_config, wl_prompt, wl_steps, sampled = WORKLOADS[args.workload]
+    args.config = args.config or wl_config
+    args.prompt = args.prompt or wl_prompt
+    args.steps = args.steps or wl_steps
     spec = rlh.SPECS[args.config]
     lib = rlh.load()
     nthreads = min(16, os.cpu_count() or 1)
@@ -120,11 +145,16 @@ def main():
     max_ctx = args.prompt + max(args.steps, args.warmup) + 8
     cache = model.new_cache(max_ctx)
 
+    params = rlh.sampling_params()  # the CLI defaults (main.rs:44-52)
+    never = spec.vocab + 7            # EOS id no token can take: fixed token counts
     # warm-up: prefill + a few decode steps (pages in code, graphs, caches)
     logits = cache.forward_into(prompt, 0)
     first = cache.greedy_next()
     if args.warmup:
         cache.generate_greedy(first, args.warmup)
+    if sampled and args.warmup:
+        cache.reset()
+        cache.generate(prompt, args.warmup, params, never)
     cache.reset()
 
     # timed prefill
@@ -133,11 +163,21 @@ def main():
     prefill_s = time.perf_counter() - t0
     first = cache.greedy_next()
 
-    # timed decode: exactly K steps (generate_greedy returns after the device
-    # finished and the tokens were copied back)
-    t0 = time.perf_counter()
-    toks = cache.generate_greedy(first, args.steps)
-    decode_s = time.perf_counter() - t0
+    if sampled:
+        # Model::generate (prefill, then sample / forward_one per token, the
+        # sampler on the host): decode time = its time minus the prefill's
+        cache.reset()
+        t0 = time.perf_counter()
+        toks = cache.generate(prompt, args.steps, params, never)
+        decode_s = time.perf_counter() - t0 - prefill_s
+        if len(toks) != args.steps:
+            raise RuntimeError(f"generate returned {len(toks)} tokens, expected {args.steps}")
+    else:
+        # timed decode: exactly K steps (generate_greedy returns after the
+        # device finished and the tokens were copied back)
+        t0 = time.perf_counter()
+        toks = cache.generate_greedy(first, args.steps)
+        decode_s = time.perf_counter() - t0
     tok_s = args.steps / decode_s
     prefill_tok_s = args.prompt / prefill_s
 
@@ -162,7 +202,9 @@ def main():
     traffic = measured_traffic(args.config)
 
     out = {
-        "metric": "decode tok/s (Qwen3-8B Q4_K_M, 1 GPU); prefill tok/s and % HBM roofline reported alongside",
+        "metric": ("decode tok/s (Qwen3-8B Q4_K_M, 1 GPU); prefill tok/s and % HBM roofline reported alongside"
+                   if args.workload == 4 else
+                   f"decode tok/s ({args.config}, 1 GPU); prefill tok/s and % HBM roofline reported alongside"),
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -173,9 +215,12 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized Q4_K/Q6_K, uniform random prompt ids)",
-        "config": {"workload": f"{args.config}: {args.prompt}-token prefill then {args.steps} greedy decode "
-                               f"tokens (KV up to {args.prompt + args.steps})",
+        "data": "synthetic (seeded N(0,0.02) weights quantized "
+                + "/".join(sorted({rlh.TYPE_NAMES.get(t, str(t)) for t in spec.types.values()}))
+                + ", uniform random prompt ids)",
+        "config": {"workload": f"{args.config}: {args.prompt}-token prefill then {args.steps} "
+                               f"{'sampled (temperature 0.7, top-k 40, top-p 0.95, repetition penalty 1.1)' if sampled else 'greedy'}"
+                               f" decode tokens (KV up to {args.prompt + args.steps})",
                    "prompt_tokens": args.prompt, "decode_tokens": args.steps, "kv": "f32",
                    "eos": "ignored", "parallelism": "single GPU"},
         "prefill_tok_s": round(prefill_tok_s, 1),
@@ -189,7 +234,8 @@ def main():
                      "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(mv_us, 3), "bytes_per_launch": int(pair_bytes)},
-        "greedy_tokens_head": [int(t) for t in toks[:8]],
+        "decode": "sampled" if sampled else "greedy",
+        "tokens_head": [int(t) for t in toks[:8]],
     }
 
     if args.cpu_decode > 0:

@@ -167,6 +167,10 @@ uint64_t rlh_sampler_init(uint64_t seed);
  * select_nth_unstable). */
 int rlh_sample(const float* logits, uint64_t n, const rlh_sampling_params* p, const uint32_t* recent,
                uint64_t n_recent, uint64_t* rng_state, uint32_t* token);
+/* ops::softmax_inplace (src/ops.rs:398-419) on host x[n], as the sampler
+ * runs it (sampler.rs:119): max, exp(x - max) with the platform expf's
+ * results, the sum in index order, then x * (1 / sum) when the sum is > 0. */
+int rlh_softmax(float* x, uint64_t n);
 /* The same on the logits of the last forward call on this cache: the greedy
  * fast path (temperature <= 0 and no penalty) runs on the device, any other
  * setting copies the logits to the host first. */

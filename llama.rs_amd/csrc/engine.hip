@@ -266,6 +266,7 @@ struct rlh_model {
   float* rope_cs = nullptr;  // [n_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i+1
   bool finalized = false;
   bool f32_route = false;  // some layer matrix multiplies f32 activations in prefill (Q5_K)
+  bool o_quant_ok = false; // attn_output fits the matvec with its quantize prologue
 };
 
 struct rlh_cache {
@@ -322,8 +323,7 @@ enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
 // cache's positions fit; attn_output then quantizes that f32 row itself.
 bool attn_resident(const rlh_cache* c) {
   const rlh_config& cfg = c->m->cfg;
-  const uint32_t qd = cfg.n_head * cfg.head_dim;
-  return qd <= kMvMaxNormCols && attn_dec_v_lds((uint32_t)c->max_ctx, cfg.n_head / cfg.n_head_kv) != 0;
+  return c->m->o_quant_ok && attn_dec_v_lds((uint32_t)c->max_ctx, cfg.n_head / cfg.n_head_kv) != 0;
 }
 
 // The attn_output plan of a decode step: its Q8 activation from the f32
@@ -625,6 +625,14 @@ int rlh_model_finalize(rlh_model* m) {
     mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, L.down.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
+    if (l == 0) m->o_quant_ok = true;
+    if (qd <= kMvMaxNormCols) {  // the attn_output launch after the resident-V attention kernel
+      mv_plan_init_quant(p, (uint32_t)qd, &kShapeOnly);
+      mv_plan_add(p, L.o.dm, nullptr, nullptr);
+      m->o_quant_ok = m->o_quant_ok && mv_plan_finish(p);
+    } else {
+      m->o_quant_ok = false;
+    }
     if (!ok) return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": matrix shapes or types are not supported by the matvec");
   }
   {

@@ -14,6 +14,8 @@
 // internals of Rust's selection; here equal probabilities are ordered by
 // token id (lower first). The two agree whenever the kept probabilities are
 // distinct.
+#include <immintrin.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -48,30 +50,139 @@ uint32_t first_max(const float* v, size_t n) {
   return (uint32_t)best;
 }
 
-// ops::softmax_inplace (ops.rs:398-419).
+// expf of glibc on x86-64 with FMA (the variant f32::exp reaches there):
+// x * 32/ln2 = k + r, exp(x) = 2^(k/32) * p(r), a cubic p in double with
+// FMAs, T[i] = bits(2^(i/32)) - (i << 47) (the method of ARM's
+// optimized-routines). Four lanes per AVX2 step; lanes with |x| >= 88 or
+// NaN take the library call. The kernels' expf_glibc_t is the same
+// computation and was checked against the library on every float of
+// [-103.9, 88.7].
+const uint64_t kExp2T[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+// x[i] = expf(x[i] - mx) for i < n.
+__attribute__((target("avx2,fma"))) void exp_shift_avx2(float* x, size_t n, float mx) {
+  const __m256d inv_ln2n = _mm256_set1_pd(0x1.71547652b82fep+0 * 32.0);
+  const __m256d shift = _mm256_set1_pd(0x1.8p+52);
+  const __m256d c0 = _mm256_set1_pd(0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0);
+  const __m256d c1 = _mm256_set1_pd(0x1.ebfce50fac4f3p-3 / 32.0 / 32.0);
+  const __m256d c2 = _mm256_set1_pd(0x1.62e42ff0c52d6p-1 / 32.0);
+  const __m256d one = _mm256_set1_pd(1.0);
+  const __m128 vmx = _mm_set1_ps(mx);
+  const __m128i lim = _mm_set1_epi32(0x42b);
+  size_t i = 0;
+  for (; i + 4 <= n; i += 4) {
+    const __m128 xs = _mm_sub_ps(_mm_loadu_ps(x + i), vmx);
+    const __m128i top = _mm_and_si128(_mm_srli_epi32(_mm_castps_si128(xs), 20), _mm_set1_epi32(0x7ff));
+    if (_mm_movemask_epi8(_mm_cmpgt_epi32(lim, top)) != 0xffff) {  // a lane with |x| >= 88 or NaN
+      float v[4];
+      _mm_storeu_ps(v, xs);
+      for (int k = 0; k < 4; k++) x[i + k] = expf(v[k]);
+      continue;
+    }
+    const __m256d xd = _mm256_cvtps_pd(xs);
+    __m256d kd = _mm256_fmadd_pd(inv_ln2n, xd, shift);
+    const __m256i ki = _mm256_castpd_si256(kd);
+    kd = _mm256_sub_pd(kd, shift);
+    const __m256d r = _mm256_fmsub_pd(inv_ln2n, xd, kd);
+    const __m256i idx = _mm256_and_si256(ki, _mm256_set1_epi64x(31));
+    const __m256i t = _mm256_add_epi64(_mm256_i64gather_epi64((const long long*)kExp2T, idx, 8),
+                                       _mm256_slli_epi64(ki, 47));
+    const __m256d sc = _mm256_castsi256_pd(t);
+    const __m256d z = _mm256_fmadd_pd(c0, r, c1);
+    const __m256d r2 = _mm256_mul_pd(r, r);
+    __m256d y = _mm256_fmadd_pd(c2, r, one);
+    y = _mm256_fmadd_pd(z, r2, y);
+    y = _mm256_mul_pd(y, sc);
+    _mm_storeu_ps(x + i, _mm256_cvtpd_ps(y));
+  }
+  for (; i < n; i++) x[i] = expf(x[i] - mx);
+}
+
+// x[i] *= f (each product rounded once, as the scalar loop).
+__attribute__((target("avx2,fma"))) void scale_avx2(float* x, size_t n, float f) {
+  const __m256 vf = _mm256_set1_ps(f);
+  size_t i = 0;
+  for (; i + 8 <= n; i += 8) _mm256_storeu_ps(x + i, _mm256_mul_ps(_mm256_loadu_ps(x + i), vf));
+  for (; i < n; i++) x[i] *= f;
+}
+
+// The reference's max (ops.rs:402-407): x[0], then every later v > max. A
+// NaN in x[0] stays; later NaNs never compare greater and are skipped, as
+// max_ps(v, acc) skips a NaN v. Equal zeros of either sign give the same
+// exponentials, so which one is kept does not matter.
+__attribute__((target("avx2,fma"))) float max_ref_avx2(const float* x, size_t n) {
+  if (x[0] != x[0]) return x[0];
+  __m256 acc = _mm256_set1_ps(x[0]);
+  size_t i = 1;
+  for (; i + 8 <= n; i += 8) acc = _mm256_max_ps(_mm256_loadu_ps(x + i), acc);
+  float v[8];
+  _mm256_storeu_ps(v, acc);
+  float mx = v[0];
+  for (int k = 1; k < 8; k++) mx = v[k] > mx ? v[k] : mx;
+  for (; i < n; i++)
+    if (x[i] > mx) mx = x[i];
+  return mx;
+}
+
+// First index at or after i whose value is >= thr (n when none): the top-k
+// scan skips eight values per compare while none can enter the list.
+__attribute__((target("avx2,fma"))) size_t next_candidate_avx2(const float* x, size_t i, size_t n, float thr) {
+  const __m256 vt = _mm256_set1_ps(thr);
+  for (; i + 8 <= n; i += 8)
+    if (_mm256_movemask_ps(_mm256_cmp_ps(_mm256_loadu_ps(x + i), vt, _CMP_GE_OQ))) break;
+  for (; i < n; i++)
+    if (x[i] >= thr) return i;
+  return n;
+}
+
+bool have_avx2_fma() {
+  static const bool ok = __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+  return ok;
+}
+
+// ops::softmax_inplace (ops.rs:398-419): the exponentials first (they are
+// independent), then the sum in index order as the reference adds them.
 void softmax_ref(float* x, size_t n) {
   if (n == 0) return;
+  const bool vec = have_avx2_fma();
   float mx = x[0];
-  for (size_t i = 1; i < n; i++)
-    if (x[i] > mx) mx = x[i];
-  float sum = 0.0f;
-  for (size_t i = 0; i < n; i++) {
-    x[i] = expf(x[i] - mx);
-    sum += x[i];
+  if (vec) {
+    mx = max_ref_avx2(x, n);
+    exp_shift_avx2(x, n, mx);
+  } else {
+    for (size_t i = 1; i < n; i++)
+      if (x[i] > mx) mx = x[i];
+    for (size_t i = 0; i < n; i++) x[i] = expf(x[i] - mx);
   }
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) sum += x[i];
   if (sum > 0.0f) {
     const float inv = 1.0f / sum;
-    for (size_t i = 0; i < n; i++) x[i] *= inv;
+    if (vec)
+      scale_avx2(x, n, inv);
+    else
+      for (size_t i = 0; i < n; i++) x[i] *= inv;
   }
 }
 
 }  // namespace
 
+void softmax_inplace(float* x, size_t n) { softmax_ref(x, n); }
+
 uint32_t sample_logits(const float* logits, size_t n, const rlh_sampling_params& p, const uint32_t* recent,
                        size_t n_recent, uint64_t* state) {
   if (n == 0) return 0;
   if (p.temperature <= 0.0f && p.repetition_penalty == 1.0f) return first_max(logits, n);
-  std::vector<float> probs(logits, logits + n);
+  thread_local std::vector<float> probs;  // reused from call to call
+  probs.assign(logits, logits + n);
   // repetition penalty over the distinct tokens of the last repeat_last_n
   // (all when 0), each at most once (sampler.rs:82-102)
   if (p.repetition_penalty != 1.0f) {
@@ -90,18 +201,37 @@ uint32_t sample_logits(const float* logits, size_t n, const rlh_sampling_params&
   }
   if (p.temperature <= 0.0f) return first_max(probs.data(), n);
   const float inv_t = 1.0f / p.temperature;  // sampler.rs:115-118
-  for (float& v : probs) v *= inv_t;
+  if (have_avx2_fma())
+    scale_avx2(probs.data(), n, inv_t);
+  else
+    for (float& v : probs) v *= inv_t;
   softmax_ref(probs.data(), n);
   // top-k (sampler.rs:122-132), as a bounded selection: descending
   // probability, equal probabilities by token id
   const size_t k = (p.top_k == 0 || p.top_k > n) ? n : p.top_k;
   auto before = [&](uint32_t a, uint32_t b) { return probs[a] > probs[b] || (probs[a] == probs[b] && a < b); };
-  std::vector<uint32_t> idx(n);
-  for (size_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
+  thread_local std::vector<uint32_t> idx;
   if (k < n) {
-    std::partial_sort(idx.begin(), idx.begin() + k, idx.end(), before);
-    idx.resize(k);
+    // one pass keeping the k best in order; a later index never precedes an
+    // equal probability already kept, so the list equals a sort's first k
+    // (values below the last kept one are skipped eight at a time)
+    idx.assign(1, 0u);
+    const bool vec = have_avx2_fma();
+    for (size_t i = 1; i < n; i++) {
+      if (idx.size() == k) {
+        if (vec) {
+          i = next_candidate_avx2(probs.data(), i, n, probs[idx.back()]);
+          if (i >= n) break;
+        }
+        if (!before((uint32_t)i, idx.back())) continue;
+      }
+      auto at = std::upper_bound(idx.begin(), idx.end(), (uint32_t)i, before);
+      if (idx.size() == k) idx.pop_back();
+      idx.insert(at, (uint32_t)i);
+    }
   } else {
+    idx.resize(n);
+    for (size_t i = 0; i < n; i++) idx[i] = (uint32_t)i;
     std::sort(idx.begin(), idx.end(), before);
   }
   // top-p on the sorted list (sampler.rs:135-146)
@@ -134,6 +264,12 @@ uint32_t sample_logits(const float* logits, size_t n, const rlh_sampling_params&
 extern "C" {
 
 uint64_t rlh_sampler_init(uint64_t seed) { return seed | 1; }  // Sampler::new (sampler.rs:33-37)
+
+int rlh_softmax(float* x, uint64_t n) {
+  if (n && !x) return rlh::set_error(RLH_EINVAL, "null argument");
+  rlh::softmax_inplace(x, (size_t)n);
+  return RLH_OK;
+}
 
 int rlh_sample(const float* logits, uint64_t n, const rlh_sampling_params* p, const uint32_t* recent,
                uint64_t n_recent, uint64_t* rng_state, uint32_t* token) {

@@ -7,6 +7,8 @@
 
 namespace rlh {
 
+// ops::softmax_inplace (ops.rs:398-419) as the sampler runs it.
+void softmax_inplace(float* x, size_t n);
 // Sampler::sample on host logits; advances the xorshift64* state.
 uint32_t sample_logits(const float* logits, size_t n, const rlh_sampling_params& p, const uint32_t* recent,
                        size_t n_recent, uint64_t* state);

@@ -229,6 +229,7 @@ def load():
         "rlh_greedy_next": (I32, [P, P, ctypes.POINTER(U32)]),
         "rlh_generate_greedy": (I32, [P, P, U32, U64, P]),
         "rlh_sampler_init": (U64, [U64]),
+        "rlh_softmax": (I32, [P, U64]),
         "rlh_sample": (I32, [P, U64, ctypes.POINTER(SamplingParams), P, U64, ctypes.POINTER(U64),
                              ctypes.POINTER(U32)]),
         "rlh_sample_next": (I32, [P, P, ctypes.POINTER(SamplingParams), P, U64, ctypes.POINTER(U64),

@@ -71,3 +71,33 @@ def test_null_arguments_rejected():
     st = ctypes.c_uint64(1)
     p = rp()
     assert lib.rlh_sample(None, 4, ctypes.byref(p), None, 0, ctypes.byref(st), ctypes.byref(t)) == rlh.RLH_EINVAL
+
+
+@pytest.mark.parametrize("case", ["normal", "wide", "ties", "nan_first", "nan_later", "inf", "tiny"])
+def test_softmax_bit_exact_against_oracle(case):
+    """rlh_softmax (the sampler's softmax_inplace, ops.rs:398-419, with
+    vectorized exponentials) against the oracle's scalar restatement with
+    the platform expf: identical bits, including the NaN rule of the max
+    (a NaN first value propagates, later NaNs are skipped), infinities,
+    overflowing and underflowing differences, and odd lengths."""
+    rng = np.random.default_rng(7)
+    n = {"tiny": 5}.get(case, 151936 + 3)
+    x = (rng.standard_normal(n) * {"wide": 40.0}.get(case, 3.0)).astype(np.float32)
+    if case == "ties":
+        x = np.round(x * 4) / 4
+    elif case == "nan_first":
+        x[0] = np.nan
+    elif case == "nan_later":
+        x[17] = np.nan
+        x[n - 2] = np.nan
+    elif case == "inf":
+        x[3] = -np.inf
+        x[9] = np.inf if n > 9 else x[9]
+    elif case == "wide":
+        x[11] = 200.0
+        x[12] = -300.0
+    got = x.copy()
+    want = x.copy()
+    assert rlh.load().rlh_softmax(got.ctypes.data, n) == 0
+    oracle.load().orc_softmax_inplace(want.ctypes.data, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
