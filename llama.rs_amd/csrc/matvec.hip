@@ -505,6 +505,18 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
     I::terms(r, la, j, region + (m * R + rl) * stride + j * I::kT, h);
   };
+  // Split chain (single matrix, two-part items, one row tile per block, a
+  // long chain): the waves' tiles come in rounds (tile w + r * nwaves in
+  // round r) and the last wave runs out of tiles kr rounds early. Once every
+  // wave has finished its first kr tiles (a block counter in LDS), the last
+  // wave adds those rounds' terms in order while the others stream the rest;
+  // wave 0 continues the chain from that partial sum after the block
+  // barrier. Items are ordered by tile, so the first kr rounds hold the
+  // row's first kr * nwaves * TJ items.
+  const uint32_t kr = ntiles > nwaves ? (ntiles - 1 - (nwaves - 1)) / nwaves + 1 : 0;
+  const bool split = NM == 1 && kP == 2 && RB == 1 && ntiles % nwaves != 0 && kr > 0 && nsb * I::kT >= 256;
+  RLH_LDS uint32_t* rounds_done = (RLH_LDS uint32_t*)(misc + 3);
+  if (split && tid == 0) *rounds_done = 0u;  // seen by all after the prologue's barriers
   // the residual of the chain lane's row, read now so that the epilogue
   // does not wait for it
   float rsd = 0.0f;
@@ -531,13 +543,27 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     if (u + 2 < nunits) issue(ua, u + 2, 0);
     __builtin_amdgcn_sched_barrier(0);
     work(ub, u + 1, kH1);
+    if (split && u / 2 < kr) {  // tile u / 2 (one tile = two units) is done
+      __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): its terms are in LDS
+      if (lane == 0) __hip_atomic_fetch_add(rounds_done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  }
+  const uint32_t n_early = split ? kr * nwaves * TJ * I::kT : 0u;
+  if (split && wave == nwaves - 1) {
+    // every wave reaches kr tiles (each has at least kr), so the wait ends
+    while (__hip_atomic_load(rounds_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < kr * nwaves)
+      __builtin_amdgcn_s_sleep(1);
+    misc[4 + lane] = chain(region + (lane < nrows ? lane : 0) * stride, n_early);
   }
   __syncthreads();
 
-  // wave m < NM: lane r adds row r's terms of matrix m in order; lanes past
-  // the valid rows chain a copy of row 0 so that the wave stays converged
+  // wave m < NM: lane r adds row r's terms of matrix m in order (after the
+  // early part of a split chain); lanes past the valid rows chain a copy of
+  // row 0 so that the wave stays converged
   float acc = 0.0f;
-  if (wave < (uint32_t)NM) acc = chain(region + (wave * R + (lane < nrows ? lane : 0)) * stride, nsb * I::kT);
+  if (wave < (uint32_t)NM)
+    acc = seq_sum_lds(region + (wave * R + (lane < nrows ? lane : 0)) * stride + n_early, nsb * I::kT - n_early,
+                      split ? misc[4 + lane] : 0.0f);
 
   if (NM == 2) {
     if (wave == 1) misc[4 + lane] = acc;
@@ -724,7 +750,10 @@ bool mv_plan_finish(MvPlan& p) {
   p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
   p.lds = plan_lds(p, R, nm);
   const uint32_t ntiles = (R / tr) * ntj;
-  p.waves = std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
+  // a quantize prologue is VALU work on the whole row in every block: all
+  // eight waves take part even where fewer carry tiles (measured 6.3 -> 5.8
+  // us for the 8B attn_output)
+  p.waves = p.quant ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;
