@@ -573,10 +573,8 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     // divides the rows, so the lanes form whole Q8 blocks)
     const float x = acc, up = misc[4 + lane];
     const float h = (x / (1.0f + expf_glibc_t(-x, exp_tab))) * up;  // ops.rs:393-395
-    if (lane < nrows) {
-      if (g.y) ((RLH_GLOBAL float*)g.y)[row0 + lane] = h;
-      q8_quant_block32(h, g.hq, (row0 + lane) / 32);
-    }
+    if (lane < nrows && g.y) ((RLH_GLOBAL float*)g.y)[row0 + lane] = h;
+    q8_quant_wave2(h, g.hq, row0 / 32, nrows > 0, nrows > 32);  // the whole wave: nrows is 32 or 64
     return;
   }
 

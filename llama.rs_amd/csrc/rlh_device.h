@@ -292,6 +292,55 @@ __device__ __forceinline__ void q8_quant_block32(float v, Q8Out o, uint32_t blk)
   }
 }
 
+// The same for a whole wave holding two blocks, lanes 0..31 = block blk and
+// 32..63 = block blk + 1 (every lane active; the stores of half h happen
+// when store[h]). The reductions use DPP instead of LDS-routed shuffles:
+// inclusive prefix steps (row_shr 1, 2, 4, 8) leave each 16-lane row's
+// result in its lane 15, row_bcast:15 on rows 1 and 3 folds row 0 into row
+// 1 and row 2 into row 3, and readlane fetches the per-row / per-block
+// values. amax is order-free and the sums are exact integers.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_keep_f(float v) {  // invalid source: keep own value
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_zero_i(int v) {  // invalid source: 0
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ void q8_quant_wave2(float v, Q8Out o, uint32_t blk, bool store0, bool store1) {
+  const uint32_t lane = threadIdx.x & 63, l = lane & 31;
+  float a = fabsf(v);
+  a = fmaxf(a, dpp_keep_f<0x111>(a));
+  a = fmaxf(a, dpp_keep_f<0x112>(a));
+  a = fmaxf(a, dpp_keep_f<0x114>(a));
+  a = fmaxf(a, dpp_keep_f<0x118>(a));
+  a = fmaxf(a, dpp_keep_f<0x142, 0xa>(a));  // rows 1, 3 take rows 0, 2
+  const float amax_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 31));  // lane index: uniform
+  const float amax_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 63));
+  const float amax = lane < 32 ? amax_lo : amax_hi;
+  const float d = amax / 127.0f;
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  const int q = cvtps_packs_i8(__builtin_rintf(v * inv));
+  int s = q;
+  s += dpp_zero_i<0x111>(s);
+  s += dpp_zero_i<0x112>(s);
+  s += dpp_zero_i<0x114>(s);
+  s += dpp_zero_i<0x118>(s);
+  const int r0 = __builtin_amdgcn_readlane(s, 15), r1 = __builtin_amdgcn_readlane(s, 31);
+  const int r2 = __builtin_amdgcn_readlane(s, 47), r3 = __builtin_amdgcn_readlane(s, 63);
+  const bool hi = lane >= 32;
+  if (hi ? store1 : store0) {
+    const uint32_t b = blk + (hi ? 1u : 0u);
+    o.qs[(size_t)b * 32 + l] = (int8_t)q;
+    if (l == 0) {
+      o.d[b] = d;
+      o.s[b] = hi ? r2 + r3 : r0 + r1;
+      o.s16[(size_t)b * 2] = hi ? r2 : r0;
+      o.s16[(size_t)b * 2 + 1] = hi ? r3 : r1;
+    }
+  }
+}
+
 // Cross-lane moves inside groups of 8 lanes with DPP (no LDS round trip):
 // lane ^ 1 and lane ^ 2 within a quad, and the mirror 7 - i of the 8-lane
 // half-row, which pairs every lane of one quad with a lane of the other.
