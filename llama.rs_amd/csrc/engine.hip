@@ -357,9 +357,11 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
     {  // rmsnorm(x, attn_norm); q, k, v (model.rs:621-624)
       MvPlan p;
       mv_plan_init_norm(p, E, c->x, L.attn_norm.p, eps);
+      // attn_v first: its blocks (Q6_K in the Q4_K_M mix: larger items, 16
+      // terms per super-block) take longest, so they are dispatched first
+      mv_plan_add(p, L.v.dm, c->v, nullptr);
       mv_plan_add(p, L.q.dm, c->q, nullptr);
       mv_plan_add(p, L.k.dm, c->k, nullptr);
-      mv_plan_add(p, L.v.dm, c->v, nullptr);
       mv_plan_finish(p);
       mv_launch(st, p);
     }
@@ -1284,9 +1286,9 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
         mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
       } else if (qkv) {
         mv_plan_init_norm(p, cfg.n_embd, c->x, L.attn_norm.p, cfg.rms_eps);
+        mv_plan_add(p, L.v.dm, c->v, nullptr);  // as the decode step orders them
         mv_plan_add(p, L.q.dm, c->q, nullptr);
         mv_plan_add(p, L.k.dm, c->k, nullptr);
-        mv_plan_add(p, L.v.dm, c->v, nullptr);
       } else {
         const DevTensor* t = find_matrix(m, kind, (int)l);
         if (!t || !t->set) return fail(RLH_EINVAL, "no such matrix");
