@@ -43,11 +43,12 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused);
 // softmax_inplace of every score row (probabilities overwrite the scores).
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a);
 // Decode (one token) after the scores: softmax and the ordered V
-// accumulation in one kernel, otherwise launch_attn_softmax + the decode PV
-// kernel. resident (when attn_dec_v_lds is nonzero): the kernel that keeps
-// its V slice in LDS, which writes out in f32 only; the other variants
-// also write the Q8 blocks out_q8.
-void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool resident);
+// accumulation. f32_out: out in f32 only (the caller quantizes it) by the
+// kernel that keeps its V slices in LDS when attn_dec_v_lds is nonzero,
+// else by launch_attn_softmax + a PV kernel streaming V and p through LDS
+// rings (any context). Otherwise the kernels that also write the Q8 blocks
+// out_q8.
+void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool f32_out);
 // LDS of the resident-V decode kernel (0 when it does not apply: more than 4
 // query heads per KV head or too many positions).
 size_t attn_dec_v_lds(uint32_t t_max, uint32_t group);

@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "attention.h"
@@ -499,6 +500,48 @@ constexpr int kVDma = 12;             // V-slice DMA pieces per wave (16 rows ea
 constexpr uint32_t kDecVMaxCtx = 8u * kVDma * 16u;  // 1536 positions
 constexpr size_t kDecVLdsMax = 150u * 1024u;
 
+// The chain wave's part of a product ring (chunk c of kPrC positions in
+// slot c % kPrSlots of slot_floats floats, chain lane l's kPrC products at
+// l * kPrStride in the slot, one block barrier per chunk): o = prod_j + o
+// in position order for chain lane lc. Chunk c + 1 is complete while chunk
+// c is added (it was made before the previous barrier), so the reads run
+// one 32-position batch ahead across chunk boundaries; the chain wave
+// writes no LDS and meets the producers at a plain s_barrier. Lanes past the
+// chain count pass a clamped lc and run a copy of a chain (uniform control
+// flow).
+__device__ __forceinline__ float chain_products(const lfloat* pr, uint32_t lc, uint32_t t, uint32_t nch,
+                                                uint32_t slot_floats) {
+  const lfloat* base = pr + lc * kPrStride;
+  auto slotp = [&](uint32_t c) { return (const lf32x4d*)(base + (c % kPrSlots) * slot_floats); };
+  float o = 0.0f;
+  f32x4d_t xa[8], xb[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) xa[i] = slotp(0)[i];
+  for (uint32_t c = 0; c < nch; c++) {
+    const lf32x4d* sc = slotp(c);
+    const lf32x4d* sn = slotp(c + 1);  // past the last chunk: read, never added
+    const uint32_t n = t - c * kPrC;
+    if (n >= (uint32_t)kPrC) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xb[i] = sc[8 + i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o = (((o + xa[i].x) + xa[i].y) + xa[i].z) + xa[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) xa[i] = sn[i];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; i++) o = (((o + xb[i].x) + xb[i].y) + xb[i].z) + xb[i].w;
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      o = seq_sum_lds((const lfloat*)sc, n, o);
+    }
+    asm volatile("s_barrier" ::: "memory");
+  }
+  return o;
+}
+
 __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   __shared__ float red[8 * kAttnMaxGroup];
   __shared__ float s_mx[kAttnMaxGroup], s_inv[kAttnMaxGroup];
@@ -616,42 +659,108 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
     }
     return;
   }
-  // the chain wave: o = prod_j + o in position order. Chunk c + 1 is complete
-  // while chunk c is added (it was made before the previous barrier), so the
-  // reads run one 32-position batch ahead across chunk boundaries; the
-  // chain wave writes no LDS and meets the producers at a plain s_barrier.
-  // Lanes past NL run a copy of the last chain (uniform control flow).
-  const uint32_t lc = min((uint32_t)lane, NL - 1);
-  const lfloat* base = pr + lc * kPrStride;
-  auto slotp = [&](uint32_t c) { return (const lf32x4d*)(base + (c % kPrSlots) * (64 * kPrStride)); };
-  float o = 0.0f;
-  f32x4d_t xa[8], xb[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) xa[i] = slotp(0)[i];
-  for (uint32_t c = 0; c < nch; c++) {
-    const lf32x4d* sc = slotp(c);
-    const lf32x4d* sn = slotp(c + 1);  // past the last chunk: read, never added
-    const uint32_t n = t - c * kPrC;
-    if (n >= (uint32_t)kPrC) {
-#pragma unroll
-      for (int i = 0; i < 8; i++) xb[i] = sc[8 + i];
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 8; i++) o = (((o + xa[i].x) + xa[i].y) + xa[i].z) + xa[i].w;
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 8; i++) xa[i] = sn[i];
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 8; i++) o = (((o + xb[i].x) + xb[i].y) + xb[i].z) + xb[i].w;
-      __builtin_amdgcn_sched_barrier(0);
-    } else {
-      o = seq_sum_lds((const lfloat*)sc, n, o);
-    }
-    asm volatile("s_barrier" ::: "memory");
-  }
+  const float o = chain_products(pr, min((uint32_t)lane, NL - 1), t, nch, 64 * kPrStride);
   if ((uint32_t)lane < NL)
     ((RLH_GLOBAL float*)a.out)[(g * G + lane / kVsW) * kHd + d0 + lane % kVsW] = o;
+}
+
+
+// Decode PV over any context (after k_attn_softmax wrote the probabilities
+// over the scores), V and p streamed through LDS. grid (128 / W slices of W
+// dimensions, KVH), W = 16 (8 when 8 query heads share a KV head, so a block
+// never has more than 64 chains), block 512. Wave 0 lane l < NL = G * W
+// (head l / W, dimension l % W) adds the products in position order
+// (chain_products); waves 1..7 (producers) stream each 64-position chunk's
+// p rows and V slice into an 8-slot input ring by DMA, and form the products
+// two chunks ahead of the chain into the 3-slot product ring (quads w - 1,
+// w + 6, w + 13 of a chunk, as in k_attn_dec_v). Every producer wave issues
+// exactly two DMA copies per chunk (duplicates of its last job where a chunk
+// has fewer jobs: the same bytes to the same place), so its vector-memory
+// count says when a chunk it is about to use has landed: at the end of
+// iteration c it waits for chunk c + 3 (the copies of chunks c + 4 .. c + 8
+// may stay in flight), and the block barrier then makes every wave's copies
+// visible. The output is written in f32 (attn_output quantizes the row).
+constexpr int kRingSlots = 8;  // input ring: chunks c .. c + 7 resident or in flight
+
+__host__ __device__ inline uint32_t pv_ring_width(uint32_t group) { return group > 4 ? 8u : 16u; }
+
+__host__ __device__ inline size_t pv_ring_lds(uint32_t group) {
+  const size_t w = pv_ring_width(group);
+  const size_t prod = (size_t)kPrSlots * 64 * kPrStride * 4;
+  const size_t in_slot = ((size_t)group * kPrC + (size_t)kPrC * w) * 4;
+  return prod + kRingSlots * in_slot;
+}
+
+__global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds_generic[];
+  const uint32_t G = (uint32_t)(a.H / a.KVH);
+  const uint32_t W = pv_ring_width(G), NL = G * W;
+  const uint32_t in_floats = G * kPrC + kPrC * W;  // p rows [G][64], then V rows [64][W]
+  lfloat* pr = (lfloat*)lds_generic;
+  lfloat* in = pr + kPrSlots * 64 * kPrStride;
+  const uint32_t d0 = blockIdx.x * W, g = blockIdx.y;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t kvd = (uint32_t)a.KVH * kHd;
+  const uint32_t t = a.pos0[0] + 1;
+  const uint32_t nch = (t + kPrC - 1) / kPrC;
+  const uint32_t nvj = W / 4;       // V copies per chunk: 16 B per lane, 256 / W rows each
+  const uint32_t njobs = nvj + G;   // + one copy per p row (4 B per lane)
+  const uint32_t pw = wave - 1;     // producer index (waves 1..7)
+  auto fetch = [&](uint32_t c) {
+    lfloat* slot = in + (c % kRingSlots) * in_floats;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t j = min(2 * pw + (uint32_t)k, njobs - 1);
+      if (j < nvj) {
+        const uint32_t rpi = 256 / W;  // rows per copy
+        const uint32_t row = min(c * kPrC + rpi * j + lane / (W / 4), t - 1);
+        __builtin_amdgcn_global_load_lds(
+            (const RLH_GLOBAL void*)(a.vcache + (size_t)row * kvd + g * kHd + d0 + (lane % (W / 4)) * 4),
+            (RLH_LDS void*)(slot + G * kPrC + rpi * j * W), 16, 0, 0);
+      } else {
+        const uint32_t h = j - nvj, pos = min(c * kPrC + lane, t - 1);
+        __builtin_amdgcn_global_load_lds(
+            (const RLH_GLOBAL void*)(a.scores + (size_t)(g * G + h) * a.t_stride + pos),
+            (RLH_LDS void*)(slot + h * kPrC), 4, 0, 0);
+      }
+    }
+  };
+  auto produce = [&](uint32_t c) {
+    if (lane >= NL) return;
+    const lfloat* slot = in + (c % kRingSlots) * in_floats;
+    lfloat* ps = pr + (c % kPrSlots) * (64 * kPrStride) + lane * kPrStride;
+    const lfloat* pc = slot + (lane / W) * kPrC;
+    const lfloat* vc = slot + G * kPrC + lane % W;
+    for (uint32_t q = pw; q < (uint32_t)kPrC / 4; q += 7) {
+      const f32x4_t p = *(const lf32x4*)(pc + 4 * q);
+      const lfloat* v = vc + 4 * q * W;
+      *(lf32x4*)(ps + 4 * q) = f32x4_t{p.x * v[0], p.y * v[W], p.z * v[2 * W], p.w * v[3 * W]};
+    }
+  };
+  // every wave meets the two set-up barriers, then the nch barriers of the
+  // chunk loop (wave 0 inside chain_products)
+  if (wave != 0) {
+    for (uint32_t c = 0; c < (uint32_t)kRingSlots; c++) fetch(c);
+    wait_vmcnt<2 * (kRingSlots - 2)>();  // chunks 0 and 1 have landed
+  }
+  lds_barrier();
+  if (wave != 0) {
+    produce(0);
+    if (nch > 1) produce(1);
+    wait_vmcnt<2 * (kRingSlots - 3)>();  // chunk 2
+  }
+  lds_barrier();
+  if (wave == 0) {
+    const float o = chain_products(pr, min(lane, NL - 1), t, nch, 64 * kPrStride);
+    if (lane < NL) ((RLH_GLOBAL float*)a.out)[(g * G + lane / W) * kHd + d0 + lane % W] = o;
+    return;
+  }
+  for (uint32_t c = 0; c < nch; c++) {
+    if (c + 2 < nch) produce(c + 2);
+    fetch(c + kRingSlots);               // into chunk c's input slot (its products were made at c - 2)
+    wait_vmcnt<2 * (kRingSlots - 3)>();  // chunk c + 3 has landed
+    lds_barrier();
+  }
 }
 
 // grid: (KVH, ceil(n_tok / TT)), TT = 32 / G tokens per block, latest (most
@@ -790,10 +899,16 @@ size_t attn_dec_v_lds(uint32_t t_max, uint32_t group) {
   return b <= kDecVLdsMax ? b : 0;
 }
 
-void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool resident) {
-  const size_t lv = resident ? attn_dec_v_lds(a.t_max, (uint32_t)(a.H / a.KVH)) : 0;
-  if (lv) {
-    hipLaunchKernelGGL(k_attn_dec_v, dim3(a.KVH, kHd / kVsW), dim3(512), lv, st, a);
+void launch_attn_decode(hipStream_t st, const AttnArgs& a, bool f32_out) {
+  const uint32_t G = (uint32_t)(a.H / a.KVH);
+  if (f32_out) {
+    const size_t lv = attn_dec_v_lds(a.t_max, G);
+    if (lv) {
+      hipLaunchKernelGGL(k_attn_dec_v, dim3(a.KVH, kHd / kVsW), dim3(512), lv, st, a);
+    } else {
+      launch_attn_softmax(st, a);
+      hipLaunchKernelGGL(k_attn_pv_ring, dim3(kHd / pv_ring_width(G), a.KVH), dim3(512), pv_ring_lds(G), st, a);
+    }
     return;
   }
   const size_t lds = attn_dec_fused_lds(a.t_max, (uint32_t)(a.H / a.KVH));
@@ -816,12 +931,16 @@ void launch_attn_pv(hipStream_t st, const AttnArgs& a, bool decode) {
 
 bool attn_init(uint32_t max_ctx) {
   if (max_ctx > kAttnMaxCtx) return false;
+  size_t ring_lds = 0;
+  for (uint32_t gq = 1; gq <= (uint32_t)kAttnMaxGroup; gq++) ring_lds = std::max(ring_lds, pv_ring_lds(gq));
   return hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_smpv_dec, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)kDecFusedLds) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_dec_v, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)kDecVLdsMax) == hipSuccess;
+                             (int)kDecVLdsMax) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_pv_ring, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)ring_lds) == hipSuccess;
 }
 
 }  // namespace rlh

@@ -319,17 +319,14 @@ float* layer_v(rlh_cache* c, uint32_t l) {
 
 enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
 
-// Decode attention keeps its V slices in LDS (and writes only f32) when the
-// cache's positions fit; attn_output then quantizes that f32 row itself.
-bool attn_resident(const rlh_cache* c) {
-  const rlh_config& cfg = c->m->cfg;
-  return c->m->o_quant_ok && attn_dec_v_lds((uint32_t)c->max_ctx, cfg.n_head / cfg.n_head_kv) != 0;
-}
+// Decode attention writes only f32 (its kernels split the head dimension in
+// 16-wide slices) when attn_output can quantize that row in its prologue.
+bool attn_f32_out(const rlh_cache* c) { return c->m->o_quant_ok; }
 
 // The attn_output plan of a decode step: its Q8 activation from the f32
 // attention output (resident attention) or the attention kernel's Q8 blocks.
 void plan_attn_output(MvPlan& p, rlh_cache* c, uint32_t qd) {
-  if (attn_resident(c)) {
+  if (attn_f32_out(c)) {
     mv_plan_init_quant(p, qd, c->attn);
   } else {
     mv_plan_init(p, qd, c->act_q);
@@ -391,7 +388,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       a.out = c->attn;
       a.out_q8 = c->act_q;
       launch_attn_scores(st, a, true);
-      launch_attn_decode(st, a, attn_resident(c));
+      launch_attn_decode(st, a, attn_f32_out(c));
     }
     {  // attn_output, x += (model.rs:713-716)
       MvPlan p;
@@ -628,7 +625,7 @@ int rlh_model_finalize(rlh_model* m) {
     mv_plan_add(p, L.down.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
     if (l == 0) m->o_quant_ok = true;
-    if (qd <= kMvMaxNormCols) {  // the attn_output launch after the resident-V attention kernel
+    if (qd <= kMvMaxQuantCols) {  // the attn_output launch after the f32-output attention kernels
       mv_plan_init_quant(p, (uint32_t)qd, &kShapeOnly);
       mv_plan_add(p, L.o.dm, nullptr, nullptr);
       m->o_quant_ok = m->o_quant_ok && mv_plan_finish(p);

@@ -87,8 +87,9 @@ void mv_plan_init(MvPlan& p, uint32_t cols, const Q8Mut& act);
 void mv_plan_init_norm(MvPlan& p, uint32_t cols, const float* x, const float* w, float eps);
 constexpr uint32_t kMvMaxNormCols = 7168;
 // Same, with the activation quantize_q8(x) of the f32 row x computed in the
-// kernel (no norm; cols <= kMvMaxNormCols).
+// kernel (no norm; cols <= kMvMaxQuantCols).
 void mv_plan_init_quant(MvPlan& p, uint32_t cols, const float* x);
+constexpr uint32_t kMvMaxQuantCols = 12288;
 // The f32 form of a Q8 launch's activation (used when a segment is Q5_K).
 void mv_plan_set_f32(MvPlan& p, const float* xf);
 void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);

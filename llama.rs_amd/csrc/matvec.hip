@@ -741,7 +741,7 @@ bool mv_plan_finish(MvPlan& p) {
     if (p.L.seg[s].w.ty == RLH_TYPE_Q5_K || (p.L.seg[s].pair && p.L.seg[s].w2.ty == RLH_TYPE_Q5_K)) p.L.need_xf = 1;
   if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // Q5_K needs the f32 activation
   if (plan_lds(p, R, nm) > kMaxLds) return false;
-  if (p.norm && (p.L.cols > kMvMaxNormCols || p.L.cols % 256 != 0)) return false;
+  if (p.norm && (p.L.cols > (p.quant ? kMvMaxQuantCols : kMvMaxNormCols) || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
   p.L.tile_stride = nsb * p.max_terms + 4;
   p.L.xf_off = plan_act_bytes(p);
