@@ -546,6 +546,7 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   __shared__ float red[8 * kAttnMaxGroup];
   __shared__ float s_mx[kAttnMaxGroup], s_inv[kAttnMaxGroup];
   __shared__ int s_on[kAttnMaxGroup];
+  __shared__ uint32_t s_exp_done[kDecVMaxCtx / 256];
   __shared__ uint64_t tab_g[32];
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   lu64* tab = (lu64*)tab_g;
@@ -558,6 +559,7 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvd = a.KVH * kHd;
   const uint32_t t = a.pos0[0] + 1;
+  if (tid < kDecVMaxCtx / 256) s_exp_done[tid] = 0u;  // seen by all after the first barrier
   const float* srow = a.scores + (size_t)g * G * a.t_stride;
   // score rows -> LDS (positions past t repeat the last score; their slots
   // lie inside the row stride), the exp table, then the V slice
@@ -608,17 +610,41 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
     s_mx[tid] = x0 != x0 ? x0 : m;
   }
   lds_barrier();
-  if (hon) {
-    const float m = s_mx[hg];
-    for (uint32_t q = lt; q < nq4; q += TPH) {
-      const f32x4_t x = *(const lf32x4*)(eh + 4 * q);
-      *(lf32x4*)(eh + 4 * q) = f32x4_t{expf_glibc_t(x.x - m, tab), expf_glibc_t(x.y - m, tab),
-                                       expf_glibc_t(x.z - m, tab), expf_glibc_t(x.w - m, tab)};
+  // The exponentials, 256 positions of every row at a time, by waves 1..3
+  // and 5..7; each of waves 1..7 announces a finished chunk on that chunk's counter, and lanes
+  // 0..G-1 of wave 0 run the G sequential sums right behind them, each chunk
+  // once all seven waves have announced it (every wave finishes every chunk,
+  // so each wait ends). One counter per chunk: waves without work in a chunk
+  // run ahead, so a single running total would not say which chunks are done.
+  constexpr uint32_t kExpC = 256;
+  RLH_LDS uint32_t* exp_done = (RLH_LDS uint32_t*)s_exp_done;
+  const uint32_t nek = (t + kExpC - 1) / kExpC;
+  if (wave != 0) {
+    // wave 4 runs on wave 0's SIMD: it takes no exponentials (they would
+    // take issue cycles from the sums) and only announces the chunks
+    const uint32_t xw = wave < 4 ? wave - 1 : wave - 2;
+    for (uint32_t k = 0; k < nek; k++) {
+      for (uint32_t i = wave == 4 ? ~0u : xw * 64 + lane; i < (uint32_t)G * (kExpC / 4); i += 384) {
+        const uint32_t h = i / (kExpC / 4), q = k * (kExpC / 4) + i % (kExpC / 4);
+        if (q < nq4) {
+          lfloat* x4 = e + h * RS + 4 * q;
+          const float m = s_mx[h];
+          const f32x4_t x = *(const lf32x4*)x4;
+          *(lf32x4*)x4 = f32x4_t{expf_glibc_t(x.x - m, tab), expf_glibc_t(x.y - m, tab),
+                                 expf_glibc_t(x.z - m, tab), expf_glibc_t(x.w - m, tab)};
+        }
+      }
+      __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): the chunk is in LDS
+      if (lane == 0) __hip_atomic_fetch_add(exp_done + k, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
-  }
-  lds_barrier();
-  if (tid < G) {  // the G sequential sums side by side, one lane each
-    const float sum = seq_sum_lds(e + tid * RS, t);
+  } else if (tid < G) {  // the G sequential sums side by side, one lane each
+    float sum = 0.0f;
+    for (uint32_t k = 0; k < nek; k++) {
+      while (__hip_atomic_load(exp_done + k, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 7u)
+        __builtin_amdgcn_s_sleep(1);
+      const uint32_t n = t - k * kExpC < kExpC ? t - k * kExpC : kExpC;
+      sum = seq_sum_lds(e + tid * RS + k * kExpC, n, sum);
+    }
     s_on[tid] = sum > 0.0f;
     s_inv[tid] = 1.0f / sum;
   }
@@ -647,9 +673,37 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
       *(lf32x4*)(slot + 4 * q) = f32x4_t{x.x * v[0], x.y * v[kVsW], x.z * v[2 * kVsW], x.w * v[3 * kVsW]};
     }
   };
-  if (wave != 0) {
-    produce(0);
-    if (nch > 1) produce(1);
+  if (wave != 0 && (uint32_t)lane < NL) {
+    // chunks 0 and 1 before the chain starts: all their reads first
+    f32x4_t px[2][3];
+    float vx[2][3][4];
+#pragma unroll
+    for (int cc = 0; cc < 2; cc++) {
+      const uint32_t c = min((uint32_t)cc, nch - 1);
+      const lfloat* ec = e + ph * RS + c * kPrC;
+      const lfloat* vc = vs + c * kPrC * kVsW + lane % kVsW;
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const uint32_t q = min((uint32_t)wave - 1 + 7u * i, (uint32_t)kPrC / 4 - 1);
+        px[cc][i] = *(const lf32x4*)(ec + 4 * q);
+#pragma unroll
+        for (int r = 0; r < 4; r++) vx[cc][i][r] = vc[(4 * q + r) * kVsW];
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < 2; cc++) {
+      if ((uint32_t)cc >= nch) break;
+      lfloat* slot = pr + cc * (64 * kPrStride) + lane * kPrStride;
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const uint32_t q = (uint32_t)wave - 1 + 7u * i;
+        if (q >= (uint32_t)kPrC / 4) break;
+        f32x4_t x = px[cc][i];
+        if (pon) x = f32x4_t{x.x * pinv, x.y * pinv, x.z * pinv, x.w * pinv};
+        *(lf32x4*)(slot + 4 * q) =
+            f32x4_t{x.x * vx[cc][i][0], x.y * vx[cc][i][1], x.z * vx[cc][i][2], x.w * vx[cc][i][3]};
+      }
+    }
   }
   lds_barrier();
   if (wave != 0) {

@@ -103,14 +103,17 @@ def test_decode_attention_paths(max_ctx):
     oc.close()
 
 
-@pytest.mark.parametrize("max_ctx,n_prompt", [(300, 62), (1200, 250), (4096, 130), (8000, 70)])
+@pytest.mark.parametrize("max_ctx,n_prompt", [(300, 62), (1200, 250), (1200, 600), (1200, 1100), (4096, 130),
+                                              (8000, 70)])
 def test_decode_attention_g4_paths(max_ctx, n_prompt):
     """Decode attention with 4 query heads per KV head. Caches up to about
     1200 positions take the kernel that keeps its V slices in LDS (the
-    products run one 64-position chunk ahead of the ordered adds: the steps
-    cross chunk boundaries and end on ragged chunks), 4096 positions the
-    streamed fused kernel, 8000 the separate softmax and V kernels. Logits
-    bit-exact in every step."""
+    products run two 64-position chunks ahead of the ordered adds, the
+    exponentials 256-position chunks ahead of the softmax sums: the steps
+    cross chunk boundaries, end on ragged chunks and, at 600 and 1100
+    positions, use three and five exponential chunks), 4096 and 8000
+    positions the softmax kernel and the PV kernel that streams p and V
+    through LDS rings. Logits bit-exact in every step."""
     print(f"decode attention g4 max_ctx {max_ctx} prompt {n_prompt}", flush=True)
     spec, tensors, m, om = _get("tiny-g4-q4km")
     prompt = rlh.synth_tokens(55, n_prompt, spec.vocab)
