@@ -634,14 +634,21 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
                                  expf_glibc_t(x.z - m, tab), expf_glibc_t(x.w - m, tab)};
         }
       }
+      // LDS-only hand-over: a wave's LDS operations complete in order, so
+      // lgkmcnt(0) before a relaxed add publishes the chunk (release/acquire
+      // atomics would also wait for the wave's in-flight global copies);
+      // the asm statements keep the compiler from moving accesses across
+      asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): the chunk is in LDS
-      if (lane == 0) __hip_atomic_fetch_add(exp_done + k, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      asm volatile("" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(exp_done + k, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   } else if (tid < G) {  // the G sequential sums side by side, one lane each
     float sum = 0.0f;
     for (uint32_t k = 0; k < nek; k++) {
-      while (__hip_atomic_load(exp_done + k, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 7u)
+      while (__hip_atomic_load(exp_done + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 7u)
         __builtin_amdgcn_s_sleep(1);
+      asm volatile("" ::: "memory");
       const uint32_t n = t - k * kExpC < kExpC ? t - k * kExpC : kExpC;
       sum = seq_sum_lds(e + tid * RS + k * kExpC, n, sum);
     }

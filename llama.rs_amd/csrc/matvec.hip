@@ -544,15 +544,22 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     __builtin_amdgcn_sched_barrier(0);
     work(ub, u + 1, kH1);
     if (split && u / 2 < kr) {  // tile u / 2 (one tile = two units) is done
+      // LDS-only hand-over (a wave's LDS operations complete in order):
+      // lgkmcnt(0), then a relaxed add; release/acquire atomics would also
+      // wait for the unit loads in flight. The asm statements keep the
+      // compiler from moving accesses across.
+      asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): its terms are in LDS
-      if (lane == 0) __hip_atomic_fetch_add(rounds_done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      asm volatile("" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(rounds_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
   const uint32_t n_early = split ? kr * nwaves * TJ * I::kT : 0u;
   if (split && wave == nwaves - 1) {
     // every wave reaches kr tiles (each has at least kr), so the wait ends
-    while (__hip_atomic_load(rounds_done, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < kr * nwaves)
+    while (__hip_atomic_load(rounds_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kr * nwaves)
       __builtin_amdgcn_s_sleep(1);
+    asm volatile("" ::: "memory");
     misc[4 + lane] = chain(region + (lane < nrows ? lane : 0) * stride, n_early);
   }
   __syncthreads();
