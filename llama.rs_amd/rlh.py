@@ -134,6 +134,13 @@ SPECS = {
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
     # 4 query heads per KV head (the 4B / 8B grouping) and a long context window
     "tiny-g4-q4km": ModelSpec("tiny-g4-q4km", 2, 256, 512, 8, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
+    # 1 and 2 query heads per KV head with a long context window
+    "tiny-g1-q4km": ModelSpec("tiny-g1-q4km", 2, 256, 512, 2, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    "tiny-g2-q4km": ModelSpec("tiny-g2-q4km", 2, 256, 512, 4, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    # 104 query heads (13312-wide attention rows: attn_output takes Q8 blocks
+    # from the attention kernels instead of quantizing the row itself)
+    "tiny-wide-q4km": ModelSpec("tiny-wide-q4km", 2, 256, 512, 104, 13, 1000, True, _q4km(True, Q4_K, None),
+                                n_ctx=4096),
 }
 
 

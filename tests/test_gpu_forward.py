@@ -133,6 +133,35 @@ def test_decode_attention_g4_paths(max_ctx, n_prompt):
     oc.close()
 
 
+@pytest.mark.parametrize("name,max_ctx,n_prompt", [("tiny-g1-q4km", 64, 30), ("tiny-g1-q4km", 2000, 200),
+                                                   ("tiny-g2-q4km", 64, 30), ("tiny-g2-q4km", 2000, 130),
+                                                   ("tiny-wide-q4km", 64, 20), ("tiny-wide-q4km", 3000, 100)])
+def test_decode_attention_groupings(name, max_ctx, n_prompt):
+    """Decode attention with 1 and 2 query heads per KV head (the resident-V
+    kernel for short caches, the softmax + streamed-ring PV kernels past
+    ~1500 positions) and with 13312-wide attention rows, where attn_output
+    reads the Q8 blocks the attention kernels write (the fused streamed
+    kernel for 64 positions, the softmax kernel + the streamed PV kernel
+    for 3000). Logits bit-exact."""
+    print(f"decode attention {name} max_ctx {max_ctx} prompt {n_prompt}", flush=True)
+    spec, tensors, m, om = _get(name)
+    prompt = rlh.synth_tokens(66, n_prompt, spec.vocab)
+    c = m.new_cache(max_ctx)
+    oc = om.new_cache(max_ctx)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg), bits(rg))
+    lib = oracle.load()
+    tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    for i in range(5):
+        lg = c.forward_into(np.array([tok], np.uint32), n_prompt + i)
+        rg = oc.forward_into(np.array([tok], np.uint32), n_prompt + i, oracle.MODE_DEFAULT)
+        assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ (rel {rel_l2(lg, rg):.2e})"
+        tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    c.close()
+    oc.close()
+
+
 @pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
 def test_generate_greedy_matches_cpu_tokens(name):
     spec, tensors, m, om = _get(name)
