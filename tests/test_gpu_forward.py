@@ -1,7 +1,7 @@
 """End-to-end parity of the device token loop against the CPU oracle.
 
 Reference modes: decode = the AVX2 integer path (ops.rs:93-128); prefill =
-RUST_LLAMA_BATCH_INT=1 (ops.rs:192-236). Bars from the north star:
+RUST_LLAMA_BATCH_INT=1 (ops.rs:192-236). Required bars:
 per-layer hidden states within 1e-3 relative L2, logits within 2e-3,
 identical greedy tokens. The device path is built to match bit for bit, and
 these tests assert that stronger property (the L2 numbers are printed).

@@ -1,7 +1,7 @@
 """Op-level parity: HIP kernels (through the C ABI) against the CPU oracle.
 
 Bars: bit-exact for dequantisation, Q8 activation blocks and integer block
-dots, and bit-exact for the matvec rows too (the kernel
+dots (the required bar), and bit-exact for the matvec rows too (the kernel
 sums the per-group terms in the reference order).
 """
 import numpy as np
