@@ -123,7 +123,7 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1:
-        print("bench.py: this build runs on one GPU only (the token loop of one model on one MI355X); "
+        print("bench.py: the benchmark runs on one GPU only (the token loop of one model on one MI355X); "
               "--gpus must be 1", file=sys.stderr)
         sys.exit(2)
 

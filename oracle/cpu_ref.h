@@ -2,7 +2,7 @@
 //
 // TEST INFRASTRUCTURE ONLY. This code is the parity oracle and the CPU
 // baseline. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
-// leg may load it, and only as the checker. The product path (librlh.so)
+// leg may load it, and only to check results against. The product path (librlh.so)
 // never links or calls anything here.
 //
 // It restates, function by function, the reference's x86-64 AVX2 path

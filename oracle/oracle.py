@@ -1,6 +1,6 @@
 """ctypes binding of the CPU oracle (liboracle.so, oracle/cpu_ref.h).
 
-TEST INFRASTRUCTURE ONLY: the parity checker and the CPU baseline. Only
+TEST INFRASTRUCTURE ONLY: the parity reference and the CPU baseline. Only
 tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load it.
 """
 import ctypes
