@@ -1,18 +1,27 @@
 """Benchmark of the Qwen3 token loop on one MI355X.
 
-Workload (default): Qwen3-8B shape, Q4_K_M mix, seeded synthetic weights;
-512-token random prompt (batched prefill), then greedy decode. Protocol of
-the reference's `bench` command (src/main.rs:466-530): warm-up prefill,
-reset, timed prefill, timed greedy decode loop (argmax after every step,
-here fused on the device). A "step" is one decode token; `value` is decode
-tokens per second. Prefill tok/s, the per-token HBM roofline and the
-dominant kernel's roofline are reported alongside, plus the CPU reference
-(oracle) timed on a bounded sample of the same workload.
+Protocol of the reference's `bench` command (src/main.rs:466-530) on seeded
+synthetic weights. A "step" is one pass of the whole workload: reset the
+cache, prefill the prompt (timed, logits copied to the host as the reference
+writes them), take the argmax of the prefill logits (untimed, as main.rs),
+then decode the workload's full token count (timed: every decode step with
+its argmax, or with the host sampler for workload 5). `--steps K` runs K
+timed passes after `--warmup W` untimed ones; the decode window of every
+pass is the workload's own (512 tokens at KV 512 -> 1024 for the headline),
+whatever K is.
+
+`value` = decode tokens per second over the K passes (total decode tokens /
+total decode time) with the weights resident in HBM. Reported alongside:
+prefill tok/s, the decode step's HBM bytes and fraction of peak, the
+dominant decode kernel's roofline (the fused rmsnorm + gate/up + silu*up
+matvec, timed per launch inside real decode steps with HIP events bound to
+the launch; its HBM traffic from the committed rocprofv3 counter summary),
+and the CPU oracle (the C++ restatement of the reference's AVX2 path) on a
+bounded sample of the same workload on the host cores.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 1..5]
 
-Workloads (the five benchmark configurations; 4 is the default and the
-headline):
+Workloads (4 is the default and the headline):
   1  Qwen3-0.6B Q4_K_M   48-token prompt,   32 greedy tokens
   2  Qwen3-0.6B Q8_0     48-token prompt,  128 greedy tokens (KV up to 176)
   3  Qwen3-4B  Q4_K_M   256-token prompt,  256 greedy tokens
@@ -22,6 +31,7 @@ headline):
      CLI's fixed seed; src/main.rs:44-52)
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -37,15 +47,16 @@ import rlh  # noqa: E402
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
 
+WORKLOADS = rlh.WORKLOADS
 
-# workload -> (model, prompt tokens, decode tokens, sampled)
-WORKLOADS = {
-    1: ("qwen3-0.6b-q4km", 48, 32, False),
-    2: ("qwen3-0.6b-q8_0", 48, 128, False),
-    3: ("qwen3-4b-q4km", 256, 256, False),
-    4: ("qwen3-8b-q4km", 512, 512, False),
-    5: ("qwen3-32b-q4km", 4096, 256, True),
-}
+# CPU oracle sample per workload: (prompt tokens prefilled in each mode,
+# greedy decode tokens), sized for roughly 10-30 s of host work.
+CPU_SAMPLE = {1: (48, 32), 2: (48, 128), 3: (128, 64), 4: (128, 64), 5: (32, 8)}
+
+METRIC = "decode tok/s, prefill tok/s, % HBM roofline"
+MODEL_NAMES = {"qwen3-0.6b-q4km": "Qwen3-0.6B Q4_K_M", "qwen3-0.6b-q8_0": "Qwen3-0.6B Q8_0",
+               "qwen3-4b-q4km": "Qwen3-4B Q4_K_M", "qwen3-8b-q4km": "Qwen3-8B Q4_K_M",
+               "qwen3-32b-q4km": "Qwen3-32B Q4_K_M"}
 
 
 def log(msg):
@@ -57,21 +68,59 @@ def kv_read_bytes(spec, t):
     return 2 * spec.n_layer * t * spec.n_head_kv * spec.head_dim * 4
 
 
-def cpu_baseline(spec, tensors, prompt, n_decode, threads):
-    """The oracle (C++ restatement of the reference AVX2 path) on the host
-    cores: default modes as the reference ships them. Bounded sample: a
-    short prefill then n_decode timed greedy steps."""
+def run_pass(cache, prompt, n_decode, sampled, params, never):
+    """One workload pass; returns (prefill_s, decode_s, tokens)."""
+    cache.reset()
+    t0 = time.perf_counter()
+    logits = cache.forward_into(prompt, 0)
+    prefill_s = time.perf_counter() - t0
+    if not sampled:
+        first = cache.greedy_next()
+        t1 = time.perf_counter()
+        toks = cache.generate_greedy(first, n_decode)
+        return prefill_s, time.perf_counter() - t1, toks
+    # Model::generate's loop (model.rs:760-774): sample from the last logits,
+    # append, forward the token; the sampler runs on the host
+    del logits
+    P = len(prompt)
+    recent = np.empty(P + n_decode, np.uint32)
+    recent[:P] = prompt
+    state = ctypes.c_uint64(rlh.load().rlh_sampler_init(params.seed))
+    one = np.empty(1, np.uint32)
+    t1 = time.perf_counter()
+    for i in range(n_decode):
+        tok = cache.sample_next(params, recent[:P + i], state)
+        if tok == never:
+            raise RuntimeError("sampled the end-of-sequence id")
+        recent[P + i] = tok
+        one[0] = tok
+        cache.forward_into(one, P + i, copy=False)
+    return prefill_s, time.perf_counter() - t1, recent[P:].copy()
+
+
+def cpu_baseline(spec, tensors, prompt, n_prompt, n_decode):
+    """The oracle on the host cores: prefill of n_prompt tokens in the
+    reference's default mode (f32 fused products, as shipped) and with
+    RUST_LLAMA_BATCH_INT=1, then n_decode greedy tokens in the default mode
+    (AVX2 integer path), by the cmd_bench protocol."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
     lib = oracle.load()
-    lib.orc_set_threads(threads)
+    threads = lib.orc_get_threads()
     om = oracle.OracleModel(spec, tensors)
-    oc = om.new_cache(len(prompt) + n_decode + 1)
-    res, toks = oc.bench(prompt, n_decode, oracle.MODE_DEFAULT, warmup=False)
+    oc = om.new_cache(n_prompt + n_decode + 1)
+    p = prompt[:n_prompt]
+    t0 = time.time()
+    res_def, toks = oc.bench(p, n_decode, oracle.MODE_DEFAULT, warmup=False)
+    res_int, _ = oc.bench(p, 0, oracle.MODE_BATCH_INT, warmup=False)
+    wall = time.time() - t0
     oc.close()
     om.close()
-    return res, toks
+    return {"decode_tok_s": res_def.generated / res_def.decode_s,
+            "prefill_tok_s_default": res_def.prompt_len / res_def.prefill_s,
+            "prefill_tok_s_batch_int": res_int.prompt_len / res_int.prefill_s,
+            "generated": res_def.generated, "threads": threads, "wall_s": wall}
 
 
 def measured_traffic(config):
@@ -91,8 +140,6 @@ def measured_traffic(config):
 def calibration_copy(mb):
     """A device-to-device copy of `mb` MiB (the runtime's copy kernel): the
     known-size reference for scaling the HBM byte counters."""
-    import ctypes
-
     hip = ctypes.CDLL("libamdhip64.so")
     n = mb << 20
     a, b = ctypes.c_void_p(), ctypes.c_void_p()
@@ -111,13 +158,12 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", type=int, default=4, choices=sorted(WORKLOADS))
-    ap.add_argument("--steps", type=int, default=None, help="timed decode tokens (default: the workload's)")
-    ap.add_argument("--warmup", type=int, default=16, help="untimed decode tokens after the warm-up prefill")
-    ap.add_argument("--config", default=None, help="model shape (default: the workload's)")
-    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: the workload's)")
-    ap.add_argument("--seed", type=int, default=20260)
-    ap.add_argument("--cpu-decode", type=int, default=6, help="CPU baseline decode tokens (0 = skip)")
-    ap.add_argument("--cpu-prompt", type=int, default=8, help="CPU baseline prompt tokens")
+    ap.add_argument("--steps", type=int, default=3, help="timed passes of the whole workload")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed passes before them")
+    ap.add_argument("--seed", type=int, default=rlh.WORKLOAD_SEED)
+    ap.add_argument("--probe-steps", type=int, default=32,
+                    help="decode steps whose dominant-kernel launches are timed with HIP events")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle sample")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -126,128 +172,124 @@ def main():
         print("bench.py: the benchmark runs on one GPU only (the token loop of one model on one MI355X); "
               "--gpus must be 1", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
 
-    wl_config, wl_prompt, wl_steps, sampled = WORKLOADS[args.workload]
-    args.config = args.config or wl_config
-    args.prompt = args.prompt or wl_prompt
-    args.steps = args.steps or wl_steps
-    spec = rlh.SPECS[args.config]
+    config, n_prompt, n_decode, sampled = WORKLOADS[args.workload]
+    spec = rlh.SPECS[config]
     lib = rlh.load()
     nthreads = min(16, os.cpu_count() or 1)
     t0 = time.time()
     tensors = rlh.synth_model(spec, args.seed, lib, nthreads)
-    log(f"synthesised {args.config} in {time.time() - t0:.1f}s")
+    log(f"synthesised {config} in {time.time() - t0:.1f}s")
     t0 = time.time()
     model = rlh.Model(spec, tensors)
     log(f"uploaded {lib.rlh_model_weight_bytes(model.h) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
 
-    prompt = rlh.synth_tokens(args.seed + 1, args.prompt, spec.vocab)
-    max_ctx = args.prompt + max(args.steps, args.warmup) + 8
-    cache = model.new_cache(max_ctx)
-
+    prompt = rlh.synth_tokens(args.seed + 1, n_prompt, spec.vocab)
+    cache = model.new_cache(n_prompt + n_decode + 1)
     params = rlh.sampling_params()  # the CLI defaults (main.rs:44-52)
-    never = spec.vocab + 7            # EOS id no token can take: fixed token counts
-    # warm-up: prefill + a few decode steps (pages in code, graphs, caches)
-    logits = cache.forward_into(prompt, 0)
-    first = cache.greedy_next()
-    if args.warmup:
-        cache.generate_greedy(first, args.warmup)
-    if sampled and args.warmup:
-        cache.reset()
-        cache.generate(prompt, args.warmup, params, never)
-    cache.reset()
+    never = spec.vocab + 7            # end-of-sequence id no token can take: fixed token counts
 
-    # timed prefill
-    t0 = time.perf_counter()
-    logits = cache.forward_into(prompt, 0)
-    prefill_s = time.perf_counter() - t0
-    first = cache.greedy_next()
-
-    if sampled:
-        # Model::generate (prefill, then sample / forward_one per token, the
-        # sampler on the host): decode time = its time minus the prefill's
-        cache.reset()
-        t0 = time.perf_counter()
-        toks = cache.generate(prompt, args.steps, params, never)
-        decode_s = time.perf_counter() - t0 - prefill_s
-        if len(toks) != args.steps:
-            raise RuntimeError(f"generate returned {len(toks)} tokens, expected {args.steps}")
-    else:
-        # timed decode: exactly K steps (generate_greedy returns after the
-        # device finished and the tokens were copied back)
-        t0 = time.perf_counter()
-        toks = cache.generate_greedy(first, args.steps)
-        decode_s = time.perf_counter() - t0
-    tok_s = args.steps / decode_s
-    prefill_tok_s = args.prompt / prefill_s
+    for i in range(args.warmup):
+        run_pass(cache, prompt, n_decode, sampled, params, never)
+        log(f"warm-up pass {i + 1}/{args.warmup}")
+    prefill_s = decode_s = 0.0
+    passes = []
+    tokens = None
+    t_all = time.perf_counter()
+    for i in range(args.steps):
+        p_s, d_s, toks = run_pass(cache, prompt, n_decode, sampled, params, never)
+        prefill_s += p_s
+        decode_s += d_s
+        passes.append(round(n_decode / d_s, 2))
+        if tokens is None:
+            tokens = toks
+        elif not np.array_equal(tokens, toks):
+            raise RuntimeError(f"pass {i} produced a different token sequence")
+        log(f"pass {i + 1}/{args.steps}: prefill {n_prompt / p_s:.1f} tok/s, decode {n_decode / d_s:.2f} tok/s")
+    wall_s = time.perf_counter() - t_all
+    tok_s = args.steps * n_decode / decode_s
+    prefill_tok_s = args.steps * n_prompt / prefill_s
 
     # per-token HBM traffic of the decode loop: packed weights + f32 KV read
-    # at the average context + K/V write
+    # at the window's average context + the K/V row written
     wbytes = spec.weight_bytes_per_token()
-    t_avg = args.prompt + (args.steps + 1) / 2.0
+    t_avg = n_prompt + (n_decode + 1) / 2.0
     kvw = 2 * spec.n_layer * spec.n_head_kv * spec.head_dim * 4
     step_bytes = wbytes + kv_read_bytes(spec, t_avg) + kvw
     hbm_frac_decode = step_bytes * tok_s / (HBM_PEAK_GBS * 1e9)
 
     # dominant decode kernel: the fused rmsnorm + ffn_gate/ffn_up + silu*up
-    # launch (k_mv<TY, 2>), timed per launch with HIP events on the cache's
-    # stream, rotating over the layers' weights
+    # launch (k_mv<TY, 2>), each launch timed with HIP events bound to it
+    # inside real decode steps (36 launches per step at 8B)
     E, F = spec.n_embd, spec.n_ff
     ff_ty = spec.types[rlh.T_FFN_GATE]
     pair_bytes = (2 * F * rlh.row_bytes(ff_ty, E)  # gate + up weights
                   + 2 * E * 4                       # residual row and ffn_norm weights
                   + F * 4 + F + (F // 32) * 16)     # h (f32) and its Q8 blocks
-    mv_us = cache.profile_matvec(rlh.T_FFN_GATE, 4 * spec.n_layer)
+    cache.reset()
+    cache.forward_into(prompt, 0, copy=False)
+    probe_steps = max(1, min(args.probe_steps, n_decode))
+    mv_us, mv_launches = cache.profile_decode_kernel(rlh.T_FFN_GATE, cache.greedy_next(), probe_steps)
     mv_gbs = pair_bytes / (mv_us * 1e-6) / 1e9
-    traffic = measured_traffic(args.config)
+    traffic = measured_traffic(config)
 
+    model_name = MODEL_NAMES[config]
+    decode_desc = ("sampled (temperature 0.7, top-k 40, top-p 0.95, repetition penalty 1.1 over the last 64, "
+                   "seed 0x123456789abcdef0)" if sampled else "greedy")
     out = {
-        "metric": ("decode tok/s (Qwen3-8B Q4_K_M, 1 GPU); prefill tok/s and % HBM roofline reported alongside"
-                   if args.workload == 4 else
-                   f"decode tok/s ({args.config}, 1 GPU); prefill tok/s and % HBM roofline reported alongside"),
+        "metric": f"{METRIC} ({model_name}, 1 GPU)",
         "value": round(tok_s, 2),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(1000.0 / tok_s, 4),
+        "ms_per_step": round(1000.0 * wall_s / args.steps, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (seeded N(0,0.02) weights quantized "
                 + "/".join(sorted({rlh.TYPE_NAMES.get(t, str(t)) for t in spec.types.values()}))
-                + ", uniform random prompt ids)",
-        "config": {"workload": f"{args.config}: {args.prompt}-token prefill then {args.steps} "
-                               f"{'sampled (temperature 0.7, top-k 40, top-p 0.95, repetition penalty 1.1)' if sampled else 'greedy'}"
-                               f" decode tokens (KV up to {args.prompt + args.steps})",
-                   "prompt_tokens": args.prompt, "decode_tokens": args.steps, "kv": "f32",
+                + ", norms 1+N(0,0.02), uniform random prompt ids)",
+        "config": {"workload": f"{config}: {n_prompt}-token prefill then {n_decode} {decode_desc} decode tokens "
+                               f"(KV {n_prompt} -> {n_prompt + n_decode}); one step = one pass of the workload",
+                   "prompt_tokens": n_prompt, "decode_tokens": n_decode, "kv": "f32",
                    "eos": "ignored", "parallelism": "single GPU"},
+        "decode_tok_s_per_pass": passes,
         "prefill_tok_s": round(prefill_tok_s, 1),
-        "prefill_ms": round(prefill_s * 1000, 3),
+        "prefill_ms": round(1000.0 * prefill_s / args.steps, 3),
+        "decode_ms_per_token": round(1000.0 / tok_s, 4),
         "decode_hbm_bytes_per_token": int(step_bytes),
         "decode_hbm_frac": round(hbm_frac_decode, 4),
-        "prefill_int8_frac": round(spec.int8_ops_per_token() * args.prompt / prefill_s / (INT8_PEAK_TOPS * 1e12), 5),
+        "prefill_int8_frac": round(spec.int8_ops_per_token() * prefill_tok_s / (INT8_PEAK_TOPS * 1e12), 5),
         "roofline": {"bound": "hbm",
-                     "kernel": f"k_mv<{rlh.TYPE_NAMES.get(ff_ty, ff_ty)}, pair>: rmsnorm + ffn_gate/ffn_up "
+                     "kernel": f"k_mv<{rlh.TYPE_NAMES.get(ff_ty, ff_ty)}, 2>: rmsnorm + ffn_gate/ffn_up "
                                f"2x{F}x{E} + silu*up",
                      "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "avg_launch_us": round(mv_us, 3), "bytes_per_launch": int(pair_bytes)},
+                     "avg_launch_us": round(mv_us, 3), "launches_timed": int(mv_launches),
+                     "bytes_per_launch": int(pair_bytes)},
         "decode": "sampled" if sampled else "greedy",
-        "tokens_head": [int(t) for t in toks[:8]],
+        "tokens_head": [int(t) for t in tokens[:8]],
     }
 
-    if args.cpu_decode > 0:
-        cpu_prompt = prompt[: args.cpu_prompt]
-        res, ctoks = cpu_baseline(spec, tensors, cpu_prompt, args.cpu_decode, nthreads)
-        out["cpu_baseline"] = {"value": round(res.generated / res.decode_s, 3), "unit": "tok/s", "cores": nthreads,
-                               "kind": "port",
-                               "sample": f"oracle (C++ AVX2 restatement of the reference) on {args.config}: "
-                                         f"{len(cpu_prompt)}-token prefill then {res.generated} greedy decode "
-                                         f"tokens; prefill {res.prompt_len / res.prefill_s:.2f} tok/s"}
-    else:
+    if args.no_cpu:
         out["cpu_baseline"] = None
+    else:
+        cp, cd = CPU_SAMPLE[args.workload]
+        r = cpu_baseline(spec, tensors, prompt, cp, cd)
+        out["cpu_baseline"] = {
+            "value": round(r["decode_tok_s"], 3), "unit": "tok/s", "cores": r["threads"], "kind": "port",
+            "prefill_tok_s_default": round(r["prefill_tok_s_default"], 2),
+            "prefill_tok_s_batch_int": round(r["prefill_tok_s_batch_int"], 2),
+            "sample": f"oracle (C++ restatement of the reference's AVX2 path) on {config}, {r['threads']} threads: "
+                      f"{cp}-token prefill in the default mode and with RUST_LLAMA_BATCH_INT=1, then "
+                      f"{r['generated']} greedy decode tokens (cmd_bench protocol; {r['wall_s']:.1f}s of host work)"}
+        log(f"cpu oracle: decode {r['decode_tok_s']:.2f} tok/s, prefill {r['prefill_tok_s_default']:.2f} "
+            f"(default) / {r['prefill_tok_s_batch_int']:.2f} (BATCH_INT) tok/s, {r['threads']} threads")
 
     cache.close()
     model.close()

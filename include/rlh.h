@@ -136,9 +136,10 @@ int rlh_forward_batch(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64
 int rlh_forward_into(rlh_model* m, rlh_cache* c, const uint32_t* tokens, uint64_t n, uint64_t start_pos,
                      float* logits);
 /* Greedy argmax of the logits computed by the last forward call on this
- * cache, on device: strict '>' so the lowest index wins ties, as the
- * sampler's greedy fast path (src/sampler.rs:62-70) and main.rs argmax
- * (main.rs:453-463) choose. */
+ * cache, on device, with main.rs argmax semantics (main.rs:453-463): the
+ * lowest index among equal maxima, NaN never wins, 0 when no value exceeds
+ * -inf. (The sampler's greedy fast path, sampler.rs:62-70, differs only in
+ * keeping index 0 when logits[0] is NaN; rlh_sample_next applies that.) */
 int rlh_greedy_next(rlh_model* m, rlh_cache* c, uint32_t* token);
 /* The greedy token loop of cmd_bench (src/main.rs:500-516) run on device:
  * starting from `first` at position cache len, n_steps decode steps, each
@@ -224,6 +225,17 @@ int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t co
  * launch, other kinds = that matrix alone. No reference counterpart
  * (measurement hook for the bench). */
 int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* avg_us);
+/* Average duration of one launch of the decode matvec of weight kind `kind`
+ * (RLH_T_ATTN_Q = the rmsnorm + q/k/v launch, RLH_T_ATTN_OUTPUT,
+ * RLH_T_FFN_GATE = the rmsnorm + gate/up + silu*up launch, RLH_T_FFN_DOWN,
+ * RLH_T_OUTPUT = the logits) inside real decode steps: `steps` greedy decode
+ * steps starting from token `first` at the cache's length run eagerly, and
+ * each launch of that kind takes its own start and end times on the cache's
+ * stream (HIP events bound to the launch, hipExtLaunchKernel), the same span
+ * a kernel trace reports. *launches receives the number of timed launches;
+ * the cache advances by `steps`. No reference counterpart (measurement). */
+int rlh_profile_decode_kernel(rlh_model* m, rlh_cache* c, int kind, uint32_t first, int steps, double* avg_us,
+                              uint64_t* launches);
 /* Average duration of one captured decode step (graph launch) over `iters`
  * steps at the cache's current length, in microseconds; the cache position
  * advances by `iters`. */

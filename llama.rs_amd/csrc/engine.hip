@@ -302,6 +302,11 @@ struct rlh_cache {
   uint32_t* tokb = nullptr;   // token ids of the whole call
   uint32_t* posb = nullptr;   // first position of every chunk
   uint64_t tokb_cap = 0, posb_cap = 0;
+  // kernel probe (rlh_profile_decode_kernel): event pairs taking the start
+  // and end of each eager launch of one weight kind's decode matvec
+  int probe_kind = -1;
+  std::vector<hipEvent_t> probe_ev;
+  uint32_t probe_used = 0;
 };
 
 namespace {
@@ -318,6 +323,19 @@ float* layer_v(rlh_cache* c, uint32_t l) {
 }
 
 enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
+
+// The matvec launch of weight kind `kind` (the kind that names its launch:
+// RLH_T_ATTN_Q for q/k/v, RLH_T_FFN_GATE for gate/up, RLH_T_OUTPUT for the
+// logits) with the probe's next event pair when a probe of that kind runs.
+void mv_launch_probed(rlh_cache* c, int kind, const MvPlan& p) {
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (c->probe_kind == kind && 2 * (c->probe_used + 1) <= c->probe_ev.size()) {
+    e0 = c->probe_ev[2 * c->probe_used];
+    e1 = c->probe_ev[2 * c->probe_used + 1];
+    c->probe_used++;
+  }
+  mv_launch(c->st, p, e0, e1);
+}
 
 // Decode attention writes only f32 (its kernels split the head dimension in
 // 16-wide slices) when attn_output can quantize that row in its prologue.
@@ -360,7 +378,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       mv_plan_add(p, L.q.dm, c->q, nullptr);
       mv_plan_add(p, L.k.dm, c->k, nullptr);
       mv_plan_finish(p);
-      mv_launch(st, p);
+      mv_launch_probed(c, RLH_T_ATTN_Q, p);
     }
     {
       AttnArgs a{};
@@ -395,14 +413,14 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       plan_attn_output(p, c, qd);
       mv_plan_add(p, L.o.dm, nullptr, c->x);
       mv_plan_finish(p);
-      mv_launch(st, p);
+      mv_launch_probed(c, RLH_T_ATTN_OUTPUT, p);
     }
     {  // rmsnorm(x, ffn_norm); gate, up, silu(g)*u and its Q8 blocks (model.rs:719-724)
       MvPlan p;
       mv_plan_init_norm(p, E, c->x, L.ffn_norm.p, eps);
       mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
       mv_plan_finish(p);
-      mv_launch(st, p);
+      mv_launch_probed(c, RLH_T_FFN_GATE, p);
     }
     {  // ffn_down, x += (model.rs:725-728)
       MvPlan p;
@@ -410,7 +428,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       mv_plan_set_f32(p, c->g);
       mv_plan_add(p, L.down.dm, nullptr, c->x);
       mv_plan_finish(p);
-      mv_launch(st, p);
+      mv_launch_probed(c, RLH_T_FFN_DOWN, p);
     }
     if (dbg_slot >= 0 && c->dbg && (uint64_t)dbg_slot < c->dbg_tokens)
       (void)hipMemcpyAsync(c->dbg + ((size_t)l * c->dbg_tokens + dbg_slot) * E, c->x, E * 4, hipMemcpyDeviceToDevice,
@@ -427,7 +445,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
     mv_plan_add(p, ow.dm, c->logits, nullptr);
     if (kind == STEP_GREEDY) mv_plan_argmax(p, MvArgmax{c->pv, c->pi});
     mv_plan_finish(p);
-    mv_launch(st, p);
+    mv_launch_probed(c, RLH_T_OUTPUT, p);
     if (kind == STEP_GREEDY) launch_argmax_final(st, c->pv, c->pi, p.blocks, tok, pos, c->st_dev + 2, c->hist);
   }
 }
@@ -1008,8 +1026,17 @@ int rlh_sample_next(rlh_model* m, rlh_cache* c, const rlh_sampling_params* p, co
   if (rc) return rc;
   if (!p || !rng_state || !token || (n_recent && !recent)) return fail(RLH_EINVAL, "null argument");
   if (!c->logits_valid) return fail(RLH_ESTATE, "no logits computed on this cache yet");
-  // sampler.rs:62-70: the greedy fast path is the device argmax (same ties)
-  if (p->temperature <= 0.0f && p->repetition_penalty == 1.0f) return rlh_greedy_next(m, c, token);
+  // sampler.rs:62-70: the greedy fast path is the device argmax (first of
+  // equal maxima, NaN never wins) with the fast path's start at index 0: a
+  // NaN logits[0] is kept, since no value compares greater than it
+  if (p->temperature <= 0.0f && p->repetition_penalty == 1.0f) {
+    if ((rc = rlh_greedy_next(m, c, token))) return rc;
+    float l0 = 0.0f;
+    HIPCHK(hipMemcpyAsync(&l0, c->logits, 4, hipMemcpyDeviceToHost, c->st));
+    HIPCHK(hipStreamSynchronize(c->st));
+    if (l0 != l0) *token = 0;
+    return RLH_OK;
+  }
   std::vector<float> host(m->cfg.vocab_size);
   HIPCHK(hipMemcpyAsync(host.data(), c->logits, host.size() * 4, hipMemcpyDeviceToHost, c->st));
   HIPCHK(hipStreamSynchronize(c->st));
@@ -1322,6 +1349,61 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("profile events: ") + hipGetErrorString(e));
   const double total_ms = ms;
   *avg_us = total_ms * 1000.0 / iters;
+  return RLH_OK;
+}
+
+int rlh_profile_decode_kernel(rlh_model* m, rlh_cache* c, int kind, uint32_t first, int steps, double* avg_us,
+                              uint64_t* launches) {
+  int rc = check_forward_args(m, c);
+  if (rc) return rc;
+  if (!avg_us || steps <= 0 || steps > 4096) return fail(RLH_EINVAL, "bad argument");
+  if (kind != RLH_T_ATTN_Q && kind != RLH_T_ATTN_OUTPUT && kind != RLH_T_FFN_GATE && kind != RLH_T_FFN_DOWN &&
+      kind != RLH_T_OUTPUT)
+    return fail(RLH_EINVAL, "kind names no decode matvec launch");
+  if (first >= m->cfg.vocab_size) return fail(RLH_EINVAL, "token id out of range");
+  if (c->len + (uint64_t)steps > c->max_ctx) return fail(RLH_ECTX, "not enough room in the cache");
+  if (c->debug) return fail(RLH_ESTATE, "profiling needs debug capture off");
+  const uint32_t per_step = kind == RLH_T_OUTPUT ? 1u : m->cfg.n_layer;
+  const size_t n = (size_t)per_step * steps;
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->probe_ev.assign(2 * n, nullptr);
+  auto release = [c] {
+    for (hipEvent_t e : c->probe_ev)
+      if (e) (void)hipEventDestroy(e);
+    c->probe_ev.clear();
+    c->probe_kind = -1;
+    c->probe_used = 0;
+  };
+  for (auto& e : c->probe_ev)
+    if (hipEventCreate(&e) != hipSuccess) {
+      release();
+      return fail(RLH_EDEVICE, "hipEventCreate");
+    }
+  c->host_st[0] = first;
+  c->host_st[1] = (uint32_t)c->len;
+  c->host_st[2] = 0;
+  if (hipMemcpyAsync(c->st_dev, c->host_st, 12, hipMemcpyHostToDevice, c->st) != hipSuccess) {
+    release();
+    return fail(RLH_EDEVICE, "hipMemcpyAsync");
+  }
+  c->probe_kind = kind;
+  c->probe_used = 0;
+  for (int i = 0; i < steps; i++) enqueue_step(c, STEP_GREEDY, -1);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipStreamSynchronize(c->st);
+  double total_ms = 0.0;
+  for (uint32_t i = 0; e == hipSuccess && i < c->probe_used; i++) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, c->probe_ev[2 * i], c->probe_ev[2 * i + 1]);
+    total_ms += ms;
+  }
+  const uint32_t used = c->probe_used;
+  release();
+  if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("kernel probe: ") + hipGetErrorString(e));
+  c->len += (uint64_t)steps;
+  c->logits_valid = true;
+  *avg_us = used ? total_ms * 1000.0 / used : 0.0;
+  if (launches) *launches = used;
   return RLH_OK;
 }
 

@@ -300,7 +300,9 @@ __global__ void __launch_bounds__(1024) k_argmax_final(const float* pv, const ui
     float b = sv[0];
     uint32_t j = si[0];
     for (int k = 1; k < 16; k++) argmax_merge(b, j, sv[k], si[k]);
-    const uint32_t best = j == 0xffffffffu ? 0u : j;  // all NaN -> 0, as main.rs argmax
+    // main.rs argmax keeps index 0 unless a value exceeds -inf (all values
+    // NaN or -inf -> 0); the merge above takes the first of equal maxima
+    const uint32_t best = (j == 0xffffffffu || !(b > -__int_as_float(0x7f800000))) ? 0u : j;
     tok_out[0] = best;
     if (step) {
       const uint32_t s = step[0] + 1;

@@ -96,7 +96,9 @@ void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
 void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h);
 void mv_plan_argmax(MvPlan& p, const MvArgmax& am);
 bool mv_plan_finish(MvPlan& p);
-void mv_launch(hipStream_t st, const MvPlan& p);
+// ev_start / ev_stop (optional, not under graph capture): events that take
+// the kernel's own start and end times (hipExtLaunchKernel), for probes.
+void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
 // Blocks of a single-matrix plan over `rows` rows of `cols` columns (the
 // argmax partial buffers of the logits launch hold one entry per block).
 uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols);

@@ -25,6 +25,7 @@
 //    blocks. Single mode can add into the residual (model.rs:714-716,
 //    726-728) or leave each block's greedy-argmax candidate of the logits.
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include <algorithm>
@@ -594,8 +595,10 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   if (wave != 0 || !L.has_argmax) return;
   // the block's greedy candidate (max, lowest index); a second launch
   // reduces the candidates of all blocks (main.rs:453-463 semantics)
-  float bv = mine ? acc : -__int_as_float(0x7f800000);
-  uint32_t bi = mine ? row : 0xffffffffu;
+  // (a NaN row never becomes a candidate: it would stick in the merge)
+  const bool cand = mine && acc == acc;
+  float bv = cand ? acc : -__int_as_float(0x7f800000);
+  uint32_t bi = cand ? row : 0xffffffffu;
   wave_argmax(bv, bi);
   if (lane == 0) {
     ((RLH_GLOBAL float*)L.am.pv)[blockIdx.x] = bv;
@@ -783,13 +786,16 @@ uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
   return p.blocks;
 }
 
-void mv_launch(hipStream_t st, const MvPlan& p) {
+void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start, hipEvent_t ev_stop) {
   const bool pair = p.L.nseg == 1 && p.L.seg[0].pair;
   uint32_t ty = p.L.seg[0].w.ty;
   for (uint32_t s = 1; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty != ty) ty = 0;
   const MvKernel k = pair ? mv_kernel<2>(ty) : mv_kernel<1>(ty);
-  hipLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, p.L);
+  if (ev_start || ev_stop)
+    hipExtLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, ev_start, ev_stop, 0, p.L);
+  else
+    hipLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, p.L);
 }
 
 bool mv_set_max_lds(size_t bytes) {

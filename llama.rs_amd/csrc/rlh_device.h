@@ -26,56 +26,15 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16) {
 }
 
 // ---------------------------------------------------------------------------
-// expf bit-identical to the host glibc expf the reference calls through
-// f32::exp (softmax_inplace ops.rs:410, silu ops.rs:394).
-// Method: the table-driven exp of ARM's optimized-routines as glibc builds it
-// for FMA-capable x86-64: x*32/ln2 = k + r, exp(x) = 2^(k/32) * p(r) with a
-// cubic p evaluated in double with FMAs. T[i] = bits(2^(i/32)) - (i << 47).
-// Exhaustively checked against glibc 2.35 expf on every float in
-// [-103.9, 88.7] (tests/test_oracle_expf.py re-checks a dense sample).
+// expf with the host glibc expf's results (the reference's f32::exp in
+// softmax_inplace ops.rs:410 and silu ops.rs:394): expf_glibc_t of
+// expf_glibc.h, the same source the host tests check against glibc expf
+// over every float (tests/test_host_expf.py).
 // ---------------------------------------------------------------------------
-__device__ __constant__ static const uint64_t kExp2Tab[32] = {
-    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
-    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
-    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
-    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
-    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
-    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
-    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
-    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+#define RLH_EXPF_QUAL __device__ __forceinline__
+#include "expf_glibc.h"
 
-// tab: the 32 entries of kExp2Tab, read through `tab[i]` (the constant
-// table itself, or a copy in LDS where many lanes look entries up at once:
-// a divergent lookup in the constant table is a global memory round trip).
-template <class Tab>
-__device__ __forceinline__ float expf_glibc_t(float x, Tab tab) {
-  const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
-  const double kShift = 0x1.8p+52;
-  const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-  const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-  const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
-  uint32_t ux = __float_as_uint(x);
-  uint32_t abstop = (ux >> 20) & 0x7ff;
-  if (abstop >= 0x42b) {                       // |x| >= 88 or NaN
-    if (ux == 0xff800000u) return 0.0f;        // -inf
-    if (abstop >= 0x7f8) return x + x;         // +inf or NaN
-    if (x > 0x1.62e42ep6f) return __int_as_float(0x7f800000);  // overflow
-    if (x < -0x1.9fe368p6f) return 0.0f;       // underflow
-  }
-  double xd = (double)x;
-  double kd = __builtin_fma(kInvLn2N, xd, kShift);
-  uint64_t ki = (uint64_t)__double_as_longlong(kd);
-  kd -= kShift;
-  double r = __builtin_fma(kInvLn2N, xd, -kd);
-  uint64_t t = tab[ki % 32] + (ki << 47);
-  double s = __longlong_as_double((long long)t);
-  double z = __builtin_fma(C0, r, C1);
-  double r2 = r * r;
-  double y = __builtin_fma(C2, r, 1.0);
-  y = __builtin_fma(z, r2, y);
-  y = y * s;
-  return (float)y;
-}
+__device__ __constant__ static const uint64_t kExp2Tab[32] = RLH_EXP2_TABLE_INIT;
 
 __device__ __forceinline__ float expf_glibc(float x) { return expf_glibc_t(x, kExp2Tab); }
 

@@ -25,6 +25,9 @@
 #include "../../include/rlh.h"
 #include "sampler.h"
 
+#define RLH_EXPF_QUAL inline
+#include "expf_glibc.h"
+
 namespace rlh {
 
 namespace {
@@ -50,30 +53,19 @@ uint32_t first_max(const float* v, size_t n) {
   return (uint32_t)best;
 }
 
-// expf of glibc on x86-64 with FMA (the variant f32::exp reaches there):
-// x * 32/ln2 = k + r, exp(x) = 2^(k/32) * p(r), a cubic p in double with
-// FMAs, T[i] = bits(2^(i/32)) - (i << 47) (the method of ARM's
-// optimized-routines). Four lanes per AVX2 step; lanes with |x| >= 88 or
-// NaN take the library call. The kernels' expf_glibc_t is the same
-// computation and was checked against the library on every float of
-// [-103.9, 88.7].
-const uint64_t kExp2T[32] = {
-    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
-    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
-    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
-    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
-    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
-    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
-    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
-    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+// expf of glibc on x86-64 with FMA (the variant f32::exp reaches there), the
+// method of expf_glibc.h four lanes per AVX2 step; lanes with |x| >= 88 or
+// NaN take the library call. tests/test_host_expf.py checks this path and
+// expf_glibc_t (the kernels' expf) against the library on every float.
+const uint64_t kExp2T[32] = RLH_EXP2_TABLE_INIT;
 
 // x[i] = expf(x[i] - mx) for i < n.
 __attribute__((target("avx2,fma"))) void exp_shift_avx2(float* x, size_t n, float mx) {
-  const __m256d inv_ln2n = _mm256_set1_pd(0x1.71547652b82fep+0 * 32.0);
-  const __m256d shift = _mm256_set1_pd(0x1.8p+52);
-  const __m256d c0 = _mm256_set1_pd(0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0);
-  const __m256d c1 = _mm256_set1_pd(0x1.ebfce50fac4f3p-3 / 32.0 / 32.0);
-  const __m256d c2 = _mm256_set1_pd(0x1.62e42ff0c52d6p-1 / 32.0);
+  const __m256d inv_ln2n = _mm256_set1_pd(RLH_EXPF_INV_LN2_N);
+  const __m256d shift = _mm256_set1_pd(RLH_EXPF_SHIFT);
+  const __m256d c0 = _mm256_set1_pd(RLH_EXPF_C0);
+  const __m256d c1 = _mm256_set1_pd(RLH_EXPF_C1);
+  const __m256d c2 = _mm256_set1_pd(RLH_EXPF_C2);
   const __m256d one = _mm256_set1_pd(1.0);
   const __m128 vmx = _mm_set1_ps(mx);
   const __m128i lim = _mm_set1_epi32(0x42b);

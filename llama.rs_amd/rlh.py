@@ -128,9 +128,9 @@ SPECS = {
     "tiny-q8_0": ModelSpec("tiny-q8_0", 2, 256, 512, 4, 2, 1000, True, _all(Q8_0), n_ctx=512),
     "tiny-q4_0": ModelSpec("tiny-q4_0", 2, 256, 512, 4, 4, 1000, True, _all(Q4_0), n_ctx=512),
     "small-q4km": ModelSpec("small-q4km", 4, 1024, 3072, 16, 8, 4096, False, _q4km(False, Q4_K, Q6_K), n_ctx=1024),
-    # 8 query heads per KV head (the 32B grouping) and a long context window
     # Q5_K matrices (no integer path in the reference: f32 products)
     "tiny-q5km": ModelSpec("tiny-q5km", 2, 256, 512, 4, 2, 1000, True, _q5km(), n_ctx=512),
+    # 8 query heads per KV head (the 32B grouping) and a long context window
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
     # 4 query heads per KV head (the 4B / 8B grouping) and a long context window
     "tiny-g4-q4km": ModelSpec("tiny-g4-q4km", 2, 256, 512, 8, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
@@ -142,6 +142,21 @@ SPECS = {
     "tiny-wide-q4km": ModelSpec("tiny-wide-q4km", 2, 256, 512, 104, 13, 1000, True, _q4km(True, Q4_K, None),
                                 n_ctx=4096),
 }
+
+
+# The five benchmark workloads: number -> (model, prompt tokens, decode
+# tokens, sampled decode). 4 is the headline. Sampled decode uses the CLI's
+# sampling defaults (src/main.rs:44-52): temperature 0.7, top-k 40,
+# top-p 0.95, repetition penalty 1.1 over the last 64 tokens, its fixed seed.
+WORKLOADS = {
+    1: ("qwen3-0.6b-q4km", 48, 32, False),
+    2: ("qwen3-0.6b-q8_0", 48, 128, False),
+    3: ("qwen3-4b-q4km", 256, 256, False),
+    4: ("qwen3-8b-q4km", 512, 512, False),
+    5: ("qwen3-32b-q4km", 4096, 256, True),
+}
+# Seed of the synthetic weights of the workloads; the prompt ids use seed + 1.
+WORKLOAD_SEED = 20260
 
 
 def tensor_id(kind, layer):
@@ -252,6 +267,8 @@ def load():
         "rlh_block_dots": (I32, [U32, P, U64, U64, P, P]),
         "rlh_profile_matvec": (I32, [P, P, I32, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
+        "rlh_profile_decode_kernel": (I32, [P, P, I32, U32, I32, ctypes.POINTER(ctypes.c_double),
+                                            ctypes.POINTER(U64)]),
         "rlh_quantize_row": (I32, [U32, P, U64, P]),
         "rlh_synth_normal": (None, [U64, U64, U64, U64, F, F, P]),
         "rlh_synth_tensor": (I32, [U64, U64, U32, U64, U64, F, F, P, I32]),
@@ -346,17 +363,28 @@ class Cache:
     def reset(self):
         check(self.lib.rlh_cache_reset(self.h))
 
-    def forward_into(self, tokens, start_pos, logits=None):
+    def forward_into(self, tokens, start_pos, logits=None, copy=True):
+        """Model::forward_into; returns the last token's logits (None when
+        copy is False: the device keeps them for greedy_next / sample_next)."""
         toks = np.ascontiguousarray(tokens, dtype=np.uint32)
-        if logits is None:
+        if copy and logits is None:
             logits = np.empty(self.model.spec.vocab, dtype=np.float32)
         check(self.lib.rlh_forward_into(self.model.h, self.h, toks.ctypes.data, len(toks), start_pos,
-                                        logits.ctypes.data))
-        return logits
+                                        logits.ctypes.data if copy else None))
+        return logits if copy else None
 
     def greedy_next(self):
         t = ctypes.c_uint32()
         check(self.lib.rlh_greedy_next(self.model.h, self.h, ctypes.byref(t)))
+        return t.value
+
+    def sample_next(self, params, recent, state):
+        """Sampler::sample on the logits of the last forward call
+        (rlh_sample_next); `state` is a ctypes.c_uint64 RNG state."""
+        r = np.ascontiguousarray(recent, dtype=np.uint32)
+        t = ctypes.c_uint32()
+        check(self.lib.rlh_sample_next(self.model.h, self.h, ctypes.byref(params), r.ctypes.data, len(r),
+                                       ctypes.byref(state), ctypes.byref(t)))
         return t.value
 
     def generate_greedy(self, first, n_steps):
@@ -385,6 +413,15 @@ class Cache:
         v = ctypes.c_double()
         check(self.lib.rlh_profile_matvec(self.model.h, self.h, kind, iters, ctypes.byref(v)))
         return v.value
+
+    def profile_decode_kernel(self, kind, first, steps):
+        """(average microseconds per launch, launches timed) of one decode
+        matvec kind inside `steps` greedy decode steps from token `first`."""
+        v = ctypes.c_double()
+        n = ctypes.c_uint64()
+        check(self.lib.rlh_profile_decode_kernel(self.model.h, self.h, kind, first, steps, ctypes.byref(v),
+                                                 ctypes.byref(n)))
+        return v.value, n.value
 
     def profile_decode(self, iters):
         v = ctypes.c_double()

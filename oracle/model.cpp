@@ -360,11 +360,13 @@ uint32_t orc_sampler_sample(orc_sampler* s, const float* logits, size_t n, const
   size_t k = (p->top_k == 0 || p->top_k > n) ? n : p->top_k;
   std::vector<size_t> idx(n);
   for (size_t i = 0; i < n; i++) idx[i] = i;
-  auto desc = [&](size_t a, size_t b) { return probs[b] < probs[a]; };
+  // select_nth_unstable_by + truncate, then sort_by (sampler.rs:122-132).
+  // For distinct probabilities that is the k largest in descending order.
+  // Exactly equal probabilities are ordered by token id here; the reference
+  // leaves their order to the internals of Rust's selection, which nothing
+  // in its tests fixes (tie order is parity-unpinned against the reference).
+  auto desc = [&](size_t a, size_t b) { return probs[b] < probs[a] || (probs[b] == probs[a] && a < b); };
   if (k < n) {
-    // select_nth_unstable_by + truncate: keeps a set of k largest; the set is
-    // what matters because it is sorted next (ties between equal
-    // probabilities may be broken differently than Rust's pdqselect).
     std::nth_element(idx.begin(), idx.begin() + (k - 1), idx.end(), desc);
     idx.resize(k);
   }

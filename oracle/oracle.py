@@ -87,8 +87,20 @@ def load():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    lib.orc_set_threads(default_threads())
     _lib = lib
     return lib
+
+
+def default_threads():
+    """Worker threads of the oracle's pool: the CPUs this process may run
+    on (what rayon's default pool takes, std::thread::available_parallelism),
+    capped at 16, the host share that goes with one GPU."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def quantize_q8(x, mode=0):

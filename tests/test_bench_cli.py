@@ -22,6 +22,7 @@ def test_workload_presets():
     bench = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(bench)
     w = bench.WORKLOADS
+    assert sorted(bench.CPU_SAMPLE) == sorted(w)
     assert sorted(w) == [1, 2, 3, 4, 5]
     assert w[4] == ("qwen3-8b-q4km", 512, 512, False)  # the headline configuration
     assert w[5] == ("qwen3-32b-q4km", 4096, 256, True)  # sampled decode

@@ -6,6 +6,8 @@ per-layer hidden states within 1e-3 relative L2, logits within 2e-3,
 identical greedy tokens. The device path is built to match bit for bit, and
 these tests assert that stronger property (the L2 numbers are printed).
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -79,14 +81,19 @@ def test_prefill_and_decode_bit_exact(name):
     oc.close()
 
 
-@pytest.mark.parametrize("max_ctx", [64, 6000])
-def test_decode_attention_paths(max_ctx):
-    """Decode attention with 8 query heads per KV head: a short cache takes
-    the fused softmax + V kernel, a 6000-position cache (score rows beyond
-    its LDS) the separate softmax and V kernels. Logits bit-exact."""
-    print(f"decode attention max_ctx {max_ctx}", flush=True)
+@pytest.mark.parametrize("max_ctx,n_prompt", [(64, 40), (6000, 40), (1600, 700), (4400, 4100)])
+def test_decode_attention_paths(max_ctx, n_prompt):
+    """Decode attention with 8 query heads per KV head (the 32B grouping):
+    the softmax kernel and the PV kernel that streams p and V through an
+    8-slot LDS ring. 40 positions fit one 64-position chunk; 700 and 4100
+    positions wrap the ring many times, hand chunks two ahead from the
+    producers to the ordered adds and end on a clamped ragged tail (4100 is
+    the 32B workload's context). The 700- and 4100-token prompts also run
+    the prefill in several 512-token chunks with 8 heads per KV head.
+    Logits bit-exact in every step."""
+    print(f"decode attention g8 max_ctx {max_ctx} prompt {n_prompt}", flush=True)
     spec, tensors, m, om = _get("tiny-g8-q4km")
-    prompt = rlh.synth_tokens(77, 40, spec.vocab)
+    prompt = rlh.synth_tokens(77, n_prompt, spec.vocab)
     c = m.new_cache(max_ctx)
     oc = om.new_cache(max_ctx)
     lg = c.forward_into(prompt, 0)
@@ -253,3 +260,53 @@ def test_long_prefill_chunks_and_continuation():
     assert c.len == 630
     c.close()
     oc.close()
+
+
+def test_nan_logits_argmax_semantics():
+    """NaN logits: every 8th row of the untied output matrix has a NaN Q6_K
+    scale, so every logits block starts with a NaN row and logits[0] is NaN.
+    The device greedy argmax follows main.rs:453-463 (NaN never wins) in the
+    standalone argmax and in the fused greedy loop, and rlh_sample_next's
+    greedy fast path follows sampler.rs:62-70 (index 0 kept when logits[0]
+    is NaN), both as the oracle."""
+    spec = rlh.SPECS["tiny-q4km-untied"]
+    tensors = rlh.synth_model(spec, 4321)
+    for kind, layer, ty, cols, rows, buf in tensors:
+        if kind == rlh.T_OUTPUT:
+            assert ty == rlh.Q6_K
+            rb = rlh.row_bytes(ty, cols)
+            for r in range(0, rows, 8):
+                buf[r * rb + 208] = 0x00  # f16 NaN 0x7e00 in d of the first super-block
+                buf[r * rb + 209] = 0x7E
+    m = rlh.Model(spec, tensors)
+    om = oracle.OracleModel(spec, tensors)
+    lib = oracle.load()
+    prompt = rlh.synth_tokens(8, 9, spec.vocab)
+    c = m.new_cache(64)
+    oc = om.new_cache(64)
+    try:
+        lg = c.forward_into(prompt, 0)
+        rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+        nan = np.isnan(rg)
+        assert nan[0] and nan.sum() == spec.vocab // 8
+        assert np.array_equal(np.isnan(lg), nan)
+        assert np.array_equal(bits(lg[~nan]), bits(rg[~nan]))
+        tok = c.greedy_next()
+        assert tok == lib.orc_argmax(rg.ctypes.data, len(rg)) and tok % 8 != 0
+        greedy = rlh.sampling_params(temperature=0.0, repetition_penalty=1.0)
+        ogreedy = oracle.SamplingParams(0.0, 40, 0.95, 1.0, 64, 1)
+        s = lib.orc_sampler_create(1)
+        assert c.sample_next(greedy, prompt, ctypes.c_uint64(1)) == 0
+        assert lib.orc_sampler_sample(s, rg.ctypes.data, len(rg), ogreedy, prompt.ctypes.data, len(prompt)) == 0
+        lib.orc_sampler_destroy(s)
+        toks = c.generate_greedy(tok, 6)
+        ref = [tok]
+        for i in range(6):
+            r = oc.forward_into(np.array([ref[-1]], np.uint32), len(prompt) + i, oracle.MODE_DEFAULT)
+            ref.append(lib.orc_argmax(r.ctypes.data, len(r)))
+        assert list(map(int, toks)) == ref
+    finally:
+        c.close()
+        oc.close()
+        m.close()
+        om.close()

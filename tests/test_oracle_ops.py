@@ -162,20 +162,66 @@ def test_batch_int_equals_sequential_int_matmul(ty):
         assert np.array_equal(bits(b[k * rows:(k + 1) * rows]), bits(y))
 
 
-@pytest.mark.parametrize("ty", [12, 14, 8])
-def test_no_int_matmul_against_f64(ty):
-    """ops.rs:131-140 fused f32 path (RUST_LLAMA_NO_INT): close to the f64
-    dot of the decoded weights with x."""
-    rng = np.random.default_rng(3 + ty)
+@pytest.mark.parametrize("ty,mode", [(12, 1), (14, 1), (8, 1), (13, 1), (13, 0)])
+def test_no_int_matmul_against_f64(ty, mode):
+    """ops.rs:131-140 fused f32 path (RUST_LLAMA_NO_INT, and the default
+    mode for Q5_K, which has no integer kernel: ops.rs:93-128 skips it):
+    close to the f64 dot of the weights decoded by the independent numpy
+    decoder with x. Q5_K's fused kernel is the generic fallback
+    (quant.rs:528-539)."""
+    rng = np.random.default_rng(3 + ty + 17 * mode)
     rows, cols = 8, 1024
-    bs = 256 if ty in (12, 14) else 32
+    bs = 256 if ty in (12, 13, 14) else 32
     w = random_blocks(ty, rows * cols // bs, rng)
     x = rng.standard_normal(cols).astype(F32)
-    y = oracle.matmul(ty, w, rows, cols, x, oracle.MODE_NO_INT)
+    y = oracle.matmul(ty, w, rows, cols, x, mode)
     wd = gf.dequant(ty, w, rows * cols).astype(np.float64).reshape(rows, cols)
     ref = wd @ x
     scale = np.abs(wd * x).sum(1)
     assert (np.abs(y - ref) <= 1e-5 * scale).all()
+
+
+def test_q5k_fused_dot_is_blockwise_dequant_then_dot():
+    """The Q5_K generic fallback (quant.rs:528-539) dequantizes one 256-value
+    block at a time and adds ops::dot(block, x) to the row total in block
+    order. Rebuilt from the independent numpy decoder's values and ops::dot
+    (pinned by its own tests) it matches bit for bit, so a dropped 5th bit,
+    a wrong min term or another accumulation order would fail here."""
+    lib = oracle.load()
+    rng = np.random.default_rng(55)
+    cols = 1024
+    for trial in range(4):
+        w = random_blocks(13, cols // 256, rng)
+        x = rng.standard_normal(cols).astype(F32)
+        wd = gf.dequant(13, w, cols).astype(F32)
+        y = oracle.matmul(13, w, 1, cols, x, oracle.MODE_DEFAULT)
+        acc = F32(0.0)
+        for b in range(cols // 256):
+            wb = np.ascontiguousarray(wd[b * 256:(b + 1) * 256])
+            xb = np.ascontiguousarray(x[b * 256:(b + 1) * 256])
+            acc = F32(acc + F32(lib.orc_dot(P(wb), P(xb), 256)))
+        assert bits(y)[0] == bits(np.array([acc], F32))[0], trial
+
+
+@pytest.mark.parametrize("ty", [13, 12, 14])
+def test_default_matmul_batch_against_f64(ty):
+    """matmul_batch's default route (ops.rs:237-312: dequantize three rows,
+    dot_multi_rows over groups of four tokens; Q5_K always takes it, also
+    with RUST_LLAMA_BATCH_INT): close to the f64 products of the numpy
+    decoder's weights, with a ragged token tail (n % 4 = 3)."""
+    rng = np.random.default_rng(70 + ty)
+    rows, cols, n = 7, 512, 7
+    w = random_blocks(ty, rows * cols // 256, rng)
+    xs = rng.standard_normal(n * cols).astype(F32)
+    wd = gf.dequant(ty, w, rows * cols).astype(np.float64).reshape(rows, cols)
+    modes = (oracle.MODE_DEFAULT, oracle.MODE_BATCH_INT) if ty == 13 else (oracle.MODE_DEFAULT,)
+    for mode in modes:
+        ys = oracle.matmul_batch(ty, w, rows, cols, xs, n, mode).reshape(n, rows)
+        for k in range(n):
+            xk = xs[k * cols:(k + 1) * cols].astype(np.float64)
+            ref = wd @ xk
+            scale = np.abs(wd * xk).sum(1)
+            assert (np.abs(ys[k] - ref) <= 1e-5 * scale).all(), (mode, k)
 
 
 def test_softmax_silu_against_f64():
