@@ -214,6 +214,21 @@ int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t 
  * Q6_K -> cols/16 values (one per 16-value half-block, unsigned u = q+32). */
 int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
 
+/* ---- greedy argmax without allocation -----------------------------------------------
+ * The greedy argmax of rlh_greedy_next (main.rs:453-463 semantics: lowest
+ * index among equal maxima, NaN never wins, 0 when no value exceeds -inf)
+ * over n floats the caller already holds in device memory, written to the
+ * device word *token. No counterpart in the reference: for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops).
+ * Allocates nothing and does not synchronize: the two kernels are enqueued
+ * on `stream` (a hipStream_t, NULL for the null stream) and the token is
+ * valid once the stream reaches them. Their 256 partial (value, index)
+ * pairs live in a 2 KB static device array per GPU, held until the process
+ * ends; every call writes all of them before reading, and calls that
+ * overlap on one GPU race on them. n must be in [1, 2^32 - 1]; logits and
+ * token must be device-accessible memory (RLH_EINVAL otherwise). */
+int rlh_argmax_noalloc(const float* logits, uint64_t n, uint32_t* token, void* stream);
+
 /* ---- measurement ---------------------------------------------------------------------
  * Runs the decode launch of one weight kind `iters` times on the cache's
  * stream, rotating over the layers' copies (so weights stream from HBM as in

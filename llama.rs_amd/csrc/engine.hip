@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -80,6 +81,9 @@ bool layout_supported(uint32_t ty) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Largest logits count of rlh_argmax_noalloc (32-bit indices).
+constexpr uint64_t kNoAllocMaxN = 0xffffffffull;
 
 // Host-side f16 -> f32 for norm/bias conversion (exact).
 float h16(uint16_t h) {
@@ -1349,6 +1353,71 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("profile events: ") + hipGetErrorString(e));
   const double total_ms = ms;
   *avg_us = total_ms * 1000.0 / iters;
+  return RLH_OK;
+}
+
+// ---- greedy argmax without allocation ------------------------------------
+}  // extern "C"
+
+namespace {
+
+// Partial (value, index) pairs of one rlh_argmax_noalloc call: one per block
+// of the partial launch, values first, then indices. Every call writes all
+// of them before the final reduction reads them, so nothing is cleared
+// between calls.
+constexpr uint32_t kNoAllocParts = 256;
+static __device__ __align__(256) uint32_t scratch[2 * kNoAllocParts];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up once per device
+// with that device current; host code uses only this address).
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(RLH_EDEVICE, "device ordinal out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(RLH_EDEVICE, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return RLH_OK;
+}
+
+// True when p is memory the current device can read or write.
+bool device_accessible(const void* p) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return a.devicePointer != nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rlh_argmax_noalloc(const float* logits, uint64_t n, uint32_t* token, void* stream) {
+  if (!logits || !token) return fail(RLH_EINVAL, "null argument");
+  if (n == 0 || n > kNoAllocMaxN)
+    return fail(RLH_EINVAL, "n = " + std::to_string(n) + " is outside [1, " + std::to_string(kNoAllocMaxN) + "]");
+  int rc = ensure_device();
+  if (rc) return rc;
+  if (!device_accessible(logits) || !device_accessible(token))
+    return fail(RLH_EINVAL, "logits and token must be device-accessible memory");
+  void* sp = nullptr;
+  if ((rc = noalloc_scratch(&sp))) return rc;
+  float* pv = (float*)sp;
+  uint32_t* pi = (uint32_t*)sp + kNoAllocParts;
+  launch_argmax((hipStream_t)stream, logits, (uint32_t)n, pv, pi, kNoAllocParts, token, nullptr, nullptr, nullptr);
+  HIPCHK(hipGetLastError());
   return RLH_OK;
 }
 

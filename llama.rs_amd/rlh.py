@@ -265,6 +265,7 @@ def load():
         "rlh_matvec": (I32, [U32, P, U64, U64, P, P]),
         "rlh_matmul_batch": (I32, [U32, P, U64, U64, P, U64, P]),
         "rlh_block_dots": (I32, [U32, P, U64, U64, P, P]),
+        "rlh_argmax_noalloc": (I32, [P, U64, P, P]),
         "rlh_profile_matvec": (I32, [P, P, I32, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode_kernel": (I32, [P, P, I32, U32, I32, ctypes.POINTER(ctypes.c_double),
