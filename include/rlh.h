@@ -41,6 +41,9 @@ extern "C" {
 #define RLH_ESTATE (-4)   /* wrong call order (e.g. model not finalized)      */
 #define RLH_ECTX (-5)     /* position at or beyond the cache's max_ctx        */
 #define RLH_EUNSUP (-6)   /* valid ggml type with no kernel on this path      */
+#define RLH_EIO (-7)      /* file cannot be opened, mapped or written         */
+#define RLH_EFORMAT (-8)  /* malformed GGUF file or missing metadata          */
+#define RLH_ENOENT (-9)   /* no such metadata key or tensor                   */
 
 /* ---- ggml tensor types (src/quant.rs:26-41, ids as in GGUF) ----------- */
 #define RLH_TYPE_F32 0u
@@ -111,6 +114,73 @@ int rlh_model_finalize(rlh_model* m);
 void rlh_model_destroy(rlh_model* m);
 /* Device bytes held by the model's weights. */
 uint64_t rlh_model_weight_bytes(const rlh_model* m);
+
+/* ---- GGUF files -------------------------------------------------------------
+ * The reference's GGUF v2/v3 reader (GgufFile, src/gguf.rs:125-421): the
+ * file is memory-mapped, metadata parsed eagerly, tensor bytes borrowed from
+ * the mapping while the handle is open. Malformed files (bad magic, other
+ * versions, truncation, absurd counts or lengths, unknown value or tensor
+ * types) return RLH_EFORMAT without aborting (gguf.rs:433-464). */
+typedef struct rlh_gguf rlh_gguf;
+/* GgufFile::open (gguf.rs:246-307), including the sibling files of a split
+ * model (split.count > 1, named "-0000k-of-0000n.gguf" as gguf.rs:262-273). */
+int rlh_gguf_open(const char* path, rlh_gguf** out);
+void rlh_gguf_close(rlh_gguf* g);
+uint32_t rlh_gguf_version(const rlh_gguf* g);
+/* Files mapped (1 + the split siblings found). */
+uint64_t rlh_gguf_n_files(const rlh_gguf* g);
+/* Tensors in file order (tensor_order, gguf.rs:127) and their TensorInfo
+ * (gguf.rs:90-123): name, ggml type, dims (dims[0] = row length; up to
+ * max_dims written, *n_dims = all), offset in its file's data section, file. */
+uint64_t rlh_gguf_n_tensors(const rlh_gguf* g);
+int rlh_gguf_tensor_info(const rlh_gguf* g, uint64_t index, const char** name, uint32_t* ggml_type,
+                         uint32_t* n_dims, uint64_t* dims, uint32_t max_dims, uint64_t* offset,
+                         uint32_t* file_index);
+/* GgufFile::tensor_bytes (gguf.rs:385-413): the tensor's bytes inside the
+ * mapping (valid until rlh_gguf_close); RLH_ENOENT for an unknown name,
+ * RLH_EFORMAT when they extend past the end of the file. */
+int rlh_gguf_tensor_bytes(const rlh_gguf* g, const char* name, const void** data, uint64_t* nbytes);
+/* Metadata: keys in file order; value type (GGUF value type ids 0-12, the
+ * element type and count of an array); MetaValue::as_u32 / as_f32 /
+ * as_str (gguf.rs:32-88) and raw scalars (u: unsigned and bool, i: signed,
+ * f: float). A missing key returns RLH_ENOENT, a value of another type
+ * RLH_EINVAL. Strings stay valid until rlh_gguf_close. */
+uint64_t rlh_gguf_n_meta(const rlh_gguf* g);
+int rlh_gguf_meta_key(const rlh_gguf* g, uint64_t index, const char** key);
+int rlh_gguf_meta_type(const rlh_gguf* g, const char* key, uint32_t* type, uint32_t* elem_type, uint64_t* n_elems);
+int rlh_gguf_meta_u32(const rlh_gguf* g, const char* key, uint32_t* v);
+int rlh_gguf_meta_f32(const rlh_gguf* g, const char* key, float* v);
+int rlh_gguf_meta_scalar(const rlh_gguf* g, const char* key, uint64_t* u, int64_t* i, double* f);
+int rlh_gguf_meta_str(const rlh_gguf* g, const char* key, const char** s, uint64_t* len);
+int rlh_gguf_meta_arr_str(const rlh_gguf* g, const char* key, uint64_t index, const char** s, uint64_t* len);
+int rlh_gguf_meta_arr_scalar(const rlh_gguf* g, const char* key, uint64_t index, uint64_t* u, int64_t* i,
+                             double* f);
+/* Model::read_config (model.rs:241-293): general.architecture (default
+ * "llama", copied to `arch`) must be qwen3 or qwen2 (check_arch,
+ * model.rs:794-808, RLH_EUNSUP otherwise); each key is read as
+ * "{arch}.{key}", then as "{key}", with the reference's defaults. */
+int rlh_gguf_config(const rlh_gguf* g, rlh_config* cfg, char* arch, uint64_t arch_cap);
+/* Model::load (model.rs:150-239): the config, the vocabulary check of
+ * read_tokenizer (tokenizer.ggml.tokens, model.rs:295-300), then every
+ * tensor by its GGUF name through rlh_model_set_tensor, and finalize. The
+ * GGUF may be closed afterwards (the device holds its own copies). */
+int rlh_model_load_gguf(const rlh_gguf* g, rlh_model** out);
+
+/* GGUF writer (write_gguf, src/prune.rs:381-442): metadata written in key
+ * byte order, tensors in the order added with their data offsets aligned to
+ * `alignment`, the data section aligned. Tensor bytes are borrowed until
+ * rlh_gguf_writer_write. Value types are the GGUF ids; a string array takes
+ * `values` as an array of NUL-terminated strings, a numeric array packed
+ * little-endian values; arrays of arrays are refused. */
+typedef struct rlh_gguf_writer rlh_gguf_writer;
+int rlh_gguf_writer_create(uint32_t version, uint64_t alignment, rlh_gguf_writer** out);
+void rlh_gguf_writer_destroy(rlh_gguf_writer* w);
+int rlh_gguf_writer_set_scalar(rlh_gguf_writer* w, const char* key, uint32_t type, const void* value);
+int rlh_gguf_writer_set_string(rlh_gguf_writer* w, const char* key, const char* s, uint64_t len);
+int rlh_gguf_writer_set_array(rlh_gguf_writer* w, const char* key, uint32_t elem_type, const void* values, uint64_t n);
+int rlh_gguf_writer_add_tensor(rlh_gguf_writer* w, const char* name, uint32_t ggml_type, uint32_t n_dims,
+                               const uint64_t* dims, const void* data, uint64_t nbytes);
+int rlh_gguf_writer_write(rlh_gguf_writer* w, const char* path);
 
 /* ---- KV cache ------------------------------------------------------------
  * Replaces Model::new_cache / KvCache (src/model.rs:107-134, 339-342):

@@ -32,6 +32,14 @@ KIND_NAMES = {0: "token_embd", 1: "output_norm", 2: "output", 3: "attn_norm", 4:
               16: "attn_v_bias"}
 
 RLH_OK, RLH_EINVAL, RLH_ENOMEM, RLH_EDEVICE, RLH_ESTATE, RLH_ECTX, RLH_EUNSUP = 0, -1, -2, -3, -4, -5, -6
+RLH_EIO, RLH_EFORMAT, RLH_ENOENT = -7, -8, -9
+
+# GGUF metadata value types (src/gguf.rs:204-235)
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL = 0, 1, 2, 3, 4, 5, 6, 7
+GGUF_STR, GGUF_ARR, GGUF_U64, GGUF_I64, GGUF_F64 = 8, 9, 10, 11, 12
+_GGUF_NP = {GGUF_U8: np.uint8, GGUF_I8: np.int8, GGUF_U16: np.uint16, GGUF_I16: np.int16, GGUF_U32: np.uint32,
+            GGUF_I32: np.int32, GGUF_F32: np.float32, GGUF_BOOL: np.uint8, GGUF_U64: np.uint64,
+            GGUF_I64: np.int64, GGUF_F64: np.float64}
 
 
 def row_bytes(ty, cols):
@@ -270,6 +278,35 @@ def load():
         "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode_kernel": (I32, [P, P, I32, U32, I32, ctypes.POINTER(ctypes.c_double),
                                             ctypes.POINTER(U64)]),
+        "rlh_gguf_open": (I32, [ctypes.c_char_p, ctypes.POINTER(P)]),
+        "rlh_gguf_close": (None, [P]),
+        "rlh_gguf_version": (U32, [P]),
+        "rlh_gguf_n_files": (U64, [P]),
+        "rlh_gguf_n_tensors": (U64, [P]),
+        "rlh_gguf_tensor_info": (I32, [P, U64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(U32),
+                                       ctypes.POINTER(U32), P, U32, ctypes.POINTER(U64), ctypes.POINTER(U32)]),
+        "rlh_gguf_tensor_bytes": (I32, [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(U64)]),
+        "rlh_gguf_n_meta": (U64, [P]),
+        "rlh_gguf_meta_key": (I32, [P, U64, ctypes.POINTER(ctypes.c_char_p)]),
+        "rlh_gguf_meta_type": (I32, [P, ctypes.c_char_p, ctypes.POINTER(U32), ctypes.POINTER(U32),
+                                     ctypes.POINTER(U64)]),
+        "rlh_gguf_meta_u32": (I32, [P, ctypes.c_char_p, ctypes.POINTER(U32)]),
+        "rlh_gguf_meta_f32": (I32, [P, ctypes.c_char_p, ctypes.POINTER(F)]),
+        "rlh_gguf_meta_scalar": (I32, [P, ctypes.c_char_p, ctypes.POINTER(U64), ctypes.POINTER(ctypes.c_int64),
+                                       ctypes.POINTER(ctypes.c_double)]),
+        "rlh_gguf_meta_str": (I32, [P, ctypes.c_char_p, ctypes.POINTER(P), ctypes.POINTER(U64)]),
+        "rlh_gguf_meta_arr_str": (I32, [P, ctypes.c_char_p, U64, ctypes.POINTER(P), ctypes.POINTER(U64)]),
+        "rlh_gguf_meta_arr_scalar": (I32, [P, ctypes.c_char_p, U64, ctypes.POINTER(U64),
+                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_double)]),
+        "rlh_gguf_config": (I32, [P, ctypes.POINTER(Config), ctypes.c_char_p, U64]),
+        "rlh_model_load_gguf": (I32, [P, ctypes.POINTER(P)]),
+        "rlh_gguf_writer_create": (I32, [U32, U64, ctypes.POINTER(P)]),
+        "rlh_gguf_writer_destroy": (None, [P]),
+        "rlh_gguf_writer_set_scalar": (I32, [P, ctypes.c_char_p, U32, P]),
+        "rlh_gguf_writer_set_string": (I32, [P, ctypes.c_char_p, ctypes.c_char_p, U64]),
+        "rlh_gguf_writer_set_array": (I32, [P, ctypes.c_char_p, U32, P, U64]),
+        "rlh_gguf_writer_add_tensor": (I32, [P, ctypes.c_char_p, U32, U32, P, P, U64]),
+        "rlh_gguf_writer_write": (I32, [P, ctypes.c_char_p]),
         "rlh_quantize_row": (I32, [U32, P, U64, P]),
         "rlh_synth_normal": (None, [U64, U64, U64, U64, F, F, P]),
         "rlh_synth_tensor": (I32, [U64, U64, U32, U64, U64, F, F, P, I32]),
@@ -477,3 +514,215 @@ def matmul_batch(ty, w, rows, cols, xs, n):
     check(load().rlh_matmul_batch(ty, np.ascontiguousarray(w).ctypes.data, rows, cols, xs.ctypes.data, n,
                                   ys.ctypes.data))
     return ys
+
+
+# ---- GGUF files (src/gguf.rs, src/prune.rs:381-442) -------------------------
+
+def gguf_tensor_name(kind, layer):
+    """GGUF name of a tensor kind (Model::load's names, model.rs:164-218)."""
+    base = KIND_NAMES[kind]
+    suffix = ".bias" if kind in (T_ATTN_Q_BIAS, T_ATTN_K_BIAS, T_ATTN_V_BIAS) else ".weight"
+    if base.endswith("_bias"):
+        base = base[:-5]
+    if kind in (T_TOKEN_EMBD, T_OUTPUT_NORM, T_OUTPUT):
+        return base + suffix
+    return f"blk.{layer}.{base}{suffix}"
+
+
+class Gguf:
+    """A GGUF file opened with rlh_gguf_open (GgufFile, gguf.rs:125-421)."""
+
+    def __init__(self, path):
+        self.lib = load()
+        h = ctypes.c_void_p()
+        check(self.lib.rlh_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.rlh_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    @property
+    def version(self):
+        return self.lib.rlh_gguf_version(self.h)
+
+    @property
+    def n_files(self):
+        return self.lib.rlh_gguf_n_files(self.h)
+
+    def tensors(self):
+        """[(name, ggml type, dims, offset, file index)] in file order."""
+        out = []
+        for i in range(self.lib.rlh_gguf_n_tensors(self.h)):
+            name, ty, nd = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_uint32()
+            dims = (ctypes.c_uint64 * 8)()
+            off, fi = ctypes.c_uint64(), ctypes.c_uint32()
+            check(self.lib.rlh_gguf_tensor_info(self.h, i, ctypes.byref(name), ctypes.byref(ty), ctypes.byref(nd),
+                                                dims, 8, ctypes.byref(off), ctypes.byref(fi)))
+            out.append((name.value.decode(), ty.value, [int(dims[k]) for k in range(min(nd.value, 8))],
+                        off.value, fi.value))
+        return out
+
+    def tensor_bytes(self, name):
+        """A copy of the tensor's bytes (uint8 array)."""
+        p, n = ctypes.c_void_p(), ctypes.c_uint64()
+        check(self.lib.rlh_gguf_tensor_bytes(self.h, name.encode(), ctypes.byref(p), ctypes.byref(n)))
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint8)), shape=(n.value,)).copy() \
+            if n.value else np.zeros(0, np.uint8)
+
+    def keys(self):
+        out = []
+        for i in range(self.lib.rlh_gguf_n_meta(self.h)):
+            k = ctypes.c_char_p()
+            check(self.lib.rlh_gguf_meta_key(self.h, i, ctypes.byref(k)))
+            out.append(k.value.decode())
+        return out
+
+    def meta_type(self, key):
+        t, e, n = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+        check(self.lib.rlh_gguf_meta_type(self.h, key.encode(), ctypes.byref(t), ctypes.byref(e), ctypes.byref(n)))
+        return t.value, e.value, n.value
+
+    def _scalar(self, ty, u, i, f):
+        if ty in (GGUF_U8, GGUF_U16, GGUF_U32, GGUF_U64):
+            return int(u)
+        if ty in (GGUF_I8, GGUF_I16, GGUF_I32, GGUF_I64):
+            return int(i)
+        if ty == GGUF_BOOL:
+            return bool(u)
+        return float(f)
+
+    def meta(self, key):
+        """The value of a metadata key as a Python value (str, int, float,
+        bool, or a list of them)."""
+        ty, et, n = self.meta_type(key)
+        kb = key.encode()
+        if ty == GGUF_STR:
+            p, ln = ctypes.c_void_p(), ctypes.c_uint64()
+            check(self.lib.rlh_gguf_meta_str(self.h, kb, ctypes.byref(p), ctypes.byref(ln)))
+            return ctypes.string_at(p, ln.value).decode("utf-8", "replace")
+        u, i, f = ctypes.c_uint64(), ctypes.c_int64(), ctypes.c_double()
+        if ty != GGUF_ARR:
+            check(self.lib.rlh_gguf_meta_scalar(self.h, kb, ctypes.byref(u), ctypes.byref(i), ctypes.byref(f)))
+            return self._scalar(ty, u.value, i.value, f.value)
+        out = []
+        for k in range(n):
+            if et == GGUF_STR:
+                p, ln = ctypes.c_void_p(), ctypes.c_uint64()
+                check(self.lib.rlh_gguf_meta_arr_str(self.h, kb, k, ctypes.byref(p), ctypes.byref(ln)))
+                out.append(ctypes.string_at(p, ln.value).decode("utf-8", "replace"))
+            else:
+                check(self.lib.rlh_gguf_meta_arr_scalar(self.h, kb, k, ctypes.byref(u), ctypes.byref(i),
+                                                        ctypes.byref(f)))
+                out.append(self._scalar(et, u.value, i.value, f.value))
+        return out
+
+    def config(self):
+        """(Config, architecture) of Model::read_config (model.rs:241-293)."""
+        c = Config()
+        arch = ctypes.create_string_buffer(64)
+        check(self.lib.rlh_gguf_config(self.h, ctypes.byref(c), arch, 64))
+        return c, arch.value.decode()
+
+
+def write_gguf(path, meta, tensors, version=3, alignment=32):
+    """write_gguf (prune.rs:381-442). meta: {key: (gguf type, value)} where an
+    array value is (GGUF_ARR, (element type, list)); tensors: [(name, ggml
+    type, dims, bytes as a uint8 array)] with dims[0] the row length."""
+    lib = load()
+    w = ctypes.c_void_p()
+    check(lib.rlh_gguf_writer_create(version, alignment, ctypes.byref(w)))
+    keep = []
+    try:
+        for key, (ty, val) in meta.items():
+            kb = key.encode()
+            if ty == GGUF_STR:
+                b = val.encode() if isinstance(val, str) else bytes(val)
+                check(lib.rlh_gguf_writer_set_string(w, kb, b, len(b)))
+            elif ty == GGUF_ARR:
+                et, items = val
+                if et == GGUF_STR:
+                    bufs = [(x.encode() if isinstance(x, str) else bytes(x)) for x in items]
+                    arr = (ctypes.c_char_p * max(1, len(bufs)))(*bufs)
+                    keep.append((bufs, arr))
+                    check(lib.rlh_gguf_writer_set_array(w, kb, et, arr, len(bufs)))
+                else:
+                    a = np.ascontiguousarray(np.array(items, dtype=_GGUF_NP[et]))
+                    keep.append(a)
+                    check(lib.rlh_gguf_writer_set_array(w, kb, et, a.ctypes.data if len(a) else None, len(a)))
+            else:
+                a = np.array([val], dtype=_GGUF_NP[ty])
+                check(lib.rlh_gguf_writer_set_scalar(w, kb, ty, a.ctypes.data))
+        for name, ty, dims, data in tensors:
+            d = np.array(dims, np.uint64)
+            buf = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+            keep.append((d, buf))
+            check(lib.rlh_gguf_writer_add_tensor(w, name.encode(), ty, len(d), d.ctypes.data,
+                                                 buf.ctypes.data if buf.size else None, buf.size))
+        check(lib.rlh_gguf_writer_write(w, os.fsencode(path)))
+    finally:
+        lib.rlh_gguf_writer_destroy(w)
+
+
+def model_gguf_meta(spec, n_ctx=None, vocab_tokens=None, extra=None):
+    """Qwen3 metadata of a synthetic model (the keys Model::read_config and
+    read_tokenizer read, model.rs:241-330). The vocabulary is placeholder
+    strings unless given."""
+    a = "qwen3"
+    tokens = vocab_tokens if vocab_tokens is not None else [f"<t{i}>" for i in range(spec.vocab)]
+    meta = {
+        "general.architecture": (GGUF_STR, a),
+        f"{a}.block_count": (GGUF_U32, spec.n_layer),
+        f"{a}.embedding_length": (GGUF_U32, spec.n_embd),
+        f"{a}.feed_forward_length": (GGUF_U32, spec.n_ff),
+        f"{a}.attention.head_count": (GGUF_U32, spec.n_head),
+        f"{a}.attention.head_count_kv": (GGUF_U32, spec.n_head_kv),
+        f"{a}.attention.key_length": (GGUF_U32, spec.head_dim),
+        f"{a}.attention.value_length": (GGUF_U32, spec.head_dim),
+        f"{a}.rope.freq_base": (GGUF_F32, spec.rope_theta),
+        f"{a}.attention.layer_norm_rms_epsilon": (GGUF_F32, spec.rms_eps),
+        f"{a}.context_length": (GGUF_U32, n_ctx or spec.n_ctx),
+        "tokenizer.ggml.model": (GGUF_STR, "gpt2"),
+        "tokenizer.ggml.tokens": (GGUF_ARR, (GGUF_STR, tokens)),
+        "tokenizer.ggml.token_type": (GGUF_ARR, (GGUF_I32, [1] * len(tokens))),
+        "tokenizer.ggml.bos_token_id": (GGUF_U32, 0),
+        "tokenizer.ggml.eos_token_id": (GGUF_U32, max(0, len(tokens) - 1)),
+    }
+    meta.update(extra or {})
+    return meta
+
+
+def model_gguf_tensors(tensors):
+    """(name, type, dims, bytes) GGUF entries of synth_model's tensors."""
+    return [(gguf_tensor_name(kind, layer), ty, [cols] if rows == 1 and kind not in (T_TOKEN_EMBD, T_OUTPUT)
+             else [cols, rows], buf) for kind, layer, ty, cols, rows, buf in tensors]
+
+
+def write_model_gguf(path, spec, tensors, **kw):
+    """A synthetic model (synth_model's tensors) as one Qwen3 GGUF file."""
+    write_gguf(path, model_gguf_meta(spec, **kw), model_gguf_tensors(tensors))
+
+
+def load_model_gguf(path, spec=None):
+    """Model::load through rlh_model_load_gguf; returns a Model whose spec is
+    `spec` (or one built from the file's config)."""
+    with Gguf(path) as g:
+        lib = load()
+        h = ctypes.c_void_p()
+        check(lib.rlh_model_load_gguf(g.h, ctypes.byref(h)))
+        if spec is None:
+            c, _ = g.config()
+            spec = ModelSpec("gguf", c.n_layer, c.n_embd, c.n_ff, c.n_head, c.n_head_kv, c.vocab_size,
+                             not c.has_output, {}, c.head_dim, c.rope_theta, c.rms_eps, c.n_ctx)
+    m = Model.__new__(Model)
+    m.lib = lib
+    m.spec = spec
+    m.h = h
+    return m
