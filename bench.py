@@ -164,6 +164,11 @@ def main():
     ap.add_argument("--probe-steps", type=int, default=32,
                     help="decode steps whose dominant-kernel launches are timed with HIP events")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle sample")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time the prefill of each pass only (no decode, no JSON line; for counter runs)")
+    ap.add_argument("--kernel-launches", type=int, default=0,
+                    help="with --prefill-only: then launch the dominant decode kernel (rmsnorm + gate/up "
+                         "+ silu*up) this many times back to back, rotating over the layers (for counter runs)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="also run a device-to-device copy of this many MiB (counter calibration under rocprofv3)")
     args = ap.parse_args()
@@ -192,6 +197,20 @@ def main():
     params = rlh.sampling_params()  # the CLI defaults (main.rs:44-52)
     never = spec.vocab + 7            # end-of-sequence id no token can take: fixed token counts
 
+    if args.prefill_only:
+        for i in range(args.warmup + args.steps):
+            cache.reset()
+            t0 = time.perf_counter()
+            cache.forward_into(prompt, 0)
+            log(f"prefill {i + 1}/{args.warmup + args.steps}: {n_prompt / (time.perf_counter() - t0):.1f} tok/s")
+        if args.kernel_launches > 0:
+            us = cache.profile_matvec(rlh.T_FFN_GATE, args.kernel_launches)
+            log(f"{args.kernel_launches} back-to-back launches of the gate/up kernel: {us:.3f} us each")
+        if args.calib_copy_mb > 0:
+            calibration_copy(args.calib_copy_mb)
+        cache.close()
+        model.close()
+        return
     for i in range(args.warmup):
         run_pass(cache, prompt, n_decode, sampled, params, never)
         log(f"warm-up pass {i + 1}/{args.warmup}")

@@ -88,6 +88,10 @@ int orc_split_dequant(uint32_t ty, const uint8_t* src, size_t n, float* dst);   
 // --- ops.rs -------------------------------------------------------------------
 // Execution modes mirror the reference's env toggles.
 enum { ORC_MODE_DEFAULT = 0, ORC_MODE_NO_INT = 1, ORC_MODE_BATCH_INT = 2, ORC_MODE_NO_SIMD = 4 };
+// Not a reference mode: decode attention with its softmax and PV sums taken
+// over four position splits (the summation order of a split-K kernel), for
+// tests that measure how far a reordered f32 sum moves the greedy sequence.
+enum { ORC_MODE_SPLIT_ATTN = 8 };
 void orc_set_threads(int n);
 int orc_get_threads(void);
 float orc_dot(const float* a, const float* b, size_t n);                                // ops.rs:9-18

@@ -150,8 +150,31 @@ static void embed_row(const Weight& w, uint32_t tok, float* out) {  // tensor.rs
 
 // One (head, query) attention row: model.rs:674-689 / 693-710 / 525-543.
 static void attend_head(const float* qh, const float* kc, const float* vc, size_t t, size_t kv_dim, size_t kvh,
-                        size_t hd, float scale, float* scores, float* ah) {
+                        size_t hd, float scale, float* scores, float* ah, int mode) {
   for (size_t j = 0; j < t; j++) scores[j] = dot(qh, kc + j * kv_dim + kvh * hd, hd) * scale;
+  if (mode & ORC_MODE_SPLIT_ATTN) {
+    // NOT the reference: the softmax sum and the PV sums taken over four
+    // contiguous position splits, each in order, then combined pairwise (the
+    // order a split-K decode kernel uses); everything else unchanged
+    float mx = scores[0];
+    for (size_t j = 1; j < t; j++)
+      if (scores[j] > mx) mx = scores[j];
+    for (size_t j = 0; j < t; j++) scores[j] = std::exp(scores[j] - mx);
+    const size_t q = (t + 3) / 4;
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+    for (size_t j = 0; j < t; j++) part[j / q] += scores[j];
+    const float sum = (part[0] + part[1]) + (part[2] + part[3]);
+    if (sum > 0.0f) {
+      const float inv = 1.0f / sum;
+      for (size_t j = 0; j < t; j++) scores[j] *= inv;
+    }
+    for (size_t i = 0; i < hd; i++) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (size_t j = 0; j < t; j++) acc[j / q] += scores[j] * vc[j * kv_dim + kvh * hd + i];
+      ah[i] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    return;
+  }
   softmax_inplace(scores, t);
   for (size_t i = 0; i < hd; i++) ah[i] = 0.0f;
   for (size_t j = 0; j < t; j++) saxpy(ah, scores[j], vc + j * kv_dim + kvh * hd, hd);
@@ -191,12 +214,12 @@ static void forward_one(orc_model* m, uint32_t token, size_t pos, orc_cache* c, 
       parallel_for(H, [&](size_t h) {
         std::vector<float> scores(t);
         attend_head(c->q.data() + h * hd, kc, vc, t, kv_dim, h / group, hd, scale, scores.data(),
-                    c->attn.data() + h * hd);
+                    c->attn.data() + h * hd, mode);
       });
     } else {
       for (size_t h = 0; h < H; h++)
         attend_head(c->q.data() + h * hd, kc, vc, t, kv_dim, h / group, hd, scale, c->scores.data(),
-                    c->attn.data() + h * hd);
+                    c->attn.data() + h * hd, mode);
     }
     mm(L.attn_output, c->attn.data(), c->xb.data(), mode);
     for (size_t i = 0; i < E; i++) c->x[i] += c->xb[i];
@@ -269,7 +292,7 @@ static void forward_batch(orc_model* m, const uint32_t* tokens, size_t n_in, siz
       size_t t = start_pos + i + 1;
       for (size_t h = 0; h < H; h++)
         attend_head(q_all.data() + i * q_dim + h * hd, kc, vc, t, kv_dim, h / group, hd, scale, scores.data(),
-                    attn_all.data() + i * q_dim + h * hd);
+                    attn_all.data() + i * q_dim + h * hd, mode & ~ORC_MODE_SPLIT_ATTN);
     });
     mmb(L.attn_output, attn_all.data(), n, xb_all.data(), mode);
     for (size_t i = 0; i < n * E; i++) xs[i] += xb_all[i];

@@ -12,6 +12,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 MODE_DEFAULT, MODE_NO_INT, MODE_BATCH_INT, MODE_NO_SIMD = 0, 1, 2, 4
+MODE_SPLIT_ATTN = 8  # not a reference mode: split-K summation order in decode attention
 
 
 class OrcConfig(ctypes.Structure):

@@ -174,3 +174,36 @@ def test_golden_tiny_trace():
         lg = oc.forward_into(np.array([toks[-1]], np.uint32), len(prompt) + i, oracle.MODE_DEFAULT)
         toks.append(lib.orc_argmax(lg.ctypes.data, len(lg)))
     assert toks == list(map(int, f["tokens"]))
+
+
+def test_split_k_summation_order_breaks_the_parity_bars():
+    """Why the device path keeps the reference's summation order: on the
+    0.6B Q8_0 workload (48-token prompt, 128 greedy tokens), taking only the
+    decode attention's softmax sum and PV sums over four position splits
+    (the order of a split-K decode kernel; everything else bit-identical)
+    moves the first decode step's logits by more than the 2e-3 relative L2
+    bar and changes the greedy sequence within the workload's 128 tokens.
+    A Q8 activation block rounds a value to the other side of a .5 boundary
+    for a perturbation of one ulp, and that changes the next product by a
+    whole quantization step."""
+    name, P, N, _ = rlh.WORKLOADS[2]
+    spec = rlh.SPECS[name]
+    tensors = rlh.synth_model(spec, rlh.WORKLOAD_SEED)
+    prompt = rlh.synth_tokens(rlh.WORKLOAD_SEED + 1, P, spec.vocab)
+    lib = oracle.load()
+    om = oracle.OracleModel(spec, tensors)
+    runs = {}
+    for mode in (oracle.MODE_DEFAULT, oracle.MODE_SPLIT_ATTN):
+        oc = om.new_cache(P + N + 1)
+        lg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+        toks, first = [lib.orc_argmax(lg.ctypes.data, len(lg))], None
+        for i in range(N):
+            lg = oc.forward_into(np.array([toks[-1]], np.uint32), P + i, mode)
+            first = lg if first is None else first
+            toks.append(lib.orc_argmax(lg.ctypes.data, len(lg)))
+        runs[mode] = (toks, first)
+        oc.close()
+    om.close()
+    (a, la), (b, lb) = runs[oracle.MODE_DEFAULT], runs[oracle.MODE_SPLIT_ATTN]
+    assert rel_l2(lb, la) > 2e-3
+    assert a != b
