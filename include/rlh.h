@@ -182,6 +182,49 @@ int rlh_gguf_writer_add_tensor(rlh_gguf_writer* w, const char* name, uint32_t gg
                                const uint64_t* dims, const void* data, uint64_t nbytes);
 int rlh_gguf_writer_write(rlh_gguf_writer* w, const char* path);
 
+/* ---- tokenizer and chat template ---------------------------------------------
+ * The reference's byte-level BPE tokenizer (GPT-2 / Qwen2 flavour,
+ * src/tokenizer.rs): GPT-2 byte-to-unicode mapping, the Qwen2 pre-tokenizer
+ * pattern written out with Rust's char::is_alphabetic / is_numeric /
+ * is_whitespace, merges applied lowest rank first (leftmost on equal rank),
+ * token types 3 and 4 matched verbatim as special tokens (longest first). */
+typedef struct rlh_tokenizer rlh_tokenizer;
+/* Tokenizer::new (tokenizer.rs:56-112): tokens (NUL-terminated), their types
+ * (1 for entries past n_types), merges "left right" in rank order. */
+int rlh_tokenizer_create(const char* const* tokens, uint64_t n_tokens, const uint32_t* token_types, uint64_t n_types,
+                         const char* const* merges, uint64_t n_merges, uint32_t bos_id, uint32_t eos_id,
+                         rlh_tokenizer** out);
+/* Model::read_tokenizer (model.rs:295-330): tokenizer.ggml.tokens (required),
+ * .token_type, .merges, .bos_token_id (default 1), .eos_token_id (default 2). */
+int rlh_tokenizer_from_gguf(const rlh_gguf* g, rlh_tokenizer** out);
+void rlh_tokenizer_destroy(rlh_tokenizer* t);
+uint64_t rlh_tokenizer_vocab_size(const rlh_tokenizer* t);
+uint32_t rlh_tokenizer_bos(const rlh_tokenizer* t);
+uint32_t rlh_tokenizer_eos(const rlh_tokenizer* t);
+/* Tokenizer::encode (tokenizer.rs:299-334) of len bytes of UTF-8 text
+ * (RLH_EINVAL if invalid). *n_ids receives the token count; when it exceeds
+ * cap the first cap ids are written and RLH_EINVAL is returned. An empty
+ * special token string never matches (the reference would loop on it). */
+int rlh_tokenizer_encode(const rlh_tokenizer* t, const char* text, uint64_t len, uint32_t* ids, uint64_t cap,
+                         uint64_t* n_ids);
+/* The pre-tokenizer's pieces (tokenizer.rs:142-246) as byte ranges
+ * [bounds[2k], bounds[2k+1]); cap counts uint64 entries (2 per piece). */
+int rlh_tokenizer_pretokenize(const rlh_tokenizer* t, const char* text, uint64_t len, uint64_t* bounds, uint64_t cap,
+                              uint64_t* n_pieces);
+/* Tokenizer::decode (tokenizer.rs:336-359): the ids' bytes as lossy UTF-8
+ * (unknown ids skipped). *len receives the byte length; the text is
+ * NUL-terminated when it fits; RLH_EINVAL when it exceeds cap. */
+int rlh_tokenizer_decode(const rlh_tokenizer* t, const uint32_t* ids, uint64_t n, char* out, uint64_t cap,
+                         uint64_t* len);
+/* Tokenizer::token_bytes (tokenizer.rs:124-140): the raw bytes of one token. */
+int rlh_tokenizer_token_bytes(const rlh_tokenizer* t, uint32_t id, char* out, uint64_t cap, uint64_t* len);
+/* format_qwen_multiturn (tokenizer.rs:403-430; with no turns it is
+ * format_qwen_chat, 386-401): optional system block, the (role, content)
+ * turns, the user prompt, the assistant header and, with no_think, the
+ * empty think block. Strings are NUL-terminated; `system` may be NULL. */
+int rlh_format_qwen_chat(const char* const* roles, const char* const* contents, uint64_t n_turns, const char* prompt,
+                         const char* system, int no_think, char* out, uint64_t cap, uint64_t* len);
+
 /* ---- KV cache ------------------------------------------------------------
  * Replaces Model::new_cache / KvCache (src/model.rs:107-134, 339-342):
  * f32 K and V per layer in the same [pos][kv_head][head_dim] layout.

@@ -28,6 +28,7 @@
 
 #include "../../include/rlh.h"
 #include "sampler.h"
+#include "utf8.h"
 
 namespace {
 
@@ -123,11 +124,12 @@ struct Cursor {
     std::memcpy(v, b, sizeof(T));
     return true;
   }
+  // strings as String::from_utf8_lossy makes them (gguf.rs:191-195)
   bool str(std::string* s) {
     uint64_t len;
     const uint8_t* b;
     if (!get(&len) || !take(len, &b)) return false;
-    s->assign((const char*)b, (size_t)len);
+    *s = rlh::utf8_lossy(b, (size_t)len);
     return true;
   }
   bool value(uint32_t ty, Meta* m, int depth) {

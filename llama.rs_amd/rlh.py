@@ -307,6 +307,18 @@ def load():
         "rlh_gguf_writer_set_array": (I32, [P, ctypes.c_char_p, U32, P, U64]),
         "rlh_gguf_writer_add_tensor": (I32, [P, ctypes.c_char_p, U32, U32, P, P, U64]),
         "rlh_gguf_writer_write": (I32, [P, ctypes.c_char_p]),
+        "rlh_tokenizer_create": (I32, [P, U64, P, U64, P, U64, U32, U32, ctypes.POINTER(P)]),
+        "rlh_tokenizer_from_gguf": (I32, [P, ctypes.POINTER(P)]),
+        "rlh_tokenizer_destroy": (None, [P]),
+        "rlh_tokenizer_vocab_size": (U64, [P]),
+        "rlh_tokenizer_bos": (U32, [P]),
+        "rlh_tokenizer_eos": (U32, [P]),
+        "rlh_tokenizer_encode": (I32, [P, ctypes.c_char_p, U64, P, U64, ctypes.POINTER(U64)]),
+        "rlh_tokenizer_pretokenize": (I32, [P, ctypes.c_char_p, U64, P, U64, ctypes.POINTER(U64)]),
+        "rlh_tokenizer_decode": (I32, [P, P, U64, P, U64, ctypes.POINTER(U64)]),
+        "rlh_tokenizer_token_bytes": (I32, [P, U32, P, U64, ctypes.POINTER(U64)]),
+        "rlh_format_qwen_chat": (I32, [P, P, U64, ctypes.c_char_p, ctypes.c_char_p, I32, P, U64,
+                                       ctypes.POINTER(U64)]),
         "rlh_quantize_row": (I32, [U32, P, U64, P]),
         "rlh_synth_normal": (None, [U64, U64, U64, U64, F, F, P]),
         "rlh_synth_tensor": (I32, [U64, U64, U32, U64, U64, F, F, P, I32]),
@@ -726,3 +738,94 @@ def load_model_gguf(path, spec=None):
     m.spec = spec
     m.h = h
     return m
+
+
+# ---- tokenizer and chat template (src/tokenizer.rs) -------------------------
+
+def _cstr_array(items):
+    bufs = [x.encode() if isinstance(x, str) else bytes(x) for x in items]
+    return bufs, (ctypes.c_char_p * max(1, len(bufs)))(*bufs)
+
+
+class Tokenizer:
+    """The byte-level BPE tokenizer (Tokenizer, src/tokenizer.rs:34-359)."""
+
+    def __init__(self, tokens=None, token_types=None, merges=None, bos=1, eos=2, gguf=None):
+        self.lib = load()
+        h = ctypes.c_void_p()
+        if gguf is not None:
+            check(self.lib.rlh_tokenizer_from_gguf(gguf.h, ctypes.byref(h)))
+        else:
+            tb, ta = _cstr_array(tokens)
+            mb, ma = _cstr_array(merges or [])
+            ty = np.ascontiguousarray(token_types if token_types is not None else [], np.uint32)
+            check(self.lib.rlh_tokenizer_create(ta, len(tb), ty.ctypes.data if len(ty) else None, len(ty),
+                                                ma, len(mb), bos, eos, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.rlh_tokenizer_destroy(self.h)
+            self.h = None
+
+    @property
+    def vocab_size(self):
+        return self.lib.rlh_tokenizer_vocab_size(self.h)
+
+    @property
+    def bos(self):
+        return self.lib.rlh_tokenizer_bos(self.h)
+
+    @property
+    def eos(self):
+        return self.lib.rlh_tokenizer_eos(self.h)
+
+    def encode(self, text):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = ctypes.c_uint64()
+        rc = self.lib.rlh_tokenizer_encode(self.h, b, len(b), None, 0, ctypes.byref(n))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        out = np.zeros(max(1, n.value), np.uint32)
+        check(self.lib.rlh_tokenizer_encode(self.h, b, len(b), out.ctypes.data, len(out), ctypes.byref(n)))
+        return [int(x) for x in out[:n.value]]
+
+    def pretokenize(self, text):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = ctypes.c_uint64()
+        rc = self.lib.rlh_tokenizer_pretokenize(self.h, b, len(b), None, 0, ctypes.byref(n))
+        if rc != 0 and n.value == 0:
+            check(rc)
+        bounds = np.zeros(max(2, 2 * n.value), np.uint64)
+        check(self.lib.rlh_tokenizer_pretokenize(self.h, b, len(b), bounds.ctypes.data, len(bounds),
+                                                 ctypes.byref(n)))
+        return [b[int(bounds[2 * k]):int(bounds[2 * k + 1])].decode() for k in range(n.value)]
+
+    def _bytes_call(self, fn, *args):
+        n = ctypes.c_uint64()
+        fn(self.h, *args, None, 0, ctypes.byref(n))
+        buf = ctypes.create_string_buffer(n.value + 1)
+        check(fn(self.h, *args, buf, n.value + 1, ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def decode(self, ids):
+        a = np.ascontiguousarray(ids, np.uint32)
+        return self._bytes_call(self.lib.rlh_tokenizer_decode, a.ctypes.data if len(a) else None,
+                                len(a)).decode("utf-8")
+
+    def token_bytes(self, token_id):
+        return self._bytes_call(self.lib.rlh_tokenizer_token_bytes, token_id)
+
+
+def format_qwen_chat(prompt, system=None, no_think=False, turns=()):
+    """format_qwen_chat / format_qwen_multiturn (tokenizer.rs:386-430)."""
+    lib = load()
+    rb, ra = _cstr_array([r for r, _ in turns])
+    cb, ca = _cstr_array([c for _, c in turns])
+    n = ctypes.c_uint64()
+    args = (ra, ca, len(turns), prompt.encode(), system.encode() if system is not None else None,
+            1 if no_think else 0)
+    lib.rlh_format_qwen_chat(*args, None, 0, ctypes.byref(n))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(lib.rlh_format_qwen_chat(*args, buf, n.value + 1, ctypes.byref(n)))
+    return buf.raw[:n.value].decode()

@@ -310,3 +310,45 @@ def test_nan_logits_argmax_semantics():
         oc.close()
         m.close()
         om.close()
+
+
+def test_qwen2_biases_bit_exact():
+    """q/k/v biases (Qwen2, model.rs:444-464 prefill and 626-640 decode): added
+    after the products, before QK-norm and RoPE; prefill and decode logits
+    bit-exact against the oracle."""
+    spec = rlh.SPECS["tiny-q4km"]
+    tensors = rlh.synth_model(spec, 606)
+    lib = rlh.load()
+    qd, kvd = spec.n_head * spec.head_dim, spec.n_head_kv * spec.head_dim
+    for layer in range(spec.n_layer):
+        for kind, n in ((rlh.T_ATTN_Q_BIAS, qd), (rlh.T_ATTN_K_BIAS, kvd), (rlh.T_ATTN_V_BIAS, kvd)):
+            v = np.empty(n, np.float32)
+            lib.rlh_synth_normal(606, rlh.tensor_id(kind, layer), 0, n, 0.0, 0.5, v.ctypes.data)
+            tensors.append((kind, layer, rlh.F32, n, 1, v.view(np.uint8)))
+    m = rlh.Model(spec, tensors)
+    om = oracle.OracleModel(spec, tensors)
+    olib = oracle.load()
+    prompt = rlh.synth_tokens(607, 13, spec.vocab)
+    c = m.new_cache(32)
+    oc = om.new_cache(32)
+    try:
+        lg = c.forward_into(prompt, 0)
+        rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+        assert np.array_equal(bits(lg), bits(rg))
+        # without the biases the logits differ (the biases are applied)
+        m0 = rlh.Model(spec, [t for t in tensors if t[0] < rlh.T_ATTN_Q_BIAS])
+        c0 = m0.new_cache(32)
+        assert not np.array_equal(bits(c0.forward_into(prompt, 0)), bits(lg))
+        c0.close()
+        m0.close()
+        tok = olib.orc_argmax(rg.ctypes.data, len(rg))
+        for i in range(5):
+            lg = c.forward_into(np.array([tok], np.uint32), len(prompt) + i)
+            rg = oc.forward_into(np.array([tok], np.uint32), len(prompt) + i, oracle.MODE_DEFAULT)
+            assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ"
+            tok = olib.orc_argmax(rg.ctypes.data, len(rg))
+    finally:
+        c.close()
+        oc.close()
+        m.close()
+        om.close()
