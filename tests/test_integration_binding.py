@@ -15,17 +15,22 @@ C_SCALARS = {"int": "c_int", "uint32_t": "u32", "uint64_t": "u64", "int32_t": "i
 
 
 def c_to_rust(ctype):
-    """'const float*' -> '*const f32', 'rlh_model**' -> '*mut *mut RlhModel'."""
-    t = " ".join(ctype.replace("*", " * ").split())
-    stars = t.count("*")
-    words = [w for w in t.split() if w != "*"]
-    const = "const" in words
-    base = [w for w in words if w != "const"]
+    """'const float*' -> '*const f32', 'rlh_model**' -> '*mut *mut RlhModel',
+    'const char* const*' -> '*const *const c_char': each '*' becomes *const
+    when what it points to is const-qualified, else *mut."""
+    toks = ctype.replace("*", " * ").split()
+    base = [t for t in toks if t not in ("const", "*")]
     assert len(base) == 1, ctype
+    levels, pending = [], False
+    for t in toks:
+        if t == "const":
+            pending = True
+        elif t == "*":
+            levels.append(pending)
+            pending = False
     out = C_SCALARS[base[0]]
-    for i in range(stars):
-        # the innermost pointer carries the const of the pointee
-        out = ("*const " if (const and i == 0) else "*mut ") + out
+    for const in levels:
+        out = ("*const " if const else "*mut ") + out
     return out
 
 
@@ -70,6 +75,7 @@ def test_type_mapping():
     assert c_to_rust("rlh_model**") == "*mut *mut RlhModel"
     assert c_to_rust("const rlh_model*") == "*const RlhModel"
     assert c_to_rust("uint64_t") == "u64"
+    assert c_to_rust("const char* const*") == "*const *const c_char"
 
 
 def test_binding_mirrors_header():
