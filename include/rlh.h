@@ -285,11 +285,41 @@ int rlh_sample(const float* logits, uint64_t n, const rlh_sampling_params* p, co
  * runs it (sampler.rs:119): max, exp(x - max) with the platform expf's
  * results, the sum in index order, then x * (1 / sum) when the sum is > 0. */
 int rlh_softmax(float* x, uint64_t n);
-/* The same on the logits of the last forward call on this cache: the greedy
- * fast path (temperature <= 0 and no penalty) runs on the device, any other
- * setting copies the logits to the host first. */
+/* The same on the logits of the last forward call on this cache, on the
+ * device (rlh_dsampler_sample on the cache's stream); only the token comes
+ * back to the host. */
 int rlh_sample_next(rlh_model* m, rlh_cache* c, const rlh_sampling_params* p, const uint32_t* recent,
                     uint64_t n_recent, uint64_t* rng_state, uint32_t* token);
+
+/* Device sampler: Sampler::sample (src/sampler.rs:56-163) and
+ * ops::softmax_inplace (src/ops.rs:398-419) on device-resident values, with
+ * the tokens, probabilities and RNG states of rlh_sample / rlh_softmax bit
+ * for bit. The reference samples on the host after forward_into copies the
+ * logits out (model.rs:353-375, 741-776); these replace that copy and the
+ * host pass. A handle holds device workspace for n <= max_n on the device
+ * current at creation; calls on one handle must not overlap. */
+typedef struct rlh_dsampler rlh_dsampler;
+int rlh_dsampler_create(uint64_t max_n, rlh_dsampler** out);
+void rlh_dsampler_destroy(rlh_dsampler* ds);
+/* logits: device f32[n]. recent, rng_state and token are host memory. The
+ * stream (hipStream_t, NULL: the null stream) orders the reads of logits;
+ * the call returns after the token is known. Logits that turn into NaN or
+ * infinity after the penalty and temperature give RLH_EINVAL (the
+ * reference's sort panics on them); the RNG state is then unchanged. */
+int rlh_dsampler_sample(rlh_dsampler* ds, const float* logits, uint64_t n, const rlh_sampling_params* p,
+                        const uint32_t* recent, uint64_t n_recent, uint64_t* rng_state, uint32_t* token,
+                        void* stream);
+/* Softmax of device x[n] in place, enqueued on the stream (no wait). */
+int rlh_dsampler_softmax(rlh_dsampler* ds, float* x, uint64_t n, void* stream);
+/* Largest candidate list the top-k / top-p search sorts on chip (default and
+ * maximum 4096); longer lists, and 0 here, take the full radix sort. */
+int rlh_dsampler_set_candidate_cap(rlh_dsampler* ds, uint32_t cap);
+/* How the last rlh_dsampler_sample call chose its token (RLH_DSAMPLER_PATH_*). */
+#define RLH_DSAMPLER_PATH_GREEDY 1u     /* argmax (temperature <= 0)               */
+#define RLH_DSAMPLER_PATH_CANDIDATES 2u /* candidate list sorted on chip           */
+#define RLH_DSAMPLER_PATH_SORT 4u       /* radix sort of every probability         */
+#define RLH_DSAMPLER_PATH_FALLBACK 8u   /* candidates did not fit: sorted instead  */
+uint32_t rlh_dsampler_last_path(const rlh_dsampler* ds);
 /* Model::generate (src/model.rs:741-776): reset the cache, prefill the
  * prompt (n_prompt >= 1), then up to max_new steps of sample -> stop at
  * `eos` -> append -> stop when the cache is full -> decode. out_tokens

@@ -25,6 +25,7 @@
 #include "gemm.h"
 #include "rlh_format.h"
 #include "sampler.h"
+#include "sampler_dev.h"
 
 using namespace rlh;
 
@@ -291,6 +292,7 @@ struct rlh_cache {
   uint32_t* pi = nullptr;
   uint32_t nparts = 256;        // partials of the standalone argmax (rlh_greedy_next)
   uint32_t* host_st = nullptr;  // pinned staging for tok/pos
+  rlh_dsampler* ds = nullptr;   // device sampler (rlh_sample_next), made on first use
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
   bool debug = false;
   bool use_graphs = true;  // RLH_GRAPHS=0 launches the same kernels eagerly
@@ -729,6 +731,7 @@ static void cache_free(rlh_cache* c) {
   for (void* p : bptrs)
     if (p) (void)hipFree(p);
   if (c->host_st) (void)hipHostFree(c->host_st);
+  if (c->ds) rlh_dsampler_destroy(c->ds);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
 }
@@ -1030,22 +1033,8 @@ int rlh_sample_next(rlh_model* m, rlh_cache* c, const rlh_sampling_params* p, co
   if (rc) return rc;
   if (!p || !rng_state || !token || (n_recent && !recent)) return fail(RLH_EINVAL, "null argument");
   if (!c->logits_valid) return fail(RLH_ESTATE, "no logits computed on this cache yet");
-  // sampler.rs:62-70: the greedy fast path is the device argmax (first of
-  // equal maxima, NaN never wins) with the fast path's start at index 0: a
-  // NaN logits[0] is kept, since no value compares greater than it
-  if (p->temperature <= 0.0f && p->repetition_penalty == 1.0f) {
-    if ((rc = rlh_greedy_next(m, c, token))) return rc;
-    float l0 = 0.0f;
-    HIPCHK(hipMemcpyAsync(&l0, c->logits, 4, hipMemcpyDeviceToHost, c->st));
-    HIPCHK(hipStreamSynchronize(c->st));
-    if (l0 != l0) *token = 0;
-    return RLH_OK;
-  }
-  std::vector<float> host(m->cfg.vocab_size);
-  HIPCHK(hipMemcpyAsync(host.data(), c->logits, host.size() * 4, hipMemcpyDeviceToHost, c->st));
-  HIPCHK(hipStreamSynchronize(c->st));
-  *token = sample_logits(host.data(), host.size(), *p, recent, (size_t)n_recent, rng_state);
-  return RLH_OK;
+  if (!c->ds && (rc = rlh_dsampler_create(m->cfg.vocab_size, &c->ds))) return rc;
+  return dsampler_sample(c->ds, c->logits, m->cfg.vocab_size, *p, recent, n_recent, rng_state, token, c->st);
 }
 
 int rlh_generate(rlh_model* m, rlh_cache* c, const uint32_t* prompt, uint64_t n_prompt, uint64_t max_new,

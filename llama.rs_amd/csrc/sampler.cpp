@@ -169,6 +169,8 @@ void softmax_ref(float* x, size_t n) {
 
 void softmax_inplace(float* x, size_t n) { softmax_ref(x, n); }
 
+float sampler_next_f32(uint64_t* state) { return next_f32(state); }
+
 uint32_t sample_logits(const float* logits, size_t n, const rlh_sampling_params& p, const uint32_t* recent,
                        size_t n_recent, uint64_t* state) {
   if (n == 0) return 0;

@@ -274,6 +274,13 @@ def load():
         "rlh_matmul_batch": (I32, [U32, P, U64, U64, P, U64, P]),
         "rlh_block_dots": (I32, [U32, P, U64, U64, P, P]),
         "rlh_argmax_noalloc": (I32, [P, U64, P, P]),
+        "rlh_dsampler_create": (I32, [U64, ctypes.POINTER(P)]),
+        "rlh_dsampler_destroy": (None, [P]),
+        "rlh_dsampler_sample": (I32, [P, P, U64, ctypes.POINTER(SamplingParams), P, U64, ctypes.POINTER(U64),
+                                      ctypes.POINTER(U32), P]),
+        "rlh_dsampler_softmax": (I32, [P, P, U64, P]),
+        "rlh_dsampler_set_candidate_cap": (I32, [P, U32]),
+        "rlh_dsampler_last_path": (U32, [P]),
         "rlh_profile_matvec": (I32, [P, P, I32, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode": (I32, [P, P, I32, ctypes.POINTER(ctypes.c_double)]),
         "rlh_profile_decode_kernel": (I32, [P, P, I32, U32, I32, ctypes.POINTER(ctypes.c_double),
@@ -346,6 +353,51 @@ class Sampler:
         check(self.lib.rlh_sample(lg.ctypes.data, len(lg), ctypes.byref(params), r.ctypes.data, len(r),
                                   ctypes.byref(self.state), ctypes.byref(t)))
         return t.value
+
+
+DSAMPLER_PATH_GREEDY, DSAMPLER_PATH_CANDIDATES, DSAMPLER_PATH_SORT, DSAMPLER_PATH_FALLBACK = 1, 2, 4, 8
+
+
+class DeviceSampler:
+    """Sampler (src/sampler.rs:29-163) over device-resident logits
+    (rlh_dsampler_*): `logits` is a device address (e.g. a torch tensor's
+    data_ptr()) of n float32 values; the RNG state lives on the host as in
+    Sampler and advances identically."""
+
+    def __init__(self, seed, max_n):
+        self.lib = load()
+        self.state = ctypes.c_uint64(self.lib.rlh_sampler_init(seed))
+        h = ctypes.c_void_p()
+        check(self.lib.rlh_dsampler_create(max_n, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.lib.rlh_dsampler_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def sample(self, logits, n, params, recent, stream=None):
+        r = np.ascontiguousarray(recent, dtype=np.uint32)
+        t = ctypes.c_uint32()
+        check(self.lib.rlh_dsampler_sample(self.h, logits, n, ctypes.byref(params), r.ctypes.data, len(r),
+                                           ctypes.byref(self.state), ctypes.byref(t), stream))
+        return t.value
+
+    def softmax(self, x, n, stream=None):
+        check(self.lib.rlh_dsampler_softmax(self.h, x, n, stream))
+
+    def set_candidate_cap(self, cap):
+        check(self.lib.rlh_dsampler_set_candidate_cap(self.h, cap))
+
+    @property
+    def last_path(self):
+        return self.lib.rlh_dsampler_last_path(self.h)
 
 
 class RlhError(RuntimeError):

@@ -69,3 +69,40 @@ def rel_l2(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+class HipBuffers:
+    """Device buffers through libamdhip64 (ctypes), for entry points that take
+    device addresses. Copies are synchronous."""
+
+    def __init__(self):
+        import ctypes
+
+        self.ct = ctypes
+        self.h = ctypes.CDLL("libamdhip64.so")
+        self.bufs = []
+
+    def malloc(self, nbytes):
+        p = self.ct.c_void_p()
+        assert self.h.hipMalloc(self.ct.byref(p), self.ct.c_size_t(max(nbytes, 4))) == 0
+        self.bufs.append(p)
+        return p
+
+    def h2d(self, dst, arr):
+        a = np.ascontiguousarray(arr)
+        assert self.h.hipMemcpy(dst, a.ctypes.data_as(self.ct.c_void_p), self.ct.c_size_t(a.nbytes), 1) == 0
+
+    def d2h(self, src, n, dtype=np.float32):
+        out = np.zeros(n, dtype)
+        if n:
+            assert self.h.hipMemcpy(out.ctypes.data_as(self.ct.c_void_p), src, self.ct.c_size_t(out.nbytes), 2) == 0
+        return out
+
+    def sync(self):
+        assert self.h.hipDeviceSynchronize() == 0
+
+    def free(self):
+        self.sync()
+        for p in self.bufs:
+            self.h.hipFree(p)
+        self.bufs = []

@@ -11,7 +11,7 @@ C_SCALARS = {"int": "c_int", "uint32_t": "u32", "uint64_t": "u64", "int32_t": "i
              "float": "f32", "double": "f64", "char": "c_char", "void": "c_void",
              "rlh_config": "RlhConfig", "rlh_model": "RlhModel", "rlh_cache": "RlhCache",
              "rlh_sampling_params": "RlhSamplingParams", "rlh_gguf": "RlhGguf",
-             "rlh_gguf_writer": "RlhGgufWriter", "rlh_tokenizer": "RlhTokenizer"}
+             "rlh_gguf_writer": "RlhGgufWriter", "rlh_tokenizer": "RlhTokenizer", "rlh_dsampler": "RlhDsampler"}
 
 
 def c_to_rust(ctype):
