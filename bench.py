@@ -5,7 +5,7 @@ synthetic weights. A "step" is one pass of the whole workload: reset the
 cache, prefill the prompt (timed, logits copied to the host as the reference
 writes them), take the argmax of the prefill logits (untimed, as main.rs),
 then decode the workload's full token count (timed: every decode step with
-its argmax, or with the host sampler for workload 5). `--steps K` runs K
+its argmax, or with the device sampler for workload 5). `--steps K` runs K
 timed passes after `--warmup W` untimed ones; the decode window of every
 pass is the workload's own (512 tokens at KV 512 -> 1024 for the headline),
 whatever K is.
@@ -16,8 +16,10 @@ prefill tok/s, the decode step's HBM bytes and fraction of peak, the
 dominant decode kernel's roofline (the fused rmsnorm + gate/up + silu*up
 matvec, timed per launch inside real decode steps with HIP events bound to
 the launch; its HBM traffic from the committed rocprofv3 counter summary),
-and the CPU oracle (the C++ restatement of the reference's AVX2 path) on a
-bounded sample of the same workload on the host cores.
+the same decode window sampled with the CLI's sampling defaults on the
+device sampler (greedy workloads; `sampled_decode_tok_s`), and the CPU oracle
+(the C++ restatement of the reference's AVX2 path) on a bounded sample of
+the same workload on the host cores.
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 1..5]
 
@@ -80,7 +82,8 @@ def run_pass(cache, prompt, n_decode, sampled, params, never):
         toks = cache.generate_greedy(first, n_decode)
         return prefill_s, time.perf_counter() - t1, toks
     # Model::generate's loop (model.rs:760-774): sample from the last logits,
-    # append, forward the token; the sampler runs on the host
+    # append, forward the token; the sampler runs on the device and returns
+    # only the token
     del logits
     P = len(prompt)
     recent = np.empty(P + n_decode, np.uint32)
@@ -240,6 +243,13 @@ def main():
     step_bytes = wbytes + kv_read_bytes(spec, t_avg) + kvw
     hbm_frac_decode = step_bytes * tok_s / (HBM_PEAK_GBS * 1e9)
 
+    # the same window sampled (Model::generate's loop with the CLI defaults)
+    sampled_tok_s = None
+    if not sampled:
+        _, sd_s, _ = run_pass(cache, prompt, n_decode, True, params, never)
+        sampled_tok_s = round(n_decode / sd_s, 2)
+        log(f"sampled decode: {sampled_tok_s} tok/s")
+
     # dominant decode kernel: the fused rmsnorm + ffn_gate/ffn_up + silu*up
     # launch (k_mv<TY, 2>), each launch timed with HIP events bound to it
     # inside real decode steps (36 launches per step at 8B)
@@ -292,6 +302,7 @@ def main():
                      "avg_launch_us": round(mv_us, 3), "launches_timed": int(mv_launches),
                      "bytes_per_launch": int(pair_bytes)},
         "decode": "sampled" if sampled else "greedy",
+        "sampled_decode_tok_s": sampled_tok_s,
         "tokens_head": [int(t) for t in tokens[:8]],
     }
 
