@@ -77,8 +77,7 @@ int type_size(uint32_t ty) {  // quant.rs:53-66
 // Types whose device layout and dequantisation exist (the embedding gather
 // and the parity entries); matvec_supported() is the subset with a matvec.
 bool layout_supported(uint32_t ty) {
-  return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 ||
-         ty == RLH_TYPE_Q4_0 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16;
+  return is_tiled(ty) || ty == RLH_TYPE_F32 || ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -131,12 +130,25 @@ struct Layer {
 };
 
 // Item bytes (see rlh_format.h) of item j of a ggml row: super-blocks are
-// taken as they are; for Q8_0/Q4_0 the quants of 8 blocks come first, then
-// their 8 f16 scales.
+// taken as they are; for the 32-value types the quants of 8 blocks come
+// first, then their high bits (Q5_0/Q5_1), then their f16 scales (and mins).
 void gather_item(uint32_t ty, const uint8_t* row, uint32_t j, uint8_t* item) {
   if (ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q6_K) {
     const uint32_t ib = item_bytes(ty);
     std::memcpy(item, row + (size_t)j * ib, ib);
+    return;
+  }
+  if (ty == RLH_TYPE_Q4_1 || ty == RLH_TYPE_Q5_0 || ty == RLH_TYPE_Q5_1) {
+    // ggml blocks: Q4_1 (d, m, qs[16]); Q5_0 (d, qh[4], qs[16]); Q5_1 (d, m, qh[4], qs[16])
+    const uint32_t bs = (uint32_t)type_size(ty);
+    const uint32_t nsc = ty == RLH_TYPE_Q5_0 ? 2 : 4;       // scale bytes per block
+    const uint32_t nqh = ty == RLH_TYPE_Q4_1 ? 0 : 4;       // qh bytes per block
+    for (uint32_t k = 0; k < 8; k++) {
+      const uint8_t* blk = row + ((size_t)j * 8 + k) * bs;
+      std::memcpy(item + k * 16, blk + nsc + nqh, 16);                 // quants
+      if (nqh) std::memcpy(item + 128 + k * 4, blk + nsc, 4);         // qh
+      std::memcpy(item + 128 + 8 * nqh + k * nsc, blk, nsc);          // d (and m)
+    }
     return;
   }
   const uint32_t bs = (uint32_t)type_size(ty), qb = bs - 2;  // 34/32 or 18/16
@@ -421,12 +433,21 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       mv_plan_finish(p);
       mv_launch_probed(c, RLH_T_ATTN_OUTPUT, p);
     }
-    {  // rmsnorm(x, ffn_norm); gate, up, silu(g)*u and its Q8 blocks (model.rs:719-724)
+    if (L.gate.ty == L.up.ty) {  // rmsnorm(x, ffn_norm); gate, up, silu(g)*u and its Q8 blocks (model.rs:719-724)
       MvPlan p;
       mv_plan_init_norm(p, E, c->x, L.ffn_norm.p, eps);
       mv_plan_add_pair(p, L.gate.dm, L.up.dm, c->act_f, c->g);
       mv_plan_finish(p);
       mv_launch_probed(c, RLH_T_FFN_GATE, p);
+    } else {  // gate and up of different types: one launch each, then silu(g)*u and its Q8 blocks
+      for (int up = 0; up < 2; up++) {
+        MvPlan p;
+        mv_plan_init_norm(p, E, c->x, L.ffn_norm.p, eps);
+        mv_plan_add(p, up ? L.up.dm : L.gate.dm, up ? c->u : c->g, nullptr);
+        mv_plan_finish(p);
+        mv_launch_probed(c, RLH_T_FFN_GATE, p);
+      }
+      launch_swiglu_q8(st, c->g, c->u, F, c->act_f, c->g);
     }
     {  // ffn_down, x += (model.rs:725-728)
       MvPlan p;
@@ -627,8 +648,6 @@ int rlh_model_finalize(rlh_model* m) {
   // every decode matvec launch must fit the kernel's LDS budget
   for (uint32_t l = 0; l < c.n_layer; l++) {
     Layer& L = m->layers[l];
-    if (L.gate.ty != L.up.ty)
-      return fail(RLH_EUNSUP, "blk." + std::to_string(l) + ": ffn_gate and ffn_up must share a ggml type");
     const Q8Mut none{};
     static const float kShapeOnly = 0.0f;  // plans below are built for their shape only
     MvPlan p;
@@ -641,9 +660,17 @@ int rlh_model_finalize(rlh_model* m) {
     mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, L.o.dm, nullptr, nullptr);
     ok = ok && mv_plan_finish(p);
-    mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
-    mv_plan_add_pair(p, L.gate.dm, L.up.dm, none, nullptr);
-    ok = ok && mv_plan_finish(p);
+    if (L.gate.ty == L.up.ty) {
+      mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
+      mv_plan_add_pair(p, L.gate.dm, L.up.dm, none, nullptr);
+      ok = ok && mv_plan_finish(p);
+    } else {  // separate launches (the decode step's fallback)
+      for (const DevTensor* t : {&L.gate, &L.up}) {
+        mv_plan_init_norm(p, (uint32_t)E, nullptr, nullptr, 0.0f);
+        mv_plan_add(p, t->dm, nullptr, nullptr);
+        ok = ok && mv_plan_finish(p);
+      }
+    }
     mv_plan_init(p, (uint32_t)F, none);
     mv_plan_set_f32(p, &kShapeOnly);
     mv_plan_add(p, L.down.dm, nullptr, nullptr);

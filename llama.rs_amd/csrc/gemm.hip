@@ -507,13 +507,15 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Prefill products for Q5_K, which has no integer batch path in the
-// reference: matmul_batch's f32 route (ops.rs:237-312) dequantizes rows
-// (quant.rs:313-349) and runs dot_multi_rows::<3, 4> (simd.rs:779-836) on the
-// f32 activations. Every output of a token group of 4 is one 8-lane FMA chain
-// over the row (lane l takes elements 8i + l in order) reduced by the AVX2
-// tree; the last n % 4 tokens take dot_f32_avx2 (32 chains over 32-value
-// chunks, (a0+a1)+(a2+a3), tree). ys starts at zero and gets `+= value`.
+// Prefill products for the types with no integer batch path in the reference
+// (Q5_K, Q4_1, Q5_0, Q5_1, F16, BF16): matmul_batch's f32 route (ops.rs:237-312)
+// dequantizes rows (quant.rs:191-385) and runs dot_multi_rows::<3, 4>
+// (simd.rs:779-836) on the f32 activations. Every output of a token group of
+// 4 is one 8-lane FMA chain over the row (lane l takes elements 8i + l in
+// order) reduced by the AVX2 tree; the last n % 4 tokens take dot_f32_avx2
+// (32 chains over 32-value chunks, (a0+a1)+(a2+a3), tree). ys starts at zero
+// and gets `+= value`. F32 weights take matmul_batch's F32 fast path
+// (ops.rs:165-174): dot(row, x) for every token, stored as is.
 // Block: 16 rows x 16 tokens, one thread per (row, token) running its
 // chains; each 256-value super-block of the 16 rows is dequantized into LDS
 // once and the 16 tokens' activations staged beside it.
@@ -533,7 +535,104 @@ __device__ __forceinline__ float tree8(const float* A) {
   return ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
 }
 
-__global__ void __launch_bounds__(256) k_gemm_f32_q5k(GemmF32Args a) {
+// Values 16 * dp .. 16 * dp + 15 of super-block j (256 values) of row r,
+// dequantized exactly (quant.rs:191-385). The loads come first, the
+// conversion second, so that callers can place a barrier between them.
+template <uint32_t TY>
+struct Dq16 {
+  u32x4_t v[4];  // raw bytes
+  uint32_t aux0, aux1;
+  __device__ __forceinline__ void load(const DevMat& w, uint32_t r, uint32_t j, uint32_t dp) {
+    if constexpr (TY == RLH_TYPE_Q5_K) {
+      const uint32_t dsub = dp / 2, dl = 16 * (dp % 2);
+      v[0] = *(const RLH_GLOBAL u32x4_t*)(w.a + item_offset(w, r, j, 0));
+      v[1] = *(const RLH_GLOBAL u32x4_t*)(w.a + item_offset(w, r, j, 48 + 32 * (dsub / 2) + dl));
+      v[2] = *(const RLH_GLOBAL u32x4_t*)(w.a + item_offset(w, r, j, 16 + dl));
+    } else if constexpr (TY == RLH_TYPE_Q4_1 || TY == RLH_TYPE_Q5_0 || TY == RLH_TYPE_Q5_1) {
+      const uint32_t k = dp / 2;  // the 32-value block
+      v[0] = *(const RLH_GLOBAL u32x4_t*)(w.a + item_offset(w, r, j, 16 * k));
+      const uint32_t sc0 = TY == RLH_TYPE_Q4_1 ? 128 : 160;
+      if constexpr (TY != RLH_TYPE_Q4_1) aux1 = *(const RLH_GLOBAL uint32_t*)(w.a + item_offset(w, r, j, 128 + 4 * k));
+      if constexpr (TY == RLH_TYPE_Q5_0)
+        aux0 = *(const RLH_GLOBAL uint16_t*)(w.a + item_offset(w, r, j, sc0 + 2 * k));
+      else
+        aux0 = *(const RLH_GLOBAL uint32_t*)(w.a + item_offset(w, r, j, sc0 + 4 * k));
+    } else if constexpr (TY == RLH_TYPE_F16 || TY == RLH_TYPE_BF16) {
+      const uint8_t* p = w.a + (size_t)r * w.row_bytes + 2 * (256 * (size_t)j + 16 * dp);
+      v[0] = *(const RLH_GLOBAL u32x4_t*)p;
+      v[1] = *(const RLH_GLOBAL u32x4_t*)(p + 16);
+    } else {  // F32
+      const uint8_t* p = w.a + (size_t)r * w.row_bytes + 4 * (256 * (size_t)j + 16 * dp);
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[q] = *(const RLH_GLOBAL u32x4_t*)(p + 16 * q);
+    }
+  }
+  __device__ __forceinline__ void values(uint32_t dp, f32x4_t* o) const {
+    if constexpr (TY == RLH_TYPE_Q5_K) {
+      const uint32_t dsub = dp / 2;
+      const u32x4_t hdr = v[0], qv = v[1], hv = v[2];
+      const float d = f16_to_f32(hdr.x & 0xffff), dmin = f16_to_f32(hdr.x >> 16);
+      uint8_t sb[12];
+      const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
+#pragma unroll
+      for (int k = 0; k < 12; k++) sb[k] = (uint8_t)(sw[k / 4] >> (8 * (k % 4)));
+      uint32_t sc, m;
+      scale_min_k4((int)dsub, sb, sc, m);
+      const float d1 = d * (float)sc, mm1 = dmin * (float)m;
+      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t u = ((qw[q] >> (4 * (dsub & 1))) & 0x0F0F0F0Fu) | (((hw[q] >> dsub) & 0x01010101u) << 4);
+        o[q].x = d1 * (float)(u & 0xff) - mm1;
+        o[q].y = d1 * (float)((u >> 8) & 0xff) - mm1;
+        o[q].z = d1 * (float)((u >> 16) & 0xff) - mm1;
+        o[q].w = d1 * (float)(u >> 24) - mm1;
+      }
+    } else if constexpr (TY == RLH_TYPE_Q4_1 || TY == RLH_TYPE_Q5_0 || TY == RLH_TYPE_Q5_1) {
+      const uint32_t half = dp % 2;  // values 16 * half .. + 15 of the block
+      const uint32_t qw[4] = {v[0].x, v[0].y, v[0].z, v[0].w};
+      float d, m = 0.0f;
+      if constexpr (TY == RLH_TYPE_Q5_0) {
+        d = f16_to_f32(aux0 & 0xffff);
+      } else {
+        d = f16_to_f32(aux0 & 0xffff);
+        m = f16_to_f32(aux0 >> 16);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        float e[4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const uint32_t i = 4 * q + b;  // byte i of the block's quants
+          uint32_t x = (qw[q] >> (8 * b + 4 * half)) & 0xF;
+          if constexpr (TY != RLH_TYPE_Q4_1) x |= ((aux1 >> (i + 16 * half)) & 1u) << 4;
+          if constexpr (TY == RLH_TYPE_Q5_0)
+            e[b] = (float)((int)x - 16) * d;
+          else
+            e[b] = (float)x * d + m;
+        }
+        o[q] = f32x4_t{e[0], e[1], e[2], e[3]};
+      }
+    } else if constexpr (TY == RLH_TYPE_F16 || TY == RLH_TYPE_BF16) {
+      const uint32_t hw[8] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w};
+      auto cv = [](uint32_t h) {
+        return TY == RLH_TYPE_F16 ? f16_to_f32(h) : __uint_as_float(h << 16);  // quant.rs:115-157, bf16_to_f32
+      };
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        o[q] = f32x4_t{cv(hw[2 * q] & 0xffff), cv(hw[2 * q] >> 16), cv(hw[2 * q + 1] & 0xffff),
+                       cv(hw[2 * q + 1] >> 16)};
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        o[q] = f32x4_t{__uint_as_float(v[q].x), __uint_as_float(v[q].y), __uint_as_float(v[q].z),
+                       __uint_as_float(v[q].w)};
+    }
+  }
+};
+
+template <uint32_t TY>
+__global__ void __launch_bounds__(256) k_gemm_f32(GemmF32Args a) {
   __shared__ __attribute__((aligned(16))) float ws_g[kFR * kFS];
   __shared__ __attribute__((aligned(16))) float xs_g[kFT * kFS];
   typedef RLH_LDS float lfloat;
@@ -545,7 +644,7 @@ __global__ void __launch_bounds__(256) k_gemm_f32_q5k(GemmF32Args a) {
   const uint32_t nsb = a.w.cols / 256;
   const bool tail = tok >= a.n4;
   // dequant duty: row r0 + tid / 16, values 16 * (tid % 16) .. + 15 of the super-block
-  const uint32_t dr = tid / 16, dp = tid % 16, dsub = dp / 2, dl = 16 * (dp % 2);
+  const uint32_t dr = tid / 16, dp = tid % 16;
   const uint32_t drow = min(r0 + dr, a.w.rows - 1);
   float c8[8], c32[4][8];
 #pragma unroll
@@ -555,35 +654,19 @@ __global__ void __launch_bounds__(256) k_gemm_f32_q5k(GemmF32Args a) {
     for (int m = 0; m < 4; m++) c32[m][l] = 0.0f;
   }
   for (uint32_t j = 0; j < nsb; j++) {
-    // this thread's 16 dequantized values: the header chunk, its 16 quant
-    // bytes and 16 high-bit bytes (all 16-byte aligned inside the item)
-    const u32x4_t hdr = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 0));
-    const u32x4_t qv = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 48 + 32 * (dsub / 2) + dl));
-    const u32x4_t hv = *(const RLH_GLOBAL u32x4_t*)(a.w.a + item_offset(a.w, drow, j, 16 + dl));
+    Dq16<TY> dq;
+    dq.load(a.w, drow, j, dp);
     f32x4_t xv[4];
     const uint32_t xt = min(t0 + tid / 16, a.n - 1);
 #pragma unroll
     for (int q = 0; q < 4; q++)  // token t0 + tid / 16, values 16 * (tid % 16) + 4q
       xv[q] = *(const RLH_GLOBAL f32x4_t*)(a.x + (size_t)xt * a.w.cols + 256 * j + 16 * (tid % 16) + 4 * q);
-    const float d = f16_to_f32(hdr.x & 0xffff), dmin = f16_to_f32(hdr.x >> 16);
-    uint8_t sb[12];
-    const uint32_t sw[3] = {hdr.y, hdr.z, hdr.w};
-#pragma unroll
-    for (int k = 0; k < 12; k++) sb[k] = (uint8_t)(sw[k / 4] >> (8 * (k % 4)));
-    uint32_t sc, m;
-    scale_min_k4((int)dsub, sb, sc, m);
-    const float d1 = d * (float)sc, mm1 = dmin * (float)m;
-    const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w}, hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    f32x4_t wv[4];
+    dq.values(dp, wv);
     __syncthreads();  // the previous super-block's tiles are consumed
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const uint32_t v = ((qw[q] >> (4 * (dsub & 1))) & 0x0F0F0F0Fu) | (((hw[q] >> dsub) & 0x01010101u) << 4);
-      f32x4_t o;
-      o.x = d1 * (float)(v & 0xff) - mm1;
-      o.y = d1 * (float)((v >> 8) & 0xff) - mm1;
-      o.z = d1 * (float)((v >> 16) & 0xff) - mm1;
-      o.w = d1 * (float)(v >> 24) - mm1;
-      *(lf32x4*)(ws + dr * kFS + 32 * dsub + dl + 4 * q) = o;
+      *(lf32x4*)(ws + dr * kFS + 16 * dp + 4 * q) = wv[q];
       *(lf32x4*)(xs + (tid / 16) * kFS + 16 * (tid % 16) + 4 * q) = xv[q];
     }
     __syncthreads();
@@ -629,7 +712,9 @@ __global__ void __launch_bounds__(256) k_gemm_f32_q5k(GemmF32Args a) {
     float A[8];
 #pragma unroll
     for (int l = 0; l < 8; l++) A[l] = (c32[0][l] + c32[1][l]) + (c32[2][l] + c32[3][l]);
-    v = 0.0f + tree8(A);
+    // F32 weights store dot(row, x) (ops.rs:169-173); the others add it to
+    // the zeroed output (ops.rs:236 ys.fill, then +=)
+    v = TY == RLH_TYPE_F32 ? tree8(A) : 0.0f + tree8(A);
   }
   const size_t idx = (size_t)tok * a.w.rows + row;
   if (a.resid) {
@@ -645,7 +730,10 @@ bool gemm_supported(uint32_t ty) {
   return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0;
 }
 
-bool gemm_f32_supported(uint32_t ty) { return ty == RLH_TYPE_Q5_K; }
+bool gemm_f32_supported(uint32_t ty) {
+  return ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q4_1 || ty == RLH_TYPE_Q5_0 || ty == RLH_TYPE_Q5_1 ||
+         ty == RLH_TYPE_F16 || ty == RLH_TYPE_BF16 || ty == RLH_TYPE_F32;
+}
 
 void launch_gemm_f32(hipStream_t st, const DevMat& w, const float* x, uint32_t n, uint32_t n4, float* y,
                      float* resid) {
@@ -656,7 +744,18 @@ void launch_gemm_f32(hipStream_t st, const DevMat& w, const float* x, uint32_t n
   a.n4 = n4;
   a.y = y;
   a.resid = resid;
-  hipLaunchKernelGGL(k_gemm_f32_q5k, dim3((w.rows + kFR - 1) / kFR, (n + kFT - 1) / kFT), dim3(256), 0, st, a);
+  if (w.ty == RLH_TYPE_F32) a.n4 = 0;  // every token takes dot_f32_avx2 (ops.rs:165-174)
+  const dim3 grid((w.rows + kFR - 1) / kFR, (n + kFT - 1) / kFT);
+  switch (w.ty) {
+    case RLH_TYPE_Q5_K: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_Q5_K>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_Q4_1: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_Q4_1>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_Q5_0: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_Q5_0>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_Q5_1: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_Q5_1>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_F16: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_F16>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_BF16: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_BF16>, grid, dim3(256), 0, st, a); break;
+    case RLH_TYPE_F32: hipLaunchKernelGGL(k_gemm_f32<RLH_TYPE_F32>, grid, dim3(256), 0, st, a); break;
+    default: break;
+  }
 }
 
 void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, float* y, float* resid) {

@@ -334,7 +334,8 @@ void launch_quantize_q8(hipStream_t st, const float* x, uint32_t n, const Q8Buf&
 
 bool matvec_supported(uint32_t ty) {
   return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
-         ty == RLH_TYPE_Q5_K;
+         ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q4_1 || ty == RLH_TYPE_Q5_0 || ty == RLH_TYPE_Q5_1 ||
+         ty == RLH_TYPE_F16 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_BF16;
 }
 
 void launch_block_dots(hipStream_t st, const DevMat& w, const int8_t* a, int32_t* out, uint32_t per_row) {

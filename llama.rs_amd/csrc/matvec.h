@@ -65,6 +65,7 @@ struct MvPlan {
   uint32_t lds = 0;
   uint32_t waves = 0;  // waves per block
   uint32_t max_terms = 0;
+  uint32_t slot_stride = 0;  // float plans: floats per row of chain results
   uint32_t rows = 0;   // rows over all segments
   bool norm = false;   // activation from the norm prologue
   bool quant = false;  // ... without the norm (quantize_q8 of the f32 row only)
@@ -72,8 +73,10 @@ struct MvPlan {
 
 // Terms (float summands of the reference's per-row chain) per 256-value
 // super-block: one per 64 values for Q4_K, per 16 for Q6_K, per 32 for
-// Q8_0/Q4_0, one per super-block for Q5_K (its f32 block dot).
+// Q8_0/Q4_0/Q4_1/Q5_0/Q5_1, one per super-block for Q5_K (its f32 block
+// dot); none for float weights, whose rows are whole chains.
 __host__ __device__ inline uint32_t mv_terms_per_sb(uint32_t ty) {
+  if (ty == RLH_TYPE_F16 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_BF16) return 0u;  // whole-row chains
   return ty == RLH_TYPE_Q6_K ? 16u : (ty == RLH_TYPE_Q4_K ? 4u : (ty == RLH_TYPE_Q5_K ? 1u : 8u));
 }
 

@@ -337,6 +337,81 @@ struct MI<RLH_TYPE_Q5_K> {
   }
 };
 
+// Q4_1 / Q5_0 / Q5_1: no integer kernel in the reference; the row is
+// dequant_dot_scalar's generic fallback (quant.rs:528-539): per 32-value
+// block, dequant_row (quant.rs:222-272) then ops::dot, which for 32 values is
+// dot_f32_avx2 (simd.rs:328-377) with one chunk: slot (m, l) = fma(w, x, +0)
+// of value 8m + l, A_l = (a0+a1)+(a2+a3), the AVX2 tree. One term per block,
+// added to the row total in block order; part h = blocks 4h .. 4h+3. Item
+// chunks: 0-7 the blocks' quants, then qh (8-9; Q5_0/Q5_1), then d / (d, m).
+template <uint32_t TY>
+struct MI32f {
+  static constexpr bool kHi = TY != RLH_TYPE_Q4_1;  // a fifth bit per value
+  static constexpr bool kMin = TY != RLH_TYPE_Q5_0;  // q * d + m (else (q - 16) * d)
+  static constexpr uint32_t kT = 8;
+  static constexpr int kParts = 2;
+  static constexpr int kLoads = kHi ? 6 : 5;
+  struct P {
+    u32x4_t q[4], sc, hi;  // hi: qh of the part's blocks (zero for Q4_1)
+  };
+  __device__ __forceinline__ static void load(P& r, const uint8_t* tile, uint32_t lane, int h) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) r.q[k] = gl_u4(tile + (4 * h + k) * 1024 + lane * 16);
+    if (kHi) {
+      r.hi = gl_u4(tile + (8 + h) * 1024 + lane * 16);
+      r.sc = gl_u4(tile + (kMin ? 10 + h : 10) * 1024 + lane * 16);
+    } else {
+      r.hi = u32x4_t{0u, 0u, 0u, 0u};
+      r.sc = gl_u4(tile + (8 + h) * 1024 + lane * 16);
+    }
+  }
+  __device__ __forceinline__ static void terms(const P& r, const LAct& act, uint32_t j, lfloat* t, int h) {
+    const lf32x4* x4 = (const lf32x4*)(act.xf + j * kXfStride);
+    const uint32_t sw[4] = {r.sc.x, r.sc.y, r.sc.z, r.sc.w};
+    const uint32_t hw[4] = {r.hi.x, r.hi.y, r.hi.z, r.hi.w};
+    float out[4];
+#pragma unroll
+    for (int kl = 0; kl < 4; kl++) {
+      const int k = 4 * h + kl;
+      float d, m = 0.0f;
+      if (kMin) {
+        d = f16_to_f32(sw[kl] & 0xffff);
+        m = f16_to_f32(sw[kl] >> 16);
+      } else {
+        d = f16_to_f32((sw[k >> 1] >> (16 * (k & 1))) & 0xffff);
+      }
+      const u32x4_t qv = r.q[kl];
+      const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+      float a[4][8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {  // values 4c .. 4c+3 of the block
+        const f32x4_t xv = x4[8 * k + c];
+        const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+          const int e = 4 * c + b;
+          const uint32_t byte = (qw[(e & 15) >> 2] >> (8 * (e & 3))) & 0xff;
+          uint32_t q = e < 16 ? (byte & 0xF) : (byte >> 4);
+          if (kHi) q |= ((hw[kl] >> e) & 1u) << 4;
+          const float wv = kMin ? (float)q * d + m : (float)((int)q - 16) * d;
+          a[e >> 3][e & 7] = __builtin_fmaf(wv, xs[b], 0.0f);
+        }
+      }
+      float A[8];
+#pragma unroll
+      for (int l = 0; l < 8; l++) A[l] = (a[0][l] + a[1][l]) + (a[2][l] + a[3][l]);
+      out[kl] = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+    }
+    *(lf32x4*)(t + 4 * h) = f32x4_t{out[0], out[1], out[2], out[3]};
+  }
+};
+template <>
+struct MI<RLH_TYPE_Q4_1> : MI32f<RLH_TYPE_Q4_1> {};
+template <>
+struct MI<RLH_TYPE_Q5_0> : MI32f<RLH_TYPE_Q5_0> {};
+template <>
+struct MI<RLH_TYPE_Q5_1> : MI32f<RLH_TYPE_Q5_1> {};
+
 // In-order sum of n terms (the per-row f32 chain).
 __device__ __forceinline__ float chain(const lfloat* t, uint32_t n) { return seq_sum_lds(t, n); }
 
@@ -455,11 +530,118 @@ __device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
   }
 }
 
+// Float weights (F16, F32, BF16: rows as stored, no tiles). The reference's
+// row products are chains over the whole row: F16 (simd.rs:401-419) eight
+// FMA chains, lane l taking values 8i + l, then the AVX2 tree; F32 weights
+// (ops.rs:77-83, dot_f32_avx2 simd.rs:328-377) 32 FMA chains, chain (m, l)
+// taking 32c + 8m + l, then (a0+a1)+(a2+a3) and the tree; BF16
+// (quant.rs:427-433) one chain acc += w * x in index order. Each thread of
+// the block runs whole chains (a row's slot) over the f32 activation in LDS;
+// lane r of wave m then reduces row r's slots, and the epilogue is the
+// tiled path's.
+__host__ __device__ constexpr uint32_t mv_float_slots(uint32_t ty) {
+  return ty == RLH_TYPE_F32 ? 32u : (ty == RLH_TYPE_F16 ? 8u : 1u);
+}
+
+template <uint32_t TY, int NM>
+__device__ __forceinline__ void mv_block_float(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds,
+                                               lfloat* misc, lu64* exp_tab) {
+  constexpr uint32_t S = mv_float_slots(TY);
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
+  const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
+  const uint32_t rows = g.w.rows, row0 = blk * R;
+  const uint32_t nrows = rows - row0 < R ? rows - row0 : R;
+  const uint32_t stride = L.tile_stride;
+  LAct la;
+  la.qs = (RLH_LDS int8_t*)lds;
+  la.d = (RLH_LDS float*)((RLH_LDS int8_t*)lds + nsb * kSbStride);
+  la.s = (RLH_LDS int32_t*)(la.d + nb);
+  la.s16x32 = (RLH_LDS float*)(la.s + nb);
+  la.xf = (RLH_LDS float*)((RLH_LDS int8_t*)lds + L.xf_off);
+  lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
+  float rsd = 0.0f;
+  if (NM == 1 && g.resid && wave == 0) rsd = ld_gf(g.resid + row0 + min(lane, nrows - 1));
+  lfloat* xs = region;
+  lfloat* ws = region + cols;
+  if (NM == 2 && wave == 0) exp_tab_dma(exp_tab);
+  if (L.nx) norm_dma(L, xs, ws);
+  else act_dma(L, la);
+  wait_vmcnt<0>();
+  if (L.nx) norm_finish(L, la, xs, ws, misc);
+  else act_finish(L, la);
+  // the chains: (matrix m, row r, slot s) for every thread in turn
+  const uint32_t nchain = (uint32_t)NM * nrows * S, steps = cols / S;
+  for (uint32_t q = tid; q < nchain; q += NT) {
+    const uint32_t m = q / (nrows * S), r = (q / S) % nrows, s = q % S;
+    const uint8_t* wrow = (m ? g.w2.a : g.w.a) + (size_t)(row0 + r) * g.w.row_bytes;
+    float a = 0.0f;
+#pragma unroll 8
+    for (uint32_t k = 0; k < steps; k++) {
+      const uint32_t e = k * S + s;
+      const float x = la.xf[(e >> 8) * kXfStride + (e & 255)];
+      float w;
+      if constexpr (TY == RLH_TYPE_F32) {
+        w = ld_gf((const float*)wrow + e);
+      } else {
+        const uint32_t h = *(const RLH_GLOBAL uint16_t*)(wrow + 2 * (size_t)e);
+        w = TY == RLH_TYPE_F16 ? f16_to_f32(h) : __uint_as_float(h << 16);
+      }
+      if constexpr (TY == RLH_TYPE_BF16)
+        a = a + w * x;  // acc += w * x: the product rounded, then the add
+      else
+        a = __builtin_fmaf(w, x, a);
+    }
+    region[(m * R + r) * stride + s] = a;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  if (wave < (uint32_t)NM) {
+    const lfloat* sl = region + (wave * R + (lane < nrows ? lane : 0)) * stride;
+    if constexpr (TY == RLH_TYPE_BF16) {
+      acc = sl[0];
+    } else {
+      float A[8];
+#pragma unroll
+      for (int l = 0; l < 8; l++) A[l] = TY == RLH_TYPE_F32 ? (sl[l] + sl[8 + l]) + (sl[16 + l] + sl[24 + l]) : sl[l];
+      acc = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+    }
+  }
+  if (NM == 2) {
+    if (wave == 1) misc[4 + lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    const float x = acc, up = misc[4 + lane];
+    const float h = (x / (1.0f + expf_glibc_t(-x, exp_tab))) * up;  // ops.rs:393-395
+    if (lane < nrows && g.y) ((RLH_GLOBAL float*)g.y)[row0 + lane] = h;
+    q8_quant_wave2(h, g.hq, row0 / 32, nrows > 0, nrows > 32);
+    return;
+  }
+  const bool mine = wave == 0 && lane < nrows;
+  const uint32_t row = row0 + lane;
+  if (mine) {
+    if (g.resid) ((RLH_GLOBAL float*)g.resid)[row] = rsd + acc;
+    if (g.y) ((RLH_GLOBAL float*)g.y)[row] = acc;
+  }
+  if (wave != 0 || !L.has_argmax) return;
+  const bool cand = mine && acc == acc;
+  float bv = cand ? acc : -__int_as_float(0x7f800000);
+  uint32_t bi = cand ? row : 0xffffffffu;
+  wave_argmax(bv, bi);
+  if (lane == 0) {
+    ((RLH_GLOBAL float*)L.am.pv)[blockIdx.x] = bv;
+    ((RLH_GLOBAL uint32_t*)L.am.pi)[blockIdx.x] = bi;
+  }
+}
+
 // The body of one block for weight type TY; NM = 2 in PAIR mode (gate and
 // up share type and tiling).
 template <uint32_t TY, int NM>
 __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc,
                                          lu64* exp_tab) {
+  if constexpr (TY == RLH_TYPE_F16 || TY == RLH_TYPE_F32 || TY == RLH_TYPE_BF16) {
+    mv_block_float<TY, NM>(L, g, blk, lds, misc, exp_tab);
+    return;
+  } else {
   using I = MI<TY>;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nwaves = blockDim.x >> 6;
   const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
@@ -604,6 +786,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     ((RLH_GLOBAL float*)L.am.pv)[blockIdx.x] = bv;
     ((RLH_GLOBAL uint32_t*)L.am.pi)[blockIdx.x] = bi;
   }
+  }  // tiled types
 }
 
 // TY = the weight type of every segment, or 0 for launches that mix types
@@ -631,6 +814,12 @@ __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
       case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       case RLH_TYPE_Q5_K: mv_block<RLH_TYPE_Q5_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q4_1: mv_block<RLH_TYPE_Q4_1, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_0: mv_block<RLH_TYPE_Q5_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_1: mv_block<RLH_TYPE_Q5_1, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_F16: mv_block<RLH_TYPE_F16, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_F32: mv_block<RLH_TYPE_F32, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_BF16: mv_block<RLH_TYPE_BF16, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       default: break;
     }
   }
@@ -646,11 +835,25 @@ MvKernel mv_kernel(uint32_t ty) {
     case RLH_TYPE_Q8_0: return k_mv<RLH_TYPE_Q8_0, NM>;
     case RLH_TYPE_Q4_0: return k_mv<RLH_TYPE_Q4_0, NM>;
     case RLH_TYPE_Q5_K: return k_mv<RLH_TYPE_Q5_K, NM>;
+    case RLH_TYPE_Q4_1: return k_mv<RLH_TYPE_Q4_1, NM>;
+    case RLH_TYPE_Q5_0: return k_mv<RLH_TYPE_Q5_0, NM>;
+    case RLH_TYPE_Q5_1: return k_mv<RLH_TYPE_Q5_1, NM>;
+    case RLH_TYPE_F16: return k_mv<RLH_TYPE_F16, NM>;
+    case RLH_TYPE_F32: return k_mv<RLH_TYPE_F32, NM>;
+    case RLH_TYPE_BF16: return k_mv<RLH_TYPE_BF16, NM>;
     default: return k_mv<0, NM>;
   }
 }
 
 constexpr uint32_t kMaxLds = 150u * 1024u;
+
+// Types whose matvec multiplies the f32 activation (the reference's fused f32
+// path: no integer kernel for them, ops.rs:93-140).
+bool mv_needs_f32(uint32_t ty) {
+  return ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q4_1 || ty == RLH_TYPE_Q5_0 || ty == RLH_TYPE_Q5_1 ||
+         ty == RLH_TYPE_F16 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_BF16;
+}
+bool mv_is_float(uint32_t ty) { return ty == RLH_TYPE_F16 || ty == RLH_TYPE_F32 || ty == RLH_TYPE_BF16; }
 
 // LDS of a plan with R rows per block: the padded Q8 activation row, the
 // padded f32 row when a segment is Q5_K, then the term tiles (which the norm
@@ -662,7 +865,7 @@ uint32_t plan_act_bytes(const MvPlan& p) {
 uint32_t plan_xf_bytes(const MvPlan& p) { return p.L.need_xf ? (p.L.cols / 256) * kXfStride * 4 : 0u; }
 uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   const uint32_t cols = p.L.cols, nsb = cols / 256;
-  const uint32_t stride = nsb * p.max_terms + 4;
+  const uint32_t stride = std::max(nsb * p.max_terms + 4, p.slot_stride);
   const uint32_t tile = nm * R * stride * 4;
   return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? 2 * cols * 4 : 0u);
 }
@@ -738,22 +941,38 @@ bool mv_plan_finish(MvPlan& p) {
   const uint32_t nm = (p.L.nseg == 1 && p.L.seg[0].pair) ? 2u : 1u;
   const uint32_t nsb = p.L.cols / 256;
   if (p.L.nseg == 0 || nsb == 0) return false;
-  const uint32_t tr = p.L.seg[0].w.tr, ntj = p.L.seg[0].w.ntj;
-  for (uint32_t s = 0; s < p.L.nseg; s++)
-    if (p.L.seg[s].w.tr != tr || p.L.seg[s].w.cols != p.L.cols || !is_tiled(p.L.seg[s].w.ty)) return false;
+  // tiled segments share one tile shape (equal row lengths give equal
+  // shapes); float segments (rows as stored) may sit beside them, and then
+  // every block takes 64 rows (a whole number of tiles of any shape)
+  bool fl = false;
+  uint32_t tr = 0, ntj = 1, slots = 0;
+  for (uint32_t s = 0; s < p.L.nseg; s++) {
+    const DevMat& w = p.L.seg[s].w;
+    if (w.cols != p.L.cols) return false;
+    if (mv_is_float(w.ty)) {
+      fl = true;
+      slots = std::max(slots, mv_float_slots(w.ty));
+    } else {
+      if (!is_tiled(w.ty) || (tr != 0 && w.tr != tr)) return false;
+      tr = w.tr;
+      ntj = w.ntj;
+    }
+  }
+  if (tr == 0) tr = 64;  // float segments only
   if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows ||
                   p.L.seg[0].w.rows % 32 != 0))
     return false;
   // the epilogue runs one row per lane: R <= 64
-  const uint32_t R = nm == 2 ? 64u : std::min<uint32_t>(p.norm && !p.quant ? 2 * tr : tr, 64);
+  const uint32_t R = nm == 2 || fl ? 64u : std::min<uint32_t>(p.norm && !p.quant ? 2 * tr : tr, 64);
   p.L.need_xf = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++)
-    if (p.L.seg[s].w.ty == RLH_TYPE_Q5_K || (p.L.seg[s].pair && p.L.seg[s].w2.ty == RLH_TYPE_Q5_K)) p.L.need_xf = 1;
-  if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // Q5_K needs the f32 activation
+    if (mv_needs_f32(p.L.seg[s].w.ty) || (p.L.seg[s].pair && mv_needs_f32(p.L.seg[s].w2.ty))) p.L.need_xf = 1;
+  if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // f32 products need the f32 activation
+  p.slot_stride = slots + 1;  // float plans: a row's chain results
   if (plan_lds(p, R, nm) > kMaxLds) return false;
   if (p.norm && (p.L.cols > (p.quant ? kMvMaxQuantCols : kMvMaxNormCols) || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
-  p.L.tile_stride = nsb * p.max_terms + 4;
+  p.L.tile_stride = std::max(nsb * p.max_terms + 4, p.slot_stride);
   p.L.xf_off = plan_act_bytes(p);
   p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
   p.lds = plan_lds(p, R, nm);
@@ -761,7 +980,7 @@ bool mv_plan_finish(MvPlan& p) {
   // a quantize prologue is VALU work on the whole row in every block: all
   // eight waves take part even where fewer carry tiles (measured 6.3 -> 5.8
   // us for the 8B attn_output)
-  p.waves = p.quant ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
+  p.waves = p.quant || fl ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;
@@ -799,7 +1018,9 @@ void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start, hipEvent_t 
 }
 
 bool mv_set_max_lds(size_t bytes) {
-  const uint32_t tys[] = {0, RLH_TYPE_Q4_K, RLH_TYPE_Q6_K, RLH_TYPE_Q8_0, RLH_TYPE_Q4_0, RLH_TYPE_Q5_K};
+  const uint32_t tys[] = {0,           RLH_TYPE_Q4_K, RLH_TYPE_Q6_K, RLH_TYPE_Q8_0, RLH_TYPE_Q4_0,
+                          RLH_TYPE_Q5_K, RLH_TYPE_Q4_1, RLH_TYPE_Q5_0, RLH_TYPE_Q5_1, RLH_TYPE_F16,
+                          RLH_TYPE_F32,  RLH_TYPE_BF16};
   for (uint32_t ty : tys) {
     const void* fns[] = {(const void*)mv_kernel<1>(ty), (const void*)mv_kernel<2>(ty)};
     for (const void* f : fns)

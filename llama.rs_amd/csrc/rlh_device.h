@@ -498,6 +498,22 @@ __device__ __forceinline__ float dq_elem(const DevMat& w, uint32_t row, uint32_t
       const float x = (float)((int)(t < 16 ? (byte & 0xF) : (byte >> 4)) - 8);
       return x * d;
     }
+    case RLH_TYPE_Q4_1:  // quant.rs:222-236: q * d + m
+    case RLH_TYPE_Q5_0:  // quant.rs:237-254: (q5 - 16) * d
+    case RLH_TYPE_Q5_1: {  // quant.rs:255-272: q5 * d + m
+      const uint32_t k = p >> 5, t = p & 31;
+      const uint32_t byte = item_u8(w, row, j, k * 16 + (t & 15));
+      uint32_t q = t < 16 ? (byte & 0xF) : (byte >> 4);
+      const uint32_t sc0 = w.ty == RLH_TYPE_Q4_1 ? 128 : 160;  // the scales follow the quants (and qh)
+      if (w.ty != RLH_TYPE_Q4_1) {
+        const uint32_t qh = item_u16(w, row, j, 128 + 4 * k) | (item_u16(w, row, j, 130 + 4 * k) << 16);
+        q |= ((qh >> t) & 1) << 4;  // bit t of qh is the 5th bit of value t
+      }
+      if (w.ty == RLH_TYPE_Q5_0) return (float)((int)q - 16) * f16_to_f32(item_u16(w, row, j, sc0 + 2 * k));
+      const float d = f16_to_f32(item_u16(w, row, j, sc0 + 4 * k));
+      const float m = f16_to_f32(item_u16(w, row, j, sc0 + 4 * k + 2));
+      return (float)q * d + m;
+    }
     case RLH_TYPE_F32:
       return ((const float*)(w.a + (size_t)row * w.row_bytes))[i];
     case RLH_TYPE_F16: {

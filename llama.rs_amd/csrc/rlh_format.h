@@ -2,12 +2,16 @@
 //
 // The bytes are the ggml block bytes of the reference (src/quant.rs:10-106);
 // only their placement in HBM differs. Quantized matrices (Q4_K, Q6_K, Q8_0,
-// Q4_0, Q5_K) are cut into items, one per 256 values of a row:
+// Q4_0, Q5_K, Q4_1, Q5_0, Q5_1) are cut into items, one per 256 values of a
+// row:
 //   Q4_K  item = the 144-byte super-block as is;
 //   Q5_K  item = the 176-byte super-block as is (d, dmin, scales[12], qh[32], qs[128]);
 //   Q6_K  item = the 210-byte super-block as is (ql[128], qh[64], scales[16], d);
 //   Q8_0  item = 8 consecutive blocks: their 8 x 32 quants, then their 8 f16 d;
-//   Q4_0  item = 8 consecutive blocks: their 8 x 16 quant bytes, then 8 f16 d.
+//   Q4_0  item = 8 consecutive blocks: their 8 x 16 quant bytes, then 8 f16 d;
+//   Q4_1  item = 8 blocks: 8 x 16 quant bytes, then 8 (f16 d, f16 m) pairs (160 B);
+//   Q5_0  item = 8 blocks: 8 x 16 quant bytes, 8 u32 qh, 8 f16 d (176 B);
+//   Q5_1  item = 8 blocks: 8 x 16 quant bytes, 8 u32 qh, 8 (d, m) pairs (192 B).
 // Items are grouped in tiles of TR rows x TJ items (TR * TJ = 64); lane
 // l = (j % TJ) * TR + (r % TR) of a wave owns item (r, j). Inside a tile the
 // k-th 16-byte chunk of lane l's item sits at k * 1024 + l * 16, so one
@@ -40,10 +44,18 @@ struct DevMat {
 
 __host__ __device__ inline bool is_tiled(uint32_t ty) {
   return ty == RLH_TYPE_Q4_K || ty == RLH_TYPE_Q6_K || ty == RLH_TYPE_Q8_0 || ty == RLH_TYPE_Q4_0 ||
-         ty == RLH_TYPE_Q5_K;
+         ty == RLH_TYPE_Q5_K || ty == RLH_TYPE_Q4_1 || ty == RLH_TYPE_Q5_0 || ty == RLH_TYPE_Q5_1;
 }
 __host__ __device__ inline uint32_t item_bytes(uint32_t ty) {
-  return ty == RLH_TYPE_Q6_K ? 210u : (ty == RLH_TYPE_Q8_0 ? 272u : (ty == RLH_TYPE_Q5_K ? 176u : 144u));
+  switch (ty) {
+    case RLH_TYPE_Q6_K: return 210u;
+    case RLH_TYPE_Q8_0: return 272u;
+    case RLH_TYPE_Q5_K: return 176u;
+    case RLH_TYPE_Q4_1: return 160u;
+    case RLH_TYPE_Q5_0: return 176u;
+    case RLH_TYPE_Q5_1: return 192u;
+    default: return 144u;  // Q4_K, Q4_0
+  }
 }
 // Items per row must be a multiple of the tile width.
 __host__ __device__ inline uint32_t tile_width(uint32_t items_per_row) {

@@ -104,6 +104,52 @@ void quant_q4_0(const float* x, size_t n, uint8_t* out) {
   }
 }
 
+// Q4_1 / Q5_1: q = round((x - m) / d) with the stored f16 d and m; Q5_0:
+// q = round(x / d) + 16. The fifth bit of value t of a block is bit t of the
+// block's little-endian qh word (quant.rs Q5_0/Q5_1 arms).
+float f16_round(float v) { return f16_to_f32(f32_to_f16(v)); }
+
+template <int BITS, bool MIN>
+void quant_q_lin(const float* x, size_t n, uint8_t* out) {
+  constexpr int qmax = (1 << BITS) - 1;
+  constexpr size_t ts = 2 + (MIN ? 2 : 0) + (BITS == 5 ? 4 : 0) + 16;
+  for (size_t b = 0; b < n / 32; b++) {
+    const float* xb = x + b * 32;
+    uint8_t* o = out + b * ts;
+    float lo = xb[0], hi = xb[0], amax = 0.f;
+    for (int i = 0; i < 32; i++) {
+      lo = std::fmin(lo, xb[i]);
+      hi = std::fmax(hi, xb[i]);
+      amax = std::fmax(amax, std::fabs(xb[i]));
+    }
+    const float dv = MIN ? (hi - lo) / (float)qmax : amax / (float)(qmax / 2);
+    put_f16(o, dv);
+    const float d = f16_round(dv), id = d > 0.f ? 1.f / d : 0.f;
+    const float m = MIN ? f16_round(lo) : 0.f;
+    if (MIN) put_f16(o + 2, lo);
+    uint8_t* qs = o + ts - 16;
+    uint32_t qh = 0;
+    int q[32];
+    for (int i = 0; i < 32; i++) {
+      const int v = MIN ? (int)std::lrint((xb[i] - m) * id) : (int)std::lrint(xb[i] * id) + (qmax + 1) / 2;
+      q[i] = clampi(v, 0, qmax);
+      if (BITS == 5) qh |= (uint32_t)(q[i] >> 4) << i;
+    }
+    for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+    if (BITS == 5) std::memcpy(o + ts - 20, &qh, 4);
+  }
+}
+
+// BF16: the upper half of the f32 bits, rounded to nearest even.
+void put_bf16(uint8_t* p, float v) {
+  uint32_t x;
+  std::memcpy(&x, &v, 4);
+  const uint16_t h = (x & 0x7fffffffu) > 0x7f800000u ? (uint16_t)((x >> 16) | 0x40u)
+                                                      : (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+  p[0] = (uint8_t)(h & 0xff);
+  p[1] = (uint8_t)(h >> 8);
+}
+
 // Q4_K: 8 sub-blocks of 32 with a 6-bit scale and a 6-bit min each, packed as
 // get_scale_min_k4 (quant.rs:176-185) unpacks them.
 void quant_q4_k(const float* x, size_t n, uint8_t* out) {
@@ -293,6 +339,12 @@ int rlh_quantize_row(uint32_t ty, const float* src, uint64_t n, void* dst) {
     case RLH_TYPE_F16:
       for (uint64_t i = 0; i < n; i++) put_f16(o + 2 * i, src[i]);
       return 0;
+    case RLH_TYPE_BF16:
+      for (uint64_t i = 0; i < n; i++) put_bf16(o + 2 * i, src[i]);
+      return 0;
+    case RLH_TYPE_Q4_1: if (n % 32) return -1; quant_q_lin<4, true>(src, n, o); return 0;
+    case RLH_TYPE_Q5_0: if (n % 32) return -1; quant_q_lin<5, false>(src, n, o); return 0;
+    case RLH_TYPE_Q5_1: if (n % 32) return -1; quant_q_lin<5, true>(src, n, o); return 0;
     case RLH_TYPE_Q8_0: if (n % 32) return -1; quant_q8_0(src, n, o); return 0;
     case RLH_TYPE_Q4_0: if (n % 32) return -1; quant_q4_0(src, n, o); return 0;
     case RLH_TYPE_Q4_K: if (n % 256) return -1; quant_q4_k(src, n, o); return 0;

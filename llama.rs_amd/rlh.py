@@ -138,6 +138,19 @@ SPECS = {
     "small-q4km": ModelSpec("small-q4km", 4, 1024, 3072, 16, 8, 4096, False, _q4km(False, Q4_K, Q6_K), n_ctx=1024),
     # Q5_K matrices (no integer path in the reference: f32 products)
     "tiny-q5km": ModelSpec("tiny-q5km", 2, 256, 512, 4, 2, 1000, True, _q5km(), n_ctx=512),
+    # the remaining weight types: 32-value blocks with a min and/or a fifth
+    # bit (no integer path in the reference) and float rows
+    "tiny-q4_1": ModelSpec("tiny-q4_1", 2, 256, 512, 4, 2, 1000, True, _all(Q4_1), n_ctx=512),
+    "tiny-q5_0": ModelSpec("tiny-q5_0", 2, 256, 512, 4, 2, 1000, False, _all(Q5_0, tied=False), n_ctx=512),
+    "tiny-q5_1": ModelSpec("tiny-q5_1", 2, 256, 512, 4, 2, 1000, True, _all(Q5_1), n_ctx=512),
+    "tiny-f16": ModelSpec("tiny-f16", 2, 256, 512, 4, 2, 1000, True, _all(F16), n_ctx=512),
+    "tiny-bf16": ModelSpec("tiny-bf16", 2, 256, 512, 4, 2, 1000, False, _all(BF16, tied=False), n_ctx=512),
+    "tiny-f32": ModelSpec("tiny-f32", 2, 256, 512, 4, 2, 1000, True, _all(F32), n_ctx=512),
+    # one launch mixing float and tiled rows (q/k/v), ffn_gate and ffn_up of
+    # different types (separate launches + silu(g)*u), eight types in all
+    "tiny-mix": ModelSpec("tiny-mix", 2, 256, 512, 4, 2, 1000, False,
+                          {T_ATTN_Q: F16, T_ATTN_K: Q8_0, T_ATTN_V: Q5_1, T_ATTN_OUTPUT: BF16, T_FFN_GATE: Q4_1,
+                           T_FFN_UP: Q5_0, T_FFN_DOWN: F32, T_TOKEN_EMBD: Q4_0, T_OUTPUT: Q5_K}, n_ctx=512),
     # 8 query heads per KV head (the 32B grouping) and a long context window
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
     # 4 query heads per KV head (the 4B / 8B grouping) and a long context window

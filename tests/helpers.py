@@ -1,7 +1,7 @@
 """Shared input generators for the parity tests."""
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, Q5_K, Q6_K = 2, 8, 12, 13, 14
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
 BLOCK = {2: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24), 8: (32, 34), 12: (256, 144), 13: (256, 176),
          14: (256, 210), 0: (1, 4), 1: (1, 2), 30: (1, 2)}
 
@@ -35,7 +35,19 @@ def random_blocks(ty, nblocks, rng, scale_lo=0.01, scale_hi=1.0):
         raw[:, col + 1] = (h >> 8).astype(np.uint8)
 
     n = nblocks
-    if ty in (Q4_K, Q5_K):
+    if ty in (0, 1, 30):  # float rows: N(0, 1) values, rounded to the type
+        v = rng.standard_normal(nblocks).astype(np.float32)
+        if ty == 0:
+            return v.view(np.uint8).copy()
+        if ty == 1:
+            return v.astype(np.float16).view(np.uint8).copy()
+        return (v.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8).copy()
+    if ty in (3, 7):  # Q4_1 / Q5_1: d and m
+        put(0, rng.uniform(scale_lo, scale_hi, n) / 16)
+        put(2, rng.uniform(-scale_hi, scale_hi, n))
+    elif ty == 6:  # Q5_0
+        put(0, rng.uniform(scale_lo, scale_hi, n) / 16)
+    elif ty in (Q4_K, Q5_K):
         put(0, rng.uniform(scale_lo, scale_hi, n) / 64)
         put(2, rng.uniform(scale_lo, scale_hi, n) / 64)
     elif ty == Q6_K:
