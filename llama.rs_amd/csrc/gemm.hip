@@ -17,9 +17,9 @@
 //
 // Tiling: a block owns 64 tokens x 64 rows; 4 waves of 32 x 32, each 2 x 2
 // MFMA tiles of 16 x 16. Per super-block (256 values) the block stages the
-// 64 tokens' Q8 bytes and block scales into LDS with global_load_lds (double
-// buffered); every lane loads the weight bytes of its row straight from the
-// tiled layout, one super-block ahead. Block b runs on XCD b % 8; the blocks
+// 64 tokens' Q8 bytes and block scales into LDS (double buffered, copied
+// through registers); every lane loads the weight bytes of its row straight
+// from the tiled layout, one super-block ahead. Block b runs on XCD b % 8; the blocks
 // of one XCD walk the token tiles of a row tile first, so each weight tile
 // is fetched into that XCD's L2 once and reused by all token tiles.
 #include <hip/hip_runtime.h>
@@ -414,29 +414,60 @@ struct GT<RLH_TYPE_Q4_0> {
 };
 
 // Stages super-block j of the block's 64 tokens: Q8 bytes into the padded
-// [64][272] layout (17 slots of 16 bytes per token, the 17th masked), the 8
-// block scales and (Q4_K) the 8 block sums per token. One copy instruction
-// fills 64 consecutive 16-byte slots; each lane picks the source of its slot.
-__device__ __forceinline__ void stage(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf, bool need_s) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// [64][272] layout (17 slots of 16 bytes per token, the 17th unused), the 8
+// block scales and (Q4_K) the 8 block sums per token. Slot p of the staged
+// super-block is thread p % 256's job p / 256. The copy goes through
+// registers: stage_load issues the global loads at the top of a super-block
+// step and stage_store writes them to LDS at its end, so their latency hides
+// behind the step's products. (Copies straight into LDS, global_load_lds,
+// measured ~0.5 us per instruction per wave here: the step's copies took as
+// long as its products.) Slots past the valid tokens or the 17th slot of a
+// token load a clamped, valid address and are not stored.
+constexpr uint32_t kStageJobs = 6;  // ceil((64 * 17 + 2 * 64 * 2) / 256)
+
+struct StageRegs {
+  u32x4_t v[kStageJobs];
+  const uint8_t* src[kStageJobs];  // job k's source for the current super-block
+  uint32_t keep;                   // bit k: job k is stored
+  uint32_t small;                  // bit k: job k is a scale or sum slot (32-byte step per super-block)
+};
+
+// Sources of super-block 0; super-block j + 1 is 256 bytes further for Q8
+// bytes and 32 bytes for scales and sums.
+__device__ __forceinline__ void stage_init(StageRegs& r, const GemmArgs& a, uint32_t t0, bool need_s) {
   const uint32_t cols = a.w.cols, nb = cols / 32;
-  const uint32_t nx = kTile * 17, nd = kTile * 2;
-  const uint32_t total = nx + nd + (need_s ? nd : 0);
-  for (uint32_t s0 = wave * 64; s0 < total; s0 += 4 * 64) {
-    const uint32_t p = s0 + lane;
-    const uint8_t* src = nullptr;
-    if (p < nx) {
-      const uint32_t tok = p / 17, ch = p - tok * 17;
-      if (ch < 16 && t0 + tok < a.n) src = (const uint8_t*)a.x.qs + (size_t)(t0 + tok) * cols + 256 * j + 16 * ch;
-    } else if (p < nx + nd) {
-      const uint32_t r = p - nx, tok = r >> 1;
-      if (t0 + tok < a.n) src = (const uint8_t*)(a.x.d + (size_t)(t0 + tok) * nb + 8 * j + 4 * (r & 1));
-    } else if (p < total) {
-      const uint32_t r = p - nx - nd, tok = r >> 1;
-      if (t0 + tok < a.n) src = (const uint8_t*)(a.x.s + (size_t)(t0 + tok) * nb + 8 * j + 4 * (r & 1));
+  const uint32_t nx = kTile * 17, nd = kTile * 2, total = nx + nd + (need_s ? nd : 0);
+  r.keep = 0;
+  r.small = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < kStageJobs; k++) {
+    const uint32_t p = threadIdx.x + 256 * k, pc = p < total ? p : total - 1;
+    if (pc < nx) {
+      const uint32_t tok = pc / 17, ch = pc - tok * 17;
+      r.keep |= (p < total && ch < 16 && t0 + tok < a.n) ? 1u << k : 0u;
+      r.src[k] = (const uint8_t*)a.x.qs + (size_t)min(t0 + tok, a.n - 1) * cols + 16 * min(ch, 15u);
+    } else {
+      const uint32_t r0 = pc - (pc < nx + nd ? nx : nx + nd), tok = r0 >> 1;
+      r.keep |= (p < total && t0 + tok < a.n) ? 1u << k : 0u;
+      r.small |= 1u << k;
+      const uint8_t* base = pc < nx + nd ? (const uint8_t*)a.x.d : (const uint8_t*)a.x.s;
+      r.src[k] = base + ((size_t)min(t0 + tok, a.n - 1) * nb + 4 * (r0 & 1)) * 4;
     }
-    if (src) __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)src, (RLH_LDS void*)(buf + s0 * 16), 16, 0, 0);
   }
+}
+
+__device__ __forceinline__ void stage_load(StageRegs& r) {
+#pragma unroll
+  for (uint32_t k = 0; k < kStageJobs; k++) {
+    r.v[k] = *(const RLH_GLOBAL u32x4_t*)r.src[k];
+    r.src[k] += (r.small >> k & 1u) ? 32 : 256;
+  }
+}
+
+__device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf) {
+#pragma unroll
+  for (uint32_t k = 0; k < kStageJobs; k++)
+    if (r.keep >> k & 1u) *(RLH_LDS u32x4_t*)(buf + (threadIdx.x + 256 * k) * 16) = r.v[k];
 }
 
 template <uint32_t TY>
@@ -467,15 +498,17 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
       for (int e = 0; e < 4; e++) acc[tr][tc][e] = 0.0f;
 
   typename G::W wc[2], wn[2];
+  StageRegs sr;
 #pragma unroll
   for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
-  stage(a, t0, 0, lds, G::kNeedS);
-  __builtin_amdgcn_s_waitcnt(0);
+  stage_init(sr, a, t0, G::kNeedS);
+  stage_load(sr);
+  stage_store(sr, lds);
   __syncthreads();
   for (uint32_t j = 0; j < nsb; j++) {
     const bool more = j + 1 < nsb;
     if (more) {
-      stage(a, t0, j + 1, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS);
+      stage_load(sr);
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) G::load(wn[tc], a.w, rowc[tc], j + 1, ln.q);
     }
@@ -483,9 +516,9 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
     if (more) {
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) wc[tc] = wn[tc];
+      stage_store(sr, lds + ((j + 1) & 1) * kStageBytes);  // that buffer was freed by the last barrier
     }
-    __builtin_amdgcn_s_waitcnt(0);  // next stage landed in this wave
-    __syncthreads();                // ... and in every wave; current buffer free
+    __syncthreads();  // the next stage is in LDS; the current buffer is free
   }
 #pragma unroll
   for (int tr = 0; tr < 2; tr++)
