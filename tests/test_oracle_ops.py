@@ -162,7 +162,12 @@ def test_batch_int_equals_sequential_int_matmul(ty):
         assert np.array_equal(bits(b[k * rows:(k + 1) * rows]), bits(y))
 
 
-@pytest.mark.parametrize("ty,mode", [(12, 1), (14, 1), (8, 1), (13, 1), (13, 0)])
+def _block_size(ty):
+    return 256 if ty in (12, 13, 14) else (1 if ty in (0, 1, 30) else 32)
+
+
+@pytest.mark.parametrize("ty,mode", [(12, 1), (14, 1), (8, 1), (13, 1), (13, 0), (3, 0), (6, 0), (7, 0), (1, 0),
+                                     (30, 0), (0, 0)])
 def test_no_int_matmul_against_f64(ty, mode):
     """ops.rs:131-140 fused f32 path (RUST_LLAMA_NO_INT, and the default
     mode for Q5_K, which has no integer kernel: ops.rs:93-128 skips it):
@@ -171,8 +176,7 @@ def test_no_int_matmul_against_f64(ty, mode):
     (quant.rs:528-539)."""
     rng = np.random.default_rng(3 + ty + 17 * mode)
     rows, cols = 8, 1024
-    bs = 256 if ty in (12, 13, 14) else 32
-    w = random_blocks(ty, rows * cols // bs, rng)
+    w = random_blocks(ty, rows * cols // _block_size(ty), rng)
     x = rng.standard_normal(cols).astype(F32)
     y = oracle.matmul(ty, w, rows, cols, x, mode)
     wd = gf.dequant(ty, w, rows * cols).astype(np.float64).reshape(rows, cols)
@@ -203,15 +207,57 @@ def test_q5k_fused_dot_is_blockwise_dequant_then_dot():
         assert bits(y)[0] == bits(np.array([acc], F32))[0], trial
 
 
-@pytest.mark.parametrize("ty", [13, 12, 14])
+@pytest.mark.parametrize("ty", [3, 6, 7])
+def test_small_block_fused_dot_is_blockwise_dequant_then_dot(ty):
+    """Q4_1/Q5_0/Q5_1 have no AVX2 kernel in the reference: dequant_dot takes
+    the generic fallback (quant.rs:528-539), one 32-value block dequantized
+    and ops::dot(block, x) added to the row total in block order. Rebuilt
+    from the independent numpy decoder and ops::dot it matches bit for bit
+    (a dropped fifth bit or min, a wrong nibble order or another
+    accumulation order fails here)."""
+    lib = oracle.load()
+    rng = np.random.default_rng(57 + ty)
+    cols = 512
+    for trial in range(3):
+        w = random_blocks(ty, cols // 32, rng)
+        x = rng.standard_normal(cols).astype(F32)
+        wd = gf.dequant(ty, w, cols).astype(F32)
+        y = oracle.matmul(ty, w, 1, cols, x, oracle.MODE_DEFAULT)
+        acc = F32(0.0)
+        for b in range(cols // 32):
+            wb = np.ascontiguousarray(wd[b * 32:(b + 1) * 32])
+            xb = np.ascontiguousarray(x[b * 32:(b + 1) * 32])
+            acc = F32(acc + F32(lib.orc_dot(P(wb), P(xb), 32)))
+        assert bits(y)[0] == bits(np.array([acc], F32))[0], trial
+
+
+def test_bf16_dot_is_the_scalar_chain():
+    """BF16 weights take dequant_dot_scalar (quant.rs:426-433): acc += w * x
+    in index order, the product rounded before the add; restated here with
+    numpy float32 steps on the numpy decoder's values."""
+    rng = np.random.default_rng(31)
+    cols = 512
+    for trial in range(3):
+        w = random_blocks(30, cols, rng)
+        x = rng.standard_normal(cols).astype(F32)
+        wd = gf.dequant(30, w, cols).astype(F32)
+        y = oracle.matmul(30, w, 1, cols, x, oracle.MODE_DEFAULT)
+        acc = F32(0.0)
+        for i in range(cols):
+            acc = F32(acc + F32(wd[i] * x[i]))
+        assert bits(y)[0] == bits(np.array([acc], F32))[0], trial
+
+
+@pytest.mark.parametrize("ty", [13, 12, 14, 3, 6, 7, 1, 30, 0])
 def test_default_matmul_batch_against_f64(ty):
     """matmul_batch's default route (ops.rs:237-312: dequantize three rows,
     dot_multi_rows over groups of four tokens; Q5_K always takes it, also
-    with RUST_LLAMA_BATCH_INT): close to the f64 products of the numpy
-    decoder's weights, with a ragged token tail (n % 4 = 3)."""
+    with RUST_LLAMA_BATCH_INT; F32 tensors take ops::dot per token,
+    ops.rs:167-175): close to the f64 products of the numpy decoder's
+    weights, with a ragged token tail (n % 4 = 3)."""
     rng = np.random.default_rng(70 + ty)
     rows, cols, n = 7, 512, 7
-    w = random_blocks(ty, rows * cols // 256, rng)
+    w = random_blocks(ty, rows * cols // _block_size(ty), rng)
     xs = rng.standard_normal(n * cols).astype(F32)
     wd = gf.dequant(ty, w, rows * cols).astype(np.float64).reshape(rows, cols)
     modes = (oracle.MODE_DEFAULT, oracle.MODE_BATCH_INT) if ty == 13 else (oracle.MODE_DEFAULT,)
