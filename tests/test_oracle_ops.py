@@ -218,9 +218,9 @@ def test_small_block_fused_dot_is_blockwise_dequant_then_dot(ty):
     lib = oracle.load()
     rng = np.random.default_rng(57 + ty)
     cols = 512
-    for trial in range(3):
+    for trial in range(8):
         w = random_blocks(ty, cols // 32, rng)
-        x = rng.standard_normal(cols).astype(F32)
+        x = _wide(rng, cols)
         wd = gf.dequant(ty, w, cols).astype(F32)
         y = oracle.matmul(ty, w, 1, cols, x, oracle.MODE_DEFAULT)
         acc = F32(0.0)
@@ -237,15 +237,71 @@ def test_bf16_dot_is_the_scalar_chain():
     numpy float32 steps on the numpy decoder's values."""
     rng = np.random.default_rng(31)
     cols = 512
-    for trial in range(3):
+    for trial in range(8):
         w = random_blocks(30, cols, rng)
-        x = rng.standard_normal(cols).astype(F32)
+        x = _wide(rng, cols)
         wd = gf.dequant(30, w, cols).astype(F32)
         y = oracle.matmul(30, w, 1, cols, x, oracle.MODE_DEFAULT)
         acc = F32(0.0)
         for i in range(cols):
             acc = F32(acc + F32(wd[i] * x[i]))
         assert bits(y)[0] == bits(np.array([acc], F32))[0], trial
+
+
+def _fma32(a, b, c):
+    """f32 fused multiply-add: the product of two f32 values is exact in f64
+    and the f64 sum is rounded once more to f32 (a double rounding that can
+    only differ from the single one on an exact f32 tie, which these
+    continuous random inputs do not produce)."""
+    return F32(np.float64(a) * np.float64(b) + np.float64(c))
+
+
+def _wide(rng, n):
+    """N(0, 1) values scaled by 2^-8 .. 2^8: partial sums of very different
+    magnitudes, so that a different summation order or rounding step changes
+    the result in most trials."""
+    return (rng.standard_normal(n) * np.exp2(rng.integers(-8, 9, n))).astype(F32)
+
+
+def _tree8(A):
+    return F32(F32(F32(A[0] + A[4]) + F32(A[2] + A[6])) + F32(F32(A[1] + A[5]) + F32(A[3] + A[7])))
+
+
+def test_f16_dot_is_eight_fma_chains():
+    """F16 weights take the AVX2 f16 kernel (simd.rs:401-419): eight FMA
+    chains, lane l over elements 8i + l, then the hsum tree (simd.rs:261-272).
+    Restated with f64-emulated FMA on the numpy decoder's values."""
+    rng = np.random.default_rng(32)
+    cols = 256
+    for trial in range(8):
+        w = random_blocks(1, cols, rng)
+        x = _wide(rng, cols)
+        wd = gf.dequant(1, w, cols).astype(F32)
+        y = oracle.matmul(1, w, 1, cols, x, oracle.MODE_DEFAULT)
+        A = [F32(0.0)] * 8
+        for i in range(0, cols, 8):
+            for l in range(8):
+                A[l] = _fma32(wd[i + l], x[i + l], A[l])
+        assert bits(y)[0] == bits(np.array([_tree8(A)], F32))[0], trial
+
+
+def test_f32_weights_dot_is_dot_f32_avx2():
+    """F32 tensors take ops::dot per row (ops.rs:77-83), dot_f32_avx2
+    (simd.rs:328-377): 32 FMA chains, chain (m, l) over elements 32c + 8m + l,
+    then (a0 + a1) + (a2 + a3) per lane and the hsum tree."""
+    rng = np.random.default_rng(33)
+    cols = 256
+    for trial in range(8):
+        w = rng.standard_normal(cols).astype(F32)
+        x = _wide(rng, cols)
+        y = oracle.matmul(0, w.view(np.uint8), 1, cols, x, oracle.MODE_DEFAULT)
+        acc = [[F32(0.0)] * 8 for _ in range(4)]
+        for c in range(0, cols, 32):
+            for m in range(4):
+                for l in range(8):
+                    acc[m][l] = _fma32(w[c + 8 * m + l], x[c + 8 * m + l], acc[m][l])
+        A = [F32(F32(acc[0][l] + acc[1][l]) + F32(acc[2][l] + acc[3][l])) for l in range(8)]
+        assert bits(y)[0] == bits(np.array([_tree8(A)], F32))[0], trial
 
 
 @pytest.mark.parametrize("ty", [13, 12, 14, 3, 6, 7, 1, 30, 0])
