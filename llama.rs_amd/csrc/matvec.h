@@ -66,6 +66,7 @@ struct MvPlan {
   uint32_t waves = 0;  // waves per block
   uint32_t max_terms = 0;
   uint32_t slot_stride = 0;  // float plans: floats per row of chain results
+  uint32_t float_stage = 0;  // float plans: LDS bytes of the row stage buffers
   uint32_t rows = 0;   // rows over all segments
   bool norm = false;   // activation from the norm prologue
   bool quant = false;  // ... without the norm (quantize_q8 of the f32 row only)

@@ -535,23 +535,41 @@ __device__ __forceinline__ void wave_argmax(float& bv, uint32_t& bi) {
 // FMA chains, lane l taking values 8i + l, then the AVX2 tree; F32 weights
 // (ops.rs:77-83, dot_f32_avx2 simd.rs:328-377) 32 FMA chains, chain (m, l)
 // taking 32c + 8m + l, then (a0+a1)+(a2+a3) and the tree; BF16
-// (quant.rs:427-433) one chain acc += w * x in index order. Each thread of
-// the block runs whole chains (a row's slot) over the f32 activation in LDS;
-// lane r of wave m then reduces row r's slots, and the epilogue is the
-// tiled path's.
+// (quant.rs:427-433) one chain acc += w * x in index order.
+// A block owns R rows (16, 32 in PAIR mode, 64 beside tiled segments). The
+// rows stream through LDS in stages of 32 KB per matrix (16 KB in PAIR mode;
+// a stage holds 1/R of it from each row), double buffered: every thread
+// loads its 16-byte pieces of the next stage into registers while the chains
+// run over the current one, and stores them after it. F16 and F32 chains are (matrix,
+// row, slot) triples spread over the block's threads, carried in registers
+// across stages; BF16 chains (one per row) read eight values per LDS read.
+// Lane r of wave m then reduces row r's slots; the epilogue is the tiled
+// path's.
 __host__ __device__ constexpr uint32_t mv_float_slots(uint32_t ty) {
   return ty == RLH_TYPE_F32 ? 32u : (ty == RLH_TYPE_F16 ? 8u : 1u);
+}
+// bytes per matrix per stage: 32 KB (16 KB in PAIR mode, two matrices)
+__host__ __device__ constexpr uint32_t mv_float_stage(uint32_t nm) { return nm == 2 ? 16384u : 32768u; }
+__host__ __device__ constexpr uint32_t mv_float_stage_bytes(uint32_t nm, uint32_t R) {
+  return nm * 2u * R * (mv_float_stage(nm) / R + 16);  // rows padded by 16 bytes
 }
 
 template <uint32_t TY, int NM>
 __device__ __forceinline__ void mv_block_float(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds,
                                                lfloat* misc, lu64* exp_tab) {
   constexpr uint32_t S = mv_float_slots(TY);
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
+  constexpr uint32_t ES = TY == RLH_TYPE_F32 ? 4u : 2u;
+  constexpr uint32_t kPer = (NM * 64u * S + 511u) / 512u;  // chains per thread at most (R <= 64)
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t R = L.rows_per_blk, cols = L.cols, nsb = cols >> 8, nb = cols >> 5;
   const uint32_t rows = g.w.rows, row0 = blk * R;
   const uint32_t nrows = rows - row0 < R ? rows - row0 : R;
   const uint32_t stride = L.tile_stride;
+  constexpr uint32_t kJ = mv_float_stage(NM) / 8192u;   // 16-byte pieces per thread per matrix
+  const uint32_t RY = mv_float_stage(NM) / R, RS = RY + 16;  // row bytes per stage, LDS row stride
+  const uint32_t C = RY / ES;                           // values per row per stage
+  const uint32_t PR = RY / 16;                          // 16-byte pieces per row per stage
+  const uint32_t bufb = NM * R * RS;                    // bytes of one stage buffer
   LAct la;
   la.qs = (RLH_LDS int8_t*)lds;
   la.d = (RLH_LDS float*)((RLH_LDS int8_t*)lds + nsb * kSbStride);
@@ -559,6 +577,9 @@ __device__ __forceinline__ void mv_block_float(const MvLaunch& L, const MvSeg& g
   la.s16x32 = (RLH_LDS float*)(la.s + nb);
   la.xf = (RLH_LDS float*)((RLH_LDS int8_t*)lds + L.xf_off);
   lfloat* region = (lfloat*)((RLH_LDS int8_t*)lds + L.region_off);
+  // stage buffers after the chain results (the norm prologue's row copies
+  // overlap them; the first stage is stored after the prologue)
+  RLH_LDS uint8_t* stg = (RLH_LDS uint8_t*)(region + NM * R * stride);
   float rsd = 0.0f;
   if (NM == 1 && g.resid && wave == 0) rsd = ld_gf(g.resid + row0 + min(lane, nrows - 1));
   lfloat* xs = region;
@@ -566,32 +587,98 @@ __device__ __forceinline__ void mv_block_float(const MvLaunch& L, const MvSeg& g
   if (NM == 2 && wave == 0) exp_tab_dma(exp_tab);
   if (L.nx) norm_dma(L, xs, ws);
   else act_dma(L, la);
-  wait_vmcnt<0>();
+  __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads
+  // piece k of this thread: P = tid + 512 (k % kJ) of matrix k / kJ: row
+  // P / PR (clamped to the valid rows), 16 bytes at 16 (P % PR) of the stage
+  constexpr int NP = (int)kJ * NM;
+  const uint8_t* src[NP];
+  uint32_t dof[NP];
+#pragma unroll
+  for (int k = 0; k < NP; k++) {
+    const uint32_t P = tid + 512u * (k % kJ), r = P / PR, c = P - r * PR;
+    src[k] = (k / kJ ? g.w2.a : g.w.a) + (size_t)(row0 + min(r, nrows - 1)) * g.w.row_bytes + 16 * c;
+    dof[k] = (k / kJ) * R * RS + r * RS + 16 * c;
+  }
+  u32x4_t pc[NP];
+#pragma unroll
+  for (int k = 0; k < NP; k++) pc[k] = *(const RLH_GLOBAL u32x4_t*)src[k];
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<NP>();  // this wave's copies have landed (the weight loads may not)
   if (L.nx) norm_finish(L, la, xs, ws, misc);
   else act_finish(L, la);
-  // the chains: (matrix m, row r, slot s) for every thread in turn
-  const uint32_t nchain = (uint32_t)NM * nrows * S, steps = cols / S;
-  for (uint32_t q = tid; q < nchain; q += NT) {
-    const uint32_t m = q / (nrows * S), r = (q / S) % nrows, s = q % S;
-    const uint8_t* wrow = (m ? g.w2.a : g.w.a) + (size_t)(row0 + r) * g.w.row_bytes;
-    float a = 0.0f;
-#pragma unroll 8
-    for (uint32_t k = 0; k < steps; k++) {
-      const uint32_t e = k * S + s;
-      const float x = la.xf[(e >> 8) * kXfStride + (e & 255)];
-      float w;
-      if constexpr (TY == RLH_TYPE_F32) {
-        w = ld_gf((const float*)wrow + e);
-      } else {
-        const uint32_t h = *(const RLH_GLOBAL uint16_t*)(wrow + 2 * (size_t)e);
-        w = TY == RLH_TYPE_F16 ? f16_to_f32(h) : __uint_as_float(h << 16);
-      }
-      if constexpr (TY == RLH_TYPE_BF16)
-        a = a + w * x;  // acc += w * x: the product rounded, then the add
-      else
-        a = __builtin_fmaf(w, x, a);
+#pragma unroll
+  for (int k = 0; k < NP; k++) *(RLH_LDS u32x4_t*)(stg + dof[k]) = pc[k];
+  float a[kPer];
+#pragma unroll
+  for (uint32_t i = 0; i < kPer; i++) a[i] = 0.0f;
+  const uint32_t nst = cols / C, nchain = NM * R * S;
+  for (uint32_t st = 0; st < nst; st++) {
+    lds_barrier();  // stage st is in its buffer; the other buffer is free
+    const bool more = st + 1 < nst;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < NP; k++) pc[k] = *(const RLH_GLOBAL u32x4_t*)(src[k] + (size_t)RY * (st + 1));
     }
-    region[(m * R + r) * stride + s] = a;
+    const RLH_LDS uint8_t* buf = stg + (st & 1) * bufb;
+    const uint32_t e0 = st * C;  // first value of the stage
+    if constexpr (TY == RLH_TYPE_BF16) {
+      if (tid < nchain) {  // chain = (matrix tid / R, row tid % R): eight values per read
+        const RLH_LDS uint8_t* wr = buf + tid * RS;
+        float acc = a[0];
+#pragma unroll 2
+        for (uint32_t k = 0; k < C / 8; k++) {
+          const uint32_t e = e0 + 8 * k;  // eight values inside one 256-value super-block
+          const lfloat* xr = la.xf + (e >> 8) * kXfStride + (e & 255);
+          const u32x4_t w8 = *(const lu32x4*)(wr + 16 * k);
+          const f32x4_t xa = *(const lf32x4*)xr, xb = *(const lf32x4*)(xr + 4);
+          const uint32_t wv[4] = {w8.x, w8.y, w8.z, w8.w};
+          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const float w = __uint_as_float(i & 1 ? wv[i / 2] & 0xffff0000u : wv[i / 2] << 16);
+            acc = acc + w * xv[i];  // acc += w * x: the product rounded, then the add
+          }
+        }
+        a[0] = acc;
+      }
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < kPer; i++) {
+        const uint32_t q = tid + 512u * i;  // chain (matrix q / (R S), row (q / S) % R, slot q % S)
+        if (q < nchain) {
+          const RLH_LDS uint8_t* wr = buf + (q / S) * RS;  // (matrix, row) rows are consecutive
+          const uint32_t s = q % S;
+          float acc = a[i];
+#pragma unroll 4
+          for (uint32_t k = 0; k < C / S; k++) {
+            const uint32_t el = k * S + s, e = e0 + el;
+            const float x = la.xf[(e >> 8) * kXfStride + (e & 255)];
+            float w;
+            if constexpr (TY == RLH_TYPE_F32)
+              w = *(const lfloat*)(wr + 4 * el);
+            else
+              w = f16_to_f32(*(const RLH_LDS uint16_t*)(wr + 2 * el));
+            acc = __builtin_fmaf(w, x, acc);
+          }
+          a[i] = acc;
+        }
+      }
+    }
+    if (more) {
+      RLH_LDS uint8_t* nbuf = stg + ((st + 1) & 1) * bufb;  // freed by this step's barrier
+#pragma unroll
+      for (int k = 0; k < NP; k++) *(RLH_LDS u32x4_t*)(nbuf + dof[k]) = pc[k];
+    }
+  }
+  // chain results into the tile [matrix][row][slot]
+  if constexpr (TY == RLH_TYPE_BF16) {
+    if (tid < nchain) region[tid * stride] = a[0];
+  } else {
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; i++) {
+      const uint32_t q = tid + 512u * i;
+      if (q < nchain) region[(q / S) * stride + q % S] = a[i];
+    }
   }
   __syncthreads();
   float acc = 0.0f;
@@ -866,7 +953,7 @@ uint32_t plan_xf_bytes(const MvPlan& p) { return p.L.need_xf ? (p.L.cols / 256) 
 uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   const uint32_t cols = p.L.cols, nsb = cols / 256;
   const uint32_t stride = std::max(nsb * p.max_terms + 4, p.slot_stride);
-  const uint32_t tile = nm * R * stride * 4;
+  const uint32_t tile = nm * R * stride * 4 + p.float_stage;  // float plans: stage buffers after the tile
   return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? 2 * cols * 4 : 0u);
 }
 
@@ -958,17 +1045,28 @@ bool mv_plan_finish(MvPlan& p) {
       ntj = w.ntj;
     }
   }
+  const bool tiled_any = tr != 0;
   if (tr == 0) tr = 64;  // float segments only
   if (nm == 2 && (p.L.seg[0].w2.ty != p.L.seg[0].w.ty || p.L.seg[0].w2.rows != p.L.seg[0].w.rows ||
                   p.L.seg[0].w.rows % 32 != 0))
     return false;
-  // the epilogue runs one row per lane: R <= 64
-  const uint32_t R = nm == 2 || fl ? 64u : std::min<uint32_t>(p.norm && !p.quant ? 2 * tr : tr, 64);
+  // the epilogue runs one row per lane: R <= 64. Float segments alone take
+  // few rows per block (many blocks stream the rows) with whole stages (a
+  // row's part of a stage, 32768 / R bytes, must divide the row): 16 rows
+  // when the row length is a multiple of 1024 values, 32 for 512, else 64;
+  // 32 in PAIR mode (16 KB stages; the Q8 blocks of h); 64 beside tiled
+  // segments
+  uint32_t R;
+  if (fl && !tiled_any)
+    R = nm == 2 ? 32u : (p.L.cols % 1024 == 0 ? 16u : (p.L.cols % 512 == 0 ? 32u : 64u));
+  else
+    R = nm == 2 || fl ? 64u : std::min<uint32_t>(p.norm && !p.quant ? 2 * tr : tr, 64);
   p.L.need_xf = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++)
     if (mv_needs_f32(p.L.seg[s].w.ty) || (p.L.seg[s].pair && mv_needs_f32(p.L.seg[s].w2.ty))) p.L.need_xf = 1;
   if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // f32 products need the f32 activation
   p.slot_stride = slots + 1;  // float plans: a row's chain results
+  p.float_stage = fl ? mv_float_stage_bytes(nm, R) : 0u;
   if (plan_lds(p, R, nm) > kMaxLds) return false;
   if (p.norm && (p.L.cols > (p.quant ? kMvMaxQuantCols : kMvMaxNormCols) || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
