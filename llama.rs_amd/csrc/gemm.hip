@@ -120,7 +120,7 @@ struct GT<RLH_TYPE_Q4_K> {
   __device__ __forceinline__ static void compute(const W (&w)[2], const StageView& v, const Lane& ln,
                                                  float (&acc)[2][2][4]) {
     const uint64_t m4 = 0x0F0F0F0F0F0F0F0Full;
-#pragma unroll 1
+#pragma unroll 2
     for (int g = 0; g < 4; g++) {
       long alo[2], ahi[2];
 #pragma unroll
@@ -314,7 +314,7 @@ struct GT<RLH_TYPE_Q8_0> {
       dw[tc][2] = wr[tc].dv.z;
       dw[tc][3] = wr[tc].dv.w;
     }
-#pragma unroll 1
+#pragma unroll 2
     for (int k = 0; k < 8; k++) {
       float dk[2];
 #pragma unroll
@@ -376,7 +376,7 @@ struct GT<RLH_TYPE_Q4_0> {
       dw[tc][2] = wr[tc].dv.z;
       dw[tc][3] = wr[tc].dv.w;
     }
-#pragma unroll 1
+#pragma unroll 2
     for (int k = 0; k < 8; k++) {
       float dk[2];
       uint64_t b[2];
