@@ -6,16 +6,18 @@
 //          p_j = e_j * (1/sum) when sum > 0)
 //   o_d  = sequential over j of (p_j * V_j[d]) + o_d (saxpy, simd.rs:674-691)
 //
-// k_attn_qk: one block per (KV head, 64-position tile, tile of query
-// tokens). The tile's K rows are staged in LDS once; each lane owns a
-// position and holds its K row in registers for all of its wave's (token,
-// head) combinations, whose q vectors are LDS broadcasts. K rows and q are
-// stored slot-major (element e = 8m + l + 32k at 16l + 4m + k): the FMA
-// chains, A_l = (a0+a1)+(a2+a3) and the reduction tree then follow the
-// reference exactly. Tiles above the causal diagonal exit at once. In decode
-// the kernel also applies QK-norm (rmsnorm_head) and NeoX RoPE to the q
-// heads and, in the block whose tile holds the new position, to k, and
-// writes K/V at pos (model.rs:642-656); all of it in registers.
+// k_attn_qk (decode): one block per (KV head, 64-position tile). The
+// tile's K rows are staged in LDS once; each lane owns a position and holds
+// its K row in registers for its wave's query head, whose q vector is an LDS
+// broadcast. K rows and q are stored slot-major (element e = 8m + l + 32k at
+// 16l + 4m + k): the FMA chains, A_l = (a0+a1)+(a2+a3) and the reduction
+// tree then follow the reference exactly. The kernel also applies QK-norm
+// (rmsnorm_head) and NeoX RoPE to the q heads and, in the block whose tile
+// holds the new position, to k, and writes K/V at pos (model.rs:642-656);
+// all of it in registers.
+// k_attn_qk_pre (prefill): one block per (KV head, 64-position tile, tile of
+// query tokens); lanes own positions as above, q reaches every lane by DPP
+// row broadcasts (below). Tiles above the causal diagonal exit at once.
 // k_attn_softmax: one block per (head, token): the row in LDS, max and exp
 // in parallel, the sequential sum in one lane, probabilities written back
 // over the scores.
@@ -79,15 +81,14 @@ __device__ __forceinline__ void norm_rope_regs(float& x0, float& x1, bool norm, 
   x1 = r1;
 }
 
-// grid: (KVH * ntiles, ceil(n_tok / TT)); block 256.
-template <bool FUSED>
+// grid: (KVH * ntiles, 1); block 256.
 __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
   __shared__ __attribute__((aligned(16))) float qv_g[kQkComb * kHd];
   lfloat* kt = (lfloat*)kt_g;
   lfloat* qv = (lfloat*)qv_g;
   const int G = a.H / a.KVH;
-  const uint32_t TT = FUSED ? 1u : (uint32_t)(kQkComb / G);
+  const uint32_t TT = 1u;  // one token
   const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
   const uint32_t g = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
   const uint32_t tok0 = blockIdx.y * TT;
@@ -99,7 +100,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
   const int qd = a.H * kHd, kvd = a.KVH * kHd;
   const int ncomb = (int)ntok * G;
   const int nmine = ncomb > wave ? (ncomb - wave + 3) / 4 : 0;  // combinations wave, wave+4, ...
-  const bool own_pos = FUSED && pos_last < j0 + kPosTile;
+  const bool own_pos = pos_last < j0 + kPosTile;
 
   // every global load first: K tile rows (the new position's row, in
   // decode, is produced below), q heads, and the decode norm/rope operands
@@ -114,7 +115,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
     const uint32_t c = (uint32_t)(tid + 256 * i), jl = c >> 5, f4 = c & 31, j = min(j0 + jl, pos_last);
     kr[i] = ld_gf4(a.kcache + (size_t)j * kvd + g * kHd + 4 * f4);
   }
-  const bool hb = FUSED && a.bq != nullptr;
+  const bool hb = a.bq != nullptr;
   const float* bq = hb ? a.bq : a.q;
   float q0[4], q1[4];
 #pragma unroll
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
     const float* src = a.q + (size_t)(tok0 + tt) * qd + h * kHd;
     q0[i] = ld_gf(src + lane);
     q1[i] = ld_gf(src + lane + 64);
-    if (FUSED) {
+    {
       const float b0 = ld_gf(bq + h * kHd + lane), b1 = ld_gf(bq + h * kHd + lane + 64);
       if (hb) {
         q0[i] = q0[i] + b0;
@@ -131,7 +132,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
       }
     }
   }
-  if (FUSED) {
+  {
     const float c = ld_gf(a.rope_cs + (size_t)pos_first * kHd + 2 * lane);
     const float sn = ld_gf(a.rope_cs + (size_t)pos_first * kHd + 2 * lane + 1);
     const bool nq = a.qn != nullptr;
@@ -174,7 +175,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     const uint32_t c = (uint32_t)(tid + 256 * i), jl = c >> 5, f4 = c & 31, j = j0 + jl;
-    if (j <= pos_last && !(FUSED && j == pos_last)) {
+    if (j < pos_last) {
       lfloat* row = kt + jl * kKStride;
       row[perm(4 * f4)] = kr[i].x;
       row[perm(4 * f4 + 1)] = kr[i].y;
@@ -222,6 +223,117 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
       const float d = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
       a.scores[((size_t)(tok0 + tt) * a.H + h) * a.t_stride + j] = d * a.scale;
     }
+  }
+}
+
+// Prefill scores (q already normed and roped): one block per (KV head,
+// 64-position tile, tile of kPreQkComb / G query tokens). The K tile is
+// staged in LDS once and each lane (= position) keeps its K row in
+// registers. The wave walks its (token, head) combinations with q held in
+// every row of 16 lanes (lane r of a row holds elements 16m + r in qm[m])
+// and broadcast to the row by DPP (row_newbcast), so no q element passes
+// through LDS; the next combination's q is loaded while the current one is
+// computed. Slot s (0..31) of dot_f32_avx2 is the FMA chain over elements s,
+// s+32, s+64, s+96, A_l = (slot l + slot l+8) + (slot l+16 + slot l+24),
+// then the AVX2 tree (simd.rs:328-377).
+// grid: (KVH * ntiles, ceil(n_tok / TP)), TP = kPreQkComb / G; block 256.
+constexpr int kPreQkComb = 64;
+
+// acc[i] = fma(q_e, k_i, acc[i]) for the 8 elements e = 16m + R0 + i, whose
+// q_e is lane R0 + i of every row of 16 lanes in qm (v_fmac_f32 takes it by
+// DPP row_newbcast; one instruction per FMA, no broadcast copies). The
+// leading s_nop covers the DPP read-after-VALU-write hazard on qm.
+template <int R0>
+__device__ __forceinline__ void fmac8_bcast(float (&acc)[32], int s0, float qm, const f32x4_t& k0, const f32x4_t& k1) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %8, %9 row_newbcast:%17 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %8, %10 row_newbcast:%18 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %8, %11 row_newbcast:%19 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %8, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %4, %8, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %5, %8, %14 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %6, %8, %15 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %7, %8, %16 row_newbcast:%24 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc[s0]), "+v"(acc[s0 + 1]), "+v"(acc[s0 + 2]), "+v"(acc[s0 + 3]), "+v"(acc[s0 + 4]), "+v"(acc[s0 + 5]),
+        "+v"(acc[s0 + 6]), "+v"(acc[s0 + 7])
+      : "v"(qm), "v"(k0.x), "v"(k0.y), "v"(k0.z), "v"(k0.w), "v"(k1.x), "v"(k1.y), "v"(k1.z), "v"(k1.w), "i"(R0),
+        "i"(R0 + 1), "i"(R0 + 2), "i"(R0 + 3), "i"(R0 + 4), "i"(R0 + 5), "i"(R0 + 6), "i"(R0 + 7));
+}
+// step K of the 32 slot chains (elements s + 32K): slots 0..15 take qm[2K],
+// slots 16..31 qm[2K + 1]
+template <int K>
+__device__ __forceinline__ void qk_step(float (&acc)[32], const float (&qm)[8], const f32x4_t (&kreg)[32]) {
+  fmac8_bcast<0>(acc, 0, qm[2 * K], kreg[8 * K], kreg[8 * K + 1]);
+  fmac8_bcast<8>(acc, 8, qm[2 * K], kreg[8 * K + 2], kreg[8 * K + 3]);
+  fmac8_bcast<0>(acc, 16, qm[2 * K + 1], kreg[8 * K + 4], kreg[8 * K + 5]);
+  fmac8_bcast<8>(acc, 24, qm[2 * K + 1], kreg[8 * K + 6], kreg[8 * K + 7]);
+}
+
+__global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
+  lfloat* kt = (lfloat*)kt_g;
+  const uint32_t G = (uint32_t)(a.H / a.KVH), TP = (uint32_t)kPreQkComb / G;
+  const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
+  const uint32_t g = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
+  const uint32_t tok0 = blockIdx.y * TP;
+  const uint32_t ntok = a.n_tok - tok0 < TP ? a.n_tok - tok0 : TP;
+  const uint32_t pos_first = a.pos0[0] + tok0, pos_last = pos_first + ntok - 1;
+  const uint32_t j0 = tile * kPosTile;
+  if (j0 > pos_last) return;  // whole tile above the causal diagonal
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t qd = (uint32_t)a.H * kHd, kvd = (uint32_t)a.KVH * kHd;
+  // K tile rows in natural element order (rows past pos_last repeat it)
+  float4 kr[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t c = tid + 256u * i, jl = c >> 5, f4 = c & 31, j = min(j0 + jl, pos_last);
+    kr[i] = ld_gf4(a.kcache + (size_t)j * kvd + g * kHd + 4 * f4);
+  }
+  // combinations of tokens that see at least one position of the tile;
+  // the wave's first q is loaded with the K tile
+  const uint32_t tt0 = j0 > pos_first ? j0 - pos_first : 0u;
+  const uint32_t ncomb = ntok * G;
+  auto q_load = [&](float (&qm)[8], uint32_t c) {
+    const uint32_t cc = min(c, ncomb - 1), tt = cc / G, h = g * G + cc % G;
+    const float* qs = a.q + (size_t)(tok0 + tt) * qd + h * kHd + (lane & 15);
+#pragma unroll
+    for (int m = 0; m < 8; m++) qm[m] = ld_gf(qs + 16 * m);
+  };
+  float qa[8], qb[8];
+  uint32_t c = tt0 * G + wave;
+  q_load(qa, c);
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t ci = tid + 256u * i, jl = ci >> 5, f4 = ci & 31;
+    *(lf32x4*)(kt + jl * kKStride + 4 * f4) = f32x4_t{kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+  }
+  __syncthreads();
+  const uint32_t j = j0 + lane;
+  f32x4_t kreg[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) kreg[i] = *(const lf32x4*)(kt + lane * kKStride + 4 * i);
+  auto one = [&](const float (&qm)[8], uint32_t cc) {
+    const uint32_t tt = cc / G, h = g * G + cc % G;
+    float acc[32];
+#pragma unroll
+    for (int s = 0; s < 32; s++) acc[s] = 0.0f;  // fma(q, k, +0) starts each chain, as the reference
+    qk_step<0>(acc, qm, kreg);
+    qk_step<1>(acc, qm, kreg);
+    qk_step<2>(acc, qm, kreg);
+    qk_step<3>(acc, qm, kreg);
+    float A[8];
+#pragma unroll
+    for (int l = 0; l < 8; l++) A[l] = (acc[l] + acc[l + 8]) + (acc[l + 16] + acc[l + 24]);
+    const float d = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+    if (j <= pos_first + tt) a.scores[((size_t)(tok0 + tt) * a.H + h) * a.t_stride + j] = d * a.scale;
+  };
+#pragma unroll 1
+  for (; c < ncomb; c += 8) {
+    q_load(qb, c + 4);
+    one(qa, c);
+    if (c + 4 >= ncomb) break;
+    q_load(qa, c + 8);
+    one(qb, c + 4);
   }
 }
 
@@ -937,11 +1049,12 @@ size_t softmax_lds(uint32_t t_max) { return (size_t)((t_max + 3) & ~3u) * 4; }
 
 void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
   const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
-  const uint32_t G = (uint32_t)(a.H / a.KVH), TT = (uint32_t)kQkComb / G;
-  if (fused)
-    hipLaunchKernelGGL(k_attn_qk<true>, dim3(a.KVH * ntiles, a.n_tok), dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL(k_attn_qk<false>, dim3(a.KVH * ntiles, (a.n_tok + TT - 1) / TT), dim3(256), 0, st, a);
+  if (fused) {
+    hipLaunchKernelGGL(k_attn_qk, dim3(a.KVH * ntiles, a.n_tok), dim3(256), 0, st, a);
+  } else {
+    const uint32_t TP = (uint32_t)kPreQkComb / (uint32_t)(a.H / a.KVH);
+    hipLaunchKernelGGL(k_attn_qk_pre, dim3(a.KVH * ntiles, (a.n_tok + TP - 1) / TP), dim3(256), 0, st, a);
+  }
 }
 
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
