@@ -371,12 +371,33 @@ __device__ __forceinline__ float rms_sumsq_lds(const RLH_LDS float* x, int n) {
   float acc = 0.0f;
   if (lane < 32) {
     int i = lane;
-    for (; i + 32 * 31 < n32; i += 32 * 32) {  // 32 reads in flight, then the chain
-      float v[32];
+    // batches of 32 elements per lane, the next batch's reads issued before
+    // the current batch's chain (two register sets used alternately, the
+    // reads unconditional with the batch index clamped, as in seq_sum_lds)
+    const int nb = n32 / (32 * 32);
+    if (nb > 0) {
+      float a[32], b[32];
 #pragma unroll
-      for (int k = 0; k < 32; k++) v[k] = x[i + 32 * k];
+      for (int k = 0; k < 32; k++) a[k] = x[i + 32 * k];
+      for (int bi = 0;; bi += 2) {
+        const int o1 = (bi + 1 < nb ? bi + 1 : nb - 1) * 1024;
 #pragma unroll
-      for (int k = 0; k < 32; k++) acc = __builtin_fmaf(v[k], v[k], acc);
+        for (int k = 0; k < 32; k++) b[k] = x[i + o1 + 32 * k];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 32; k++) acc = __builtin_fmaf(a[k], a[k], acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (bi + 1 >= nb) break;
+        const int o2 = (bi + 2 < nb ? bi + 2 : nb - 1) * 1024;
+#pragma unroll
+        for (int k = 0; k < 32; k++) a[k] = x[i + o2 + 32 * k];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < 32; k++) acc = __builtin_fmaf(b[k], b[k], acc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (bi + 2 >= nb) break;
+      }
+      i += nb * 1024;
     }
     for (; i + 32 * 7 < n32; i += 32 * 8) {
       float v[8];
