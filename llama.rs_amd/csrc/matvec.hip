@@ -957,6 +957,28 @@ uint32_t plan_lds(const MvPlan& p, uint32_t R, uint32_t nm) {
   return plan_act_bytes(p) + plan_xf_bytes(p) + std::max(tile, p.norm ? 2 * cols * 4 : 0u);
 }
 
+// Waves of a tiled block of R rows (all eight for a quantize prologue).
+uint32_t plan_waves(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj, uint32_t nm) {
+  return p.quant ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, (R / tr) * ntj));
+}
+
+// Blocks of R rows the GPU holds at once (CUs x blocks per CU for the plan's
+// kernel, its block size and LDS), 0 if unknown.
+uint32_t mv_resident_blocks(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj) {
+  uint32_t ty = p.L.seg[0].w.ty;
+  for (uint32_t s = 1; s < p.L.nseg; s++)
+    if (p.L.seg[s].w.ty != ty) ty = 0;
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const uint32_t threads = 64 * plan_waves(p, R, tr, ntj, 1);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)mv_kernel<1>(ty), (int)threads,
+                                                   plan_lds(p, R, 1)) != hipSuccess)
+    return 0;
+  return (uint32_t)(cus * per_cu);
+}
+
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
   uint32_t b = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) b += (p.L.seg[s].w.rows + R - 1) / R;
@@ -1068,6 +1090,16 @@ bool mv_plan_finish(MvPlan& p) {
   p.slot_stride = slots + 1;  // float plans: a row's chain results
   p.float_stage = fl ? mv_float_stage_bytes(nm, R) : 0u;
   if (plan_lds(p, R, nm) > kMaxLds) return false;
+  // A grid just above the blocks the GPU holds at once would run a second,
+  // short round of blocks after the first (every block pays its prologue and
+  // tail again, and most CUs idle meanwhile): then blocks of twice the rows,
+  // when those fit in one round (the 32B q/k/v launch: 320 blocks of 32 rows
+  // at one block per CU, 160 of 64)
+  if (tiled_any && !fl && nm == 1 && 2 * R <= 64 && plan_lds(p, 2 * R, nm) <= kMaxLds) {
+    const uint32_t b0 = plan_blocks(p, R), b1 = plan_blocks(p, 2 * R);
+    const uint32_t s0 = mv_resident_blocks(p, R, tr, ntj), s1 = mv_resident_blocks(p, 2 * R, tr, ntj);
+    if (s0 && s1 && b0 > s0 && b0 <= 2 * s0 && b1 <= s1) R *= 2;
+  }
   if (p.norm && (p.L.cols > (p.quant ? kMvMaxQuantCols : kMvMaxNormCols) || p.L.cols % 256 != 0)) return false;
   p.L.rows_per_blk = R;
   p.L.tile_stride = std::max(nsb * p.max_terms + 4, p.slot_stride);
