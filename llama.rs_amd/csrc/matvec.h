@@ -54,6 +54,10 @@ struct MvLaunch {
   uint32_t xf_off;  // byte offset of the f32 row in LDS
   uint32_t region_off;    // byte offset of the term tiles in LDS
   uint32_t tile_stride;   // floats per term-tile row
+  // ring plans (long rows, one row tile per block): the term region holds
+  // `ring` rounds of the producer waves' tiles, which wave 0 chains as they
+  // complete; 0 = every row's terms stay in LDS until the end
+  uint32_t ring;
   uint32_t has_argmax;
   MvArgmax am;
 };

@@ -29,6 +29,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "kernels.h"
 #include "matvec.h"
@@ -762,18 +763,56 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   using P = typename I::P;
   constexpr int kP = I::kParts;
   constexpr int kH1 = kP == 2 ? 1 : 0;  // part of the odd units
-  const uint32_t my_tiles = wave < ntiles ? (ntiles - 1 - wave) / nwaves + 1 : 0;
+  // Ring plan (NM = 1, one row tile per block): waves 1.. produce tiles in
+  // rounds (producer p takes tiles p, p + np, ...; round r = the r-th tile
+  // of every producer), writing round r's terms into slot r % ring of the
+  // region, and wave 0 adds each completed round to the row chains in item
+  // order. done[s] counts the tiles written into slot s so far (a round is
+  // complete when the count reaches the tiles of all rounds of that slot up
+  // to it: only the last round may be short); `consumed` counts the rounds
+  // wave 0 has added, and a producer writes round r only once round
+  // r - ring has been consumed. Relaxed LDS atomics after lgkmcnt(0), as in
+  // the split chain below.
+  const uint32_t ring = NM == 1 ? L.ring : 0u;
+  const uint32_t np = ring ? nwaves - 1 : nwaves;           // producer waves
+  const uint32_t pw = ring ? wave - 1 : wave;               // producer index (wave 0 of a ring: none)
+  const bool producer = !ring || wave != 0;
+  RLH_LDS uint32_t* ring_done = (RLH_LDS uint32_t*)(misc + 4);  // [ring], then `consumed`
+  RLH_LDS uint32_t* ring_consumed = ring_done + 3;
+  const uint32_t my_tiles = producer && pw < ntiles ? (ntiles - 1 - pw) / np + 1 : 0;
   const uint32_t nunits = my_tiles * NM * kP;
   auto tile_off = [&](uint32_t t) { return ((size_t)(rt0 + t / ntj) * ntj + t % ntj) * tile_bytes; };
   auto issue = [&](P& r, uint32_t u, int h) {
-    const uint32_t t = min(wave + (u / (NM * kP)) * nwaves, ntiles - 1);
+    const uint32_t t = min(pw + (u / (NM * kP)) * np, ntiles - 1);
     const uint8_t* base = (NM == 2 && (u / kP) % NM == 1) ? g.w2.a : g.w.a;
     I::load(r, base + tile_off(t), lane, h);
   };
   auto work = [&](const P& r, uint32_t u, int h) {
-    const uint32_t t = wave + (u / (NM * kP)) * nwaves, m = (u / kP) % NM;
+    const uint32_t rr = u / (NM * kP), t = pw + rr * np, m = (u / kP) % NM;
     const uint32_t rl = (t / ntj) * TR + lane % TR, j = (t % ntj) * TJ + lane / TR;
-    I::terms(r, la, j, region + (m * R + rl) * stride + j * I::kT, h);
+    if (ring)  // slot rr % ring, the round's items from 0 (one row tile: t < ntj)
+      I::terms(r, la, j, region + ((rr % ring) * R + rl) * stride + (pw * TJ + lane / TR) * I::kT, h);
+    else
+      I::terms(r, la, j, region + (m * R + rl) * stride + j * I::kT, h);
+  };
+  // ring: before the first part of a tile, wait until its slot is free;
+  // after the last part, count the tile into its slot
+  auto ring_wait = [&](uint32_t u) {
+    const uint32_t rr = u / kP;
+    if (u % kP != 0 || rr < ring) return;
+    for (uint32_t spin = 0; spin < (1u << 26); spin++) {  // bounded: wave 0 keeps consuming
+      if (__hip_atomic_load(ring_consumed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= rr - ring + 1) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+  };
+  auto ring_signal = [&](uint32_t u) {
+    if (u % kP != kP - 1) return;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): the terms are in LDS
+    asm volatile("" ::: "memory");
+    if (lane == 0)
+      __hip_atomic_fetch_add(ring_done + (u / kP) % max(ring, 1u), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   };
   // Split chain (single matrix, two-part items, one row tile per block, a
   // long chain): the waves' tiles come in rounds (tile w + r * nwaves in
@@ -784,9 +823,11 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   // barrier. Items are ordered by tile, so the first kr rounds hold the
   // row's first kr * nwaves * TJ items.
   const uint32_t kr = ntiles > nwaves ? (ntiles - 1 - (nwaves - 1)) / nwaves + 1 : 0;
-  const bool split = NM == 1 && kP == 2 && RB == 1 && ntiles % nwaves != 0 && kr > 0 && nsb * I::kT >= 256;
+  const bool split = !ring && NM == 1 && kP == 2 && RB == 1 && ntiles % nwaves != 0 && kr > 0 && nsb * I::kT >= 256;
   RLH_LDS uint32_t* rounds_done = (RLH_LDS uint32_t*)(misc + 3);
   if (split && tid == 0) *rounds_done = 0u;  // seen by all after the prologue's barriers
+  if (ring && tid == 0)
+    for (int i = 0; i < 4; i++) ring_done[i] = 0u;
   // the residual of the chain lane's row, read now so that the epilogue
   // does not wait for it
   float rsd = 0.0f;
@@ -798,21 +839,28 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   else act_dma(L, la);
   __builtin_amdgcn_sched_barrier(0);  // the copies stay ahead of the weight loads
   P ua, ub;
-  issue(ua, 0, 0);
+  if (producer) issue(ua, 0, 0);
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<I::kLoads>();  // this wave's copies have landed (the unit's loads may not)
+  if (producer)
+    wait_vmcnt<I::kLoads>();  // this wave's copies have landed (the unit's loads may not)
+  else
+    wait_vmcnt<0>();
   if (L.nx) norm_finish(L, la, xs, ws, misc);
   else act_finish(L, la);
   for (uint32_t u = 0; u < nunits; u += 2) {
     weights_ready(ua);
     if (u + 1 < nunits) issue(ub, u + 1, kH1);
     __builtin_amdgcn_sched_barrier(0);
+    if (ring) ring_wait(u);
     work(ua, u, 0);
+    if (ring) ring_signal(u);
     if (u + 1 >= nunits) break;
     weights_ready(ub);
     if (u + 2 < nunits) issue(ua, u + 2, 0);
     __builtin_amdgcn_sched_barrier(0);
+    if (ring) ring_wait(u + 1);
     work(ub, u + 1, kH1);
+    if (ring) ring_signal(u + 1);
     if (split && u / 2 < kr) {  // tile u / 2 (one tile = two units) is done
       // LDS-only hand-over (a wave's LDS operations complete in order):
       // lgkmcnt(0), then a relaxed add; release/acquire atomics would also
@@ -824,6 +872,26 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
       if (lane == 0) __hip_atomic_fetch_add(rounds_done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   }
+  float acc = 0.0f;
+  if (ring) {
+    if (wave != 0) return;
+    // the row chains, round by round as the producers complete them
+    const uint32_t nr = (ntiles + np - 1) / np;
+    const lfloat* rowp = region + (lane < nrows ? lane : 0) * stride;
+    for (uint32_t rr = 0; rr < nr; rr++) {
+      const uint32_t s = rr % ring, tin = min(np, ntiles - rr * np), need = np * (rr / ring) + tin;
+      for (uint32_t spin = 0; spin < (1u << 26); spin++) {  // bounded: every producer reaches its tiles
+        if (__hip_atomic_load(ring_done + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      asm volatile("" ::: "memory");
+      acc = seq_sum_lds(rowp + s * R * stride, tin * TJ * I::kT, acc);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): the slot's reads are done
+      asm volatile("" ::: "memory");
+      if (lane == 0) __hip_atomic_fetch_add(ring_consumed, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  } else {
   const uint32_t n_early = split ? kr * nwaves * TJ * I::kT : 0u;
   if (split && wave == nwaves - 1) {
     // every wave reaches kr tiles (each has at least kr), so the wait ends
@@ -837,10 +905,10 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   // wave m < NM: lane r adds row r's terms of matrix m in order (after the
   // early part of a split chain); lanes past the valid rows chain a copy of
   // row 0 so that the wave stays converged
-  float acc = 0.0f;
   if (wave < (uint32_t)NM)
     acc = seq_sum_lds(region + (wave * R + (lane < nrows ? lane : 0)) * stride + n_early, nsb * I::kT - n_early,
                       split ? misc[4 + lane] : 0.0f);
+  }
 
   if (NM == 2) {
     if (wave == 1) misc[4 + lane] = acc;
@@ -962,9 +1030,9 @@ uint32_t plan_waves(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj, uint
   return p.quant ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, (R / tr) * ntj));
 }
 
-// Blocks of R rows the GPU holds at once (CUs x blocks per CU for the plan's
-// kernel, its block size and LDS), 0 if unknown.
-uint32_t mv_resident_blocks(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj) {
+// Blocks the GPU holds at once (CUs x blocks per CU) for the plan's single
+// kernel with `threads` per block and `lds` bytes, 0 if unknown.
+uint32_t mv_resident(const MvPlan& p, uint32_t threads, uint32_t lds) {
   uint32_t ty = p.L.seg[0].w.ty;
   for (uint32_t s = 1; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty != ty) ty = 0;
@@ -972,11 +1040,20 @@ uint32_t mv_resident_blocks(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t n
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  const uint32_t threads = 64 * plan_waves(p, R, tr, ntj, 1);
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)mv_kernel<1>(ty), (int)threads,
-                                                   plan_lds(p, R, 1)) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)mv_kernel<1>(ty), (int)threads, lds) !=
+      hipSuccess)
     return 0;
   return (uint32_t)(cus * per_cu);
+}
+uint32_t mv_resident_blocks(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj) {
+  return mv_resident(p, 64 * plan_waves(p, R, tr, ntj, 1), plan_lds(p, R, 1));
+}
+
+// Ring plan rows: floats per row of one slot (np producers' tiles of tj
+// items), 16-byte aligned, padded like the whole-row tiles.
+uint32_t ring_stride(const MvPlan& p, uint32_t np, uint32_t tj) { return ((np * tj * p.max_terms + 3) & ~3u) + 4; }
+uint32_t ring_lds(const MvPlan& p, uint32_t R, uint32_t np, uint32_t tj, uint32_t slots) {
+  return plan_act_bytes(p) + plan_xf_bytes(p) + slots * R * ring_stride(p, np, tj) * 4;
 }
 
 uint32_t plan_blocks(const MvPlan& p, uint32_t R) {
@@ -1101,16 +1178,39 @@ bool mv_plan_finish(MvPlan& p) {
     if (s0 && s1 && b0 > s0 && b0 <= 2 * s0 && b1 <= s1) R *= 2;
   }
   if (p.norm && (p.L.cols > (p.quant ? kMvMaxQuantCols : kMvMaxNormCols) || p.L.cols % 256 != 0)) return false;
+  // Still more blocks than the GPU holds (rows so long that their whole-row
+  // terms leave one block per CU: the 32B ffn_down, 5120 rows of 25600
+  // values in 320 blocks of 143 KB): a ring plan keeps two rounds of the
+  // producers' tiles instead of whole rows, with the most producer waves
+  // (two to seven, plus the chain wave) that let every block be resident at
+  // once (32B ffn_down: four producers, 74 KB, two blocks per CU)
+  // (RLH_MV_RING=1 in the environment takes a ring plan wherever one
+  // applies, with the most producers that fit the LDS: the tests run the
+  // ring on small shapes and every tiled type with it)
+  uint32_t ring_np = 0;
+  const uint32_t tj = tiled_any ? p.L.seg[0].w.tj : 1u;
+  if (tiled_any && !fl && nm == 1 && !p.norm && R == tr && ntj >= 2) {
+    const char* env = std::getenv("RLH_MV_RING");
+    const bool force = env && env[0] == '1';
+    const uint32_t b = plan_blocks(p, R), s = force ? 0u : mv_resident_blocks(p, R, tr, ntj);
+    if (force || (s && b > s))
+      for (uint32_t np = std::min<uint32_t>(7, ntj); np >= 2 && !ring_np; np--)  // np + 1 <= 8 waves (launch bound)
+        if (ring_lds(p, R, np, tj, 2) <= kMaxLds &&
+            (force || mv_resident(p, 64 * (np + 1), ring_lds(p, R, np, tj, 2)) >= b))
+          ring_np = np;
+  }
   p.L.rows_per_blk = R;
-  p.L.tile_stride = std::max(nsb * p.max_terms + 4, p.slot_stride);
+  p.L.ring = ring_np ? 2u : 0u;
+  p.L.tile_stride = ring_np ? ring_stride(p, ring_np, tj) : std::max(nsb * p.max_terms + 4, p.slot_stride);
   p.L.xf_off = plan_act_bytes(p);
   p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
-  p.lds = plan_lds(p, R, nm);
+  p.lds = ring_np ? ring_lds(p, R, ring_np, tj, 2) : plan_lds(p, R, nm);
   const uint32_t ntiles = (R / tr) * ntj;
   // a quantize prologue is VALU work on the whole row in every block: all
   // eight waves take part even where fewer carry tiles (measured 6.3 -> 5.8
   // us for the 8B attn_output)
-  p.waves = p.quant || fl ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles));
+  p.waves = ring_np ? ring_np + 1 : (p.quant || fl ? 8u : std::max<uint32_t>(nm, std::min<uint32_t>(8, ntiles)));
+  if (p.waves > 8) return false;  // k_mv's launch bound: 512 threads
   p.blocks = 0;
   for (uint32_t s = 0; s < p.L.nseg; s++) {
     p.L.seg[s].blk_begin = p.blocks;

@@ -81,6 +81,31 @@ def test_prefill_and_decode_bit_exact(name):
     oc.close()
 
 
+@pytest.mark.parametrize("name", ["tiny-q4km", "small-q4km"])
+def test_decode_ring_plans_bit_exact(name, monkeypatch):
+    """Decode with ring plans forced (RLH_MV_RING=1 when the cache, and with
+    it the captured step, is made): ffn_down's row chains are added round by
+    round while the producers stream the next tiles."""
+    print(f"ring decode parity {name}", flush=True)
+    monkeypatch.setenv("RLH_MV_RING", "1")
+    spec, tensors, m, om = _get(name)
+    n_prompt = 8
+    prompt = rlh.synth_tokens(98, n_prompt, spec.vocab)
+    c = m.new_cache(64)
+    oc = om.new_cache(64)
+    c.forward_into(prompt, 0)
+    ref = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    lib = oracle.load()
+    tok = lib.orc_argmax(ref.ctypes.data, len(ref))
+    for i in range(6):
+        lg = c.forward_into(np.array([tok], np.uint32), n_prompt + i)
+        rg = oc.forward_into(np.array([tok], np.uint32), n_prompt + i, oracle.MODE_DEFAULT)
+        assert np.array_equal(bits(lg), bits(rg)), f"decode step {i} logits differ (rel {rel_l2(lg, rg):.2e})"
+        tok = lib.orc_argmax(rg.ctypes.data, len(rg))
+    c.close()
+    oc.close()
+
+
 @pytest.mark.parametrize("max_ctx,n_prompt", [(64, 40), (6000, 40), (1600, 700), (4400, 4100)])
 def test_decode_attention_paths(max_ctx, n_prompt):
     """Decode attention with 8 query heads per KV head (the 32B grouping):

@@ -9,7 +9,7 @@ import pytest
 
 import oracle
 import rlh
-from helpers import Q4_0, Q4_K, Q6_K, Q8_0, BLOCK, bits, random_activation, random_blocks
+from helpers import Q4_0, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_0, BLOCK, bits, random_activation, random_blocks
 
 pytestmark = pytest.mark.gpu
 
@@ -95,6 +95,44 @@ def test_matvec_large_rows():
     got = rlh.matvec(Q6_K, w, rows, cols, x)
     ref = oracle.matmul(Q6_K, w, rows, cols, x, oracle.MODE_DEFAULT)
     assert np.array_equal(bits(got), bits(ref))
+
+
+def test_matvec_32b_ffn_down_shape():
+    """The 32B ffn_down (5120 x 25600, Q6_K): whole-row terms would leave one
+    block per CU and 320 blocks, so the launch takes the ring plan (two rounds
+    of four producers' tiles in LDS, chained by wave 0 as they complete)."""
+    rng = np.random.default_rng(6)
+    rows, cols = 5120, 25600
+    w = random_blocks(Q6_K, rows * cols // 256, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = rlh.matvec(Q6_K, w, rows, cols, x)
+    ref = oracle.matmul(Q6_K, w, rows, cols, x, oracle.MODE_DEFAULT)
+    assert np.array_equal(bits(got), bits(ref))
+
+
+# Ring plans forced on small shapes (RLH_MV_RING=1; at most seven producer
+# waves): one round (2048-4096 values), three rounds with a short last one
+# and a slot reused (9728: 19 tiles of 2 items over 7 producers), two rounds
+# (12288: 12 tiles), four rounds with a four-tile last round (25600: 25
+# tiles), for every tiled type (Q5_K and the 32-value types through their
+# f32 products).
+RING_TYPES = [Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, Q4_1, Q5_0, Q5_1]
+
+
+@pytest.mark.parametrize("ty", RING_TYPES)
+@pytest.mark.parametrize("rows,cols", [(33, 2048), (100, 2560), (48, 4096), (7, 9728), (20, 12288), (9, 25600)])
+def test_matvec_ring_plan_bit_exact(ty, rows, cols, monkeypatch):
+    if ty in (Q4_1, Q5_0, Q5_1) and cols > 12288:
+        pytest.skip("no decode plan at this row length: the f32 row and the whole-row terms exceed the LDS budget")
+    print(f"ring matvec ty={ty} {rows}x{cols}", flush=True)
+    monkeypatch.setenv("RLH_MV_RING", "1")
+    rng = np.random.default_rng(rows * 3 + cols + ty)
+    bs, ts = BLOCK[ty]
+    w = random_blocks(ty, rows * cols // bs, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = rlh.matvec(ty, w, rows, cols, x)
+    ref = oracle.matmul(ty, w, rows, cols, x, oracle.MODE_DEFAULT)
+    assert np.array_equal(bits(got), bits(ref)), f"max diff {np.max(np.abs(got - ref))}"
 
 
 def test_matvec_rejects_bad_shape():
