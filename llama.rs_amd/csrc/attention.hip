@@ -586,16 +586,19 @@ __device__ __forceinline__ float wave_max(float x) {
 }
 
 // Decode softmax + PV with the block's V slice resident in LDS.
-// grid (KVH, 8 slices of 16 dimensions), block 512 (8 waves); G <= 4.
-// Dynamic LDS: score rows e[G][RS] | V slice vs[RS][16] | product ring
-// pr[3][64 chain lanes][kPrStride].
+// grid (KVH, 16 slices of kVsW = 8 dimensions), block 512 (8 waves); G <= 4.
+// Dynamic LDS: score rows e[G][RS] | V slice vs[RS][kVsW] | product ring
+// pr[3][64 chain lanes][kPrStride]. (8-wide slices: twice the blocks of
+// 16-wide ones, each with half the product traffic through LDS; measured
+// 8B 421.0 -> 422.3, 4B 490.2 -> 491.3, 0.6B 946.9 -> 952.5 tok/s.)
 // * At entry every wave issues its DMA copies: the G score rows, then exactly
-//   kVDma 1 KB pieces of the V slice (16 rows x 64 B each; a piece index
-//   past the last is clamped, so a repeated piece rewrites the same bytes).
+//   kVDma 1 KB pieces of the V slice (kVRows rows x 4 kVsW bytes each; a
+//   piece index past the last is clamped, so a repeated piece rewrites the
+//   same bytes).
 //   The softmax runs while the V slice lands.
 // * softmax_inplace of the G rows as in k_attn_smpv_dec.
-// * PV: chain lane l < G*16 of wave 0 owns (head l / 16, dimension l % 16)
-//   and adds its products in position order, o = prod_j + o (the saxpy's
+// * PV: chain lane l < G*kVsW of wave 0 owns (head l / kVsW, dimension
+//   l % kVsW) and adds its products in position order, o = prod_j + o (the saxpy's
 //   add); the products prod_j = p_j * v_j[d] are formed by waves 1..7 one
 //   64-position chunk ahead into a ring of three chunk slots, so the chain
 //   wave issues one add per position and a 16-byte LDS read per four (a
@@ -604,12 +607,13 @@ __device__ __forceinline__ float wave_max(float x) {
 //   the producers fill slot (c + 2) % 3.
 // The output is written in f32; its Q8 blocks are made by the attn_output
 // matvec's prologue.
-constexpr int kVsW = 16;              // dimensions per block
+constexpr int kVsW = 8;               // dimensions per block
 constexpr int kPrC = 64;              // positions per product chunk
 constexpr int kPrStride = kPrC + 4;   // floats per chain lane in a chunk slot
 constexpr int kPrSlots = 3;
-constexpr int kVDma = 12;             // V-slice DMA pieces per wave (16 rows each)
-constexpr uint32_t kDecVMaxCtx = 8u * kVDma * 16u;  // 1536 positions
+constexpr int kVRows = 256 / kVsW;    // V-slice rows per 1 KB DMA piece
+constexpr int kVDma = 1536 / (8 * kVRows);  // V-slice DMA pieces per wave
+constexpr uint32_t kDecVMaxCtx = 8u * kVDma * kVRows;  // 1536 positions
 constexpr size_t kDecVLdsMax = 150u * 1024u;
 
 // The chain wave's part of a product ring (chunk c of kPrC positions in
@@ -683,14 +687,14 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   }
   if (wave == 0) exp_tab_dma(tab);
   {
-    const uint32_t nvp = (t + 15) / 16;
-    const float* vsrc = a.vcache + g * kHd + d0 + (lane & 3) * 4;
+    const uint32_t nvp = (t + kVRows - 1) / kVRows;
+    const float* vsrc = a.vcache + g * kHd + d0 + (lane % (kVsW / 4)) * 4;
 #pragma unroll
     for (int i = 0; i < kVDma; i++) {
       const uint32_t pc = min((uint32_t)(wave + 8 * i), nvp - 1);
-      const uint32_t row = min(pc * 16 + (uint32_t)(lane >> 2), t - 1);
+      const uint32_t row = min(pc * kVRows + (uint32_t)lane / (kVsW / 4), t - 1);
       __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(vsrc + (size_t)row * kvd),
-                                       (RLH_LDS void*)(vs + pc * 16 * kVsW), 16, 0, 0);
+                                       (RLH_LDS void*)(vs + pc * kVRows * kVsW), 16, 0, 0);
     }
   }
   wait_vmcnt<kVDma>();  // this wave's score rows (and table) have landed
