@@ -723,7 +723,7 @@ __device__ __forceinline__ void mv_block_float(const MvLaunch& L, const MvSeg& g
 
 // The body of one block for weight type TY; NM = 2 in PAIR mode (gate and
 // up share type and tiling).
-template <uint32_t TY, int NM>
+template <uint32_t TY, int NM, bool RING = false>
 __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint32_t blk, lfloat* lds, lfloat* misc,
                                          lu64* exp_tab) {
   if constexpr (TY == RLH_TYPE_F16 || TY == RLH_TYPE_F32 || TY == RLH_TYPE_BF16) {
@@ -773,7 +773,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   // wave 0 has added, and a producer writes round r only once round
   // r - ring has been consumed. Relaxed LDS atomics after lgkmcnt(0), as in
   // the split chain below.
-  const uint32_t ring = NM == 1 ? L.ring : 0u;
+  const uint32_t ring = NM == 1 && RING ? L.ring : 0u;  // RING: the ring plans' own instantiation
   const uint32_t np = ring ? nwaves - 1 : nwaves;           // producer waves
   const uint32_t pw = ring ? wave - 1 : wave;               // producer index (wave 0 of a ring: none)
   const bool producer = !ring || wave != 0;
@@ -947,7 +947,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
 // TY = the weight type of every segment, or 0 for launches that mix types
 // (a switch per block); one instantiation per type keeps each kernel's
 // register allocation to what its own item type needs.
-template <uint32_t TY, int NM>
+template <uint32_t TY, int NM, bool RING = false>
 __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   __shared__ float misc_generic[4 + 64];
@@ -961,20 +961,20 @@ __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
   if (L.nseg > 2 && blockIdx.x >= L.seg[2].blk_begin) g = L.seg[2];
   const uint32_t blk = blockIdx.x - g.blk_begin;
   if constexpr (TY != 0) {
-    mv_block<TY, NM>(L, g, blk, lds, misc, (lu64*)tab_g);
+    mv_block<TY, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g);
   } else {
     switch (g.w.ty) {
-      case RLH_TYPE_Q4_K: mv_block<RLH_TYPE_Q4_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q5_K: mv_block<RLH_TYPE_Q5_K, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q4_1: mv_block<RLH_TYPE_Q4_1, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q5_0: mv_block<RLH_TYPE_Q5_0, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_Q5_1: mv_block<RLH_TYPE_Q5_1, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_F16: mv_block<RLH_TYPE_F16, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_F32: mv_block<RLH_TYPE_F32, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
-      case RLH_TYPE_BF16: mv_block<RLH_TYPE_BF16, NM>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q4_K: mv_block<RLH_TYPE_Q4_K, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q6_K: mv_block<RLH_TYPE_Q6_K, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q8_0: mv_block<RLH_TYPE_Q8_0, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q4_0: mv_block<RLH_TYPE_Q4_0, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_K: mv_block<RLH_TYPE_Q5_K, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q4_1: mv_block<RLH_TYPE_Q4_1, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_0: mv_block<RLH_TYPE_Q5_0, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_Q5_1: mv_block<RLH_TYPE_Q5_1, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_F16: mv_block<RLH_TYPE_F16, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_F32: mv_block<RLH_TYPE_F32, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
+      case RLH_TYPE_BF16: mv_block<RLH_TYPE_BF16, NM, RING>(L, g, blk, lds, misc, (lu64*)tab_g); break;
       default: break;
     }
   }
@@ -982,21 +982,21 @@ __global__ void __launch_bounds__(512) k_mv(MvLaunch L) {
 
 typedef void (*MvKernel)(MvLaunch);
 
-template <int NM>
+template <int NM, bool RING = false>
 MvKernel mv_kernel(uint32_t ty) {
   switch (ty) {
-    case RLH_TYPE_Q4_K: return k_mv<RLH_TYPE_Q4_K, NM>;
-    case RLH_TYPE_Q6_K: return k_mv<RLH_TYPE_Q6_K, NM>;
-    case RLH_TYPE_Q8_0: return k_mv<RLH_TYPE_Q8_0, NM>;
-    case RLH_TYPE_Q4_0: return k_mv<RLH_TYPE_Q4_0, NM>;
-    case RLH_TYPE_Q5_K: return k_mv<RLH_TYPE_Q5_K, NM>;
-    case RLH_TYPE_Q4_1: return k_mv<RLH_TYPE_Q4_1, NM>;
-    case RLH_TYPE_Q5_0: return k_mv<RLH_TYPE_Q5_0, NM>;
-    case RLH_TYPE_Q5_1: return k_mv<RLH_TYPE_Q5_1, NM>;
-    case RLH_TYPE_F16: return k_mv<RLH_TYPE_F16, NM>;
-    case RLH_TYPE_F32: return k_mv<RLH_TYPE_F32, NM>;
-    case RLH_TYPE_BF16: return k_mv<RLH_TYPE_BF16, NM>;
-    default: return k_mv<0, NM>;
+    case RLH_TYPE_Q4_K: return k_mv<RLH_TYPE_Q4_K, NM, RING>;
+    case RLH_TYPE_Q6_K: return k_mv<RLH_TYPE_Q6_K, NM, RING>;
+    case RLH_TYPE_Q8_0: return k_mv<RLH_TYPE_Q8_0, NM, RING>;
+    case RLH_TYPE_Q4_0: return k_mv<RLH_TYPE_Q4_0, NM, RING>;
+    case RLH_TYPE_Q5_K: return k_mv<RLH_TYPE_Q5_K, NM, RING>;
+    case RLH_TYPE_Q4_1: return k_mv<RLH_TYPE_Q4_1, NM, RING>;
+    case RLH_TYPE_Q5_0: return k_mv<RLH_TYPE_Q5_0, NM, RING>;
+    case RLH_TYPE_Q5_1: return k_mv<RLH_TYPE_Q5_1, NM, RING>;
+    case RLH_TYPE_F16: return k_mv<RLH_TYPE_F16, NM, RING>;
+    case RLH_TYPE_F32: return k_mv<RLH_TYPE_F32, NM, RING>;
+    case RLH_TYPE_BF16: return k_mv<RLH_TYPE_BF16, NM, RING>;
+    default: return k_mv<0, NM, RING>;
   }
 }
 
@@ -1032,7 +1032,7 @@ uint32_t plan_waves(const MvPlan& p, uint32_t R, uint32_t tr, uint32_t ntj, uint
 
 // Blocks the GPU holds at once (CUs x blocks per CU) for the plan's single
 // kernel with `threads` per block and `lds` bytes, 0 if unknown.
-uint32_t mv_resident(const MvPlan& p, uint32_t threads, uint32_t lds) {
+uint32_t mv_resident(const MvPlan& p, uint32_t threads, uint32_t lds, bool ring = false) {
   uint32_t ty = p.L.seg[0].w.ty;
   for (uint32_t s = 1; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty != ty) ty = 0;
@@ -1040,7 +1040,8 @@ uint32_t mv_resident(const MvPlan& p, uint32_t threads, uint32_t lds) {
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)mv_kernel<1>(ty), (int)threads, lds) !=
+  const void* k = ring ? (const void*)mv_kernel<1, true>(ty) : (const void*)mv_kernel<1>(ty);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, (int)threads, lds) !=
       hipSuccess)
     return 0;
   return (uint32_t)(cus * per_cu);
@@ -1196,7 +1197,7 @@ bool mv_plan_finish(MvPlan& p) {
     if (force || (s && b > s))
       for (uint32_t np = std::min<uint32_t>(7, ntj); np >= 2 && !ring_np; np--)  // np + 1 <= 8 waves (launch bound)
         if (ring_lds(p, R, np, tj, 2) <= kMaxLds &&
-            (force || mv_resident(p, 64 * (np + 1), ring_lds(p, R, np, tj, 2)) >= b))
+            (force || mv_resident(p, 64 * (np + 1), ring_lds(p, R, np, tj, 2), true) >= b))
           ring_np = np;
   }
   p.L.rows_per_blk = R;
@@ -1240,7 +1241,7 @@ void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start, hipEvent_t 
   uint32_t ty = p.L.seg[0].w.ty;
   for (uint32_t s = 1; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty != ty) ty = 0;
-  const MvKernel k = pair ? mv_kernel<2>(ty) : mv_kernel<1>(ty);
+  const MvKernel k = pair ? mv_kernel<2>(ty) : (p.L.ring ? mv_kernel<1, true>(ty) : mv_kernel<1>(ty));
   if (ev_start || ev_stop)
     hipExtLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, ev_start, ev_stop, 0, p.L);
   else
@@ -1252,7 +1253,7 @@ bool mv_set_max_lds(size_t bytes) {
                           RLH_TYPE_Q5_K, RLH_TYPE_Q4_1, RLH_TYPE_Q5_0, RLH_TYPE_Q5_1, RLH_TYPE_F16,
                           RLH_TYPE_F32,  RLH_TYPE_BF16};
   for (uint32_t ty : tys) {
-    const void* fns[] = {(const void*)mv_kernel<1>(ty), (const void*)mv_kernel<2>(ty)};
+    const void* fns[] = {(const void*)mv_kernel<1>(ty), (const void*)mv_kernel<2>(ty), (const void*)mv_kernel<1, true>(ty)};
     for (const void* f : fns)
       if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess) return false;
   }
