@@ -36,6 +36,9 @@
 
 #include "attention.h"
 #include "rlh_device.h"
+#define RLH_MONO_QUAL __device__ __forceinline__
+#include "monosum.h"
+#include "monosum_wave.h"
 
 namespace rlh {
 
@@ -338,12 +341,112 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
 }
 
 // grid: (H, n_tok); block 256; dynamic LDS: one row of t_max floats.
+// The softmax sum ((0 + e_0) + e_1) + ... of the t non-negative terms in LDS
+// (16-byte aligned), bit for bit as the sequential loop rounds it
+// (ops.rs:408-412), by a block of 256 threads. Thread r takes run r (K
+// consecutive terms, K a multiple of 4), predicts the binade of the running
+// sum at the run's start from an approximate f32 prefix and forms the run's
+// increment pair there (monosum.h). Wave 0 then takes the runs 64 at a
+// time: one scan of their pairs gives every run's exact start inside the
+// current binade; the first run whose prediction misses that binade or
+// whose increments leave it is added with f32 adds from its exact start,
+// and the scan resumes after it (a few runs per row: about one per doubling
+// of the sum). The prediction only chooses between the two paths. Rows with
+// a NaN or infinite term take the plain loop, and so do short rows. Only
+// the decode launch (one row per head) uses it: in prefill the blocks'
+// chains overlap each other, and the walk's LDS and extra work per term
+// made the 32B 4096-token prefill slower (1931 -> 1957 ms); decode at 4.1 K
+// positions gains (96.1 -> 97.6 tok/s). Every thread gets the sum.
+constexpr uint32_t kSoftmaxWalkMin = 1024;  // shorter rows: the plain chain
+struct SoftmaxSumLds {
+  uint32_t a0[256], a1[256];
+  int u[256];
+  float wsum[4];
+  float out;
+};
+__device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* sl) {
+  RLH_LDS SoftmaxSumLds* L = (RLH_LDS SoftmaxSumLds*)sl;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (t < kSoftmaxWalkMin) {
+    if (tid == 0) L->out = seq_sum_lds(e, t);
+    __syncthreads();
+    return L->out;
+  }
+  const uint32_t K = (((t + 255) / 256) + 3) & ~3u;
+  const uint32_t j0 = min(tid * K, t), j1 = min(j0 + K, t);
+  float a = 0.0f;
+  bool bad = false;
+  for (uint32_t j = j0; j < j1; j++) {
+    const float v = e[j];
+    a += v;
+    bad |= !(v < __int_as_float(0x7f800000));
+  }
+  float inc = a;  // the approximate prefix: any order serves
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float v = __shfl_up(inc, o);
+    if ((int)lane >= o) inc += v;
+  }
+  if (lane == 63) L->wsum[wave] = inc;
+  if (__syncthreads_or(bad)) {
+    if (tid == 0) L->out = seq_sum_lds(e, t);
+    __syncthreads();
+    return L->out;
+  }
+  float base = 0.0f;
+  for (uint32_t w = 0; w < wave; w++) base += L->wsum[w];
+  const int ur = mono_binade(base + inc - a);
+  const MonoFn f = mono_run_pair(e + j0, j1 - j0, ur);
+  L->a0[tid] = f.a0;
+  L->a1[tid] = f.a1;
+  L->u[tid] = ur;
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t nr = (t + K - 1) / K;
+    int u = -149;  // the state of the sum 0
+    uint32_t N = 0;
+    for (uint32_t gb = 0; gb < nr; gb += 64) {
+      const uint32_t r = gb + lane;
+      const bool live = r < nr;
+      const MonoFn fr{L->a0[r], L->a1[r]};
+      const int urr = L->u[r];
+      uint32_t l0 = 0;
+      for (;;) {
+        const bool mine = live && lane >= l0;
+        const bool hit = urr == u;
+        const MonoFn g = mine && hit ? fr : mono_identity();
+        const MonoFn incl = wave_scan_fn(g);
+        const uint32_t nl = N + mono_apply(wave_excl_fn(incl), N);
+        const bool stop = mine && (!hit || mono_inc_leaves(nl, mono_apply(fr, nl)));
+        const uint64_t mask = __ballot(stop);
+        if (mask == 0) {
+          N += mono_apply(MonoFn{readlane_u32(incl.a0, 63), readlane_u32(incl.a1, 63)}, N);
+          break;
+        }
+        const uint32_t lc = (uint32_t)__builtin_ctzll(mask);
+        const uint32_t k0 = (gb + lc) * K;
+        const float sv = seq_sum_lds(e + k0, min(t, k0 + K) - k0, mono_value(u, readlane_u32(nl, (int)lc)));
+        mono_state(sv, &u, &N);
+        u = __builtin_amdgcn_readfirstlane(u);
+        N = (uint32_t)__builtin_amdgcn_readfirstlane((int)N);
+        if (lc == 63) break;
+        l0 = lc + 1;
+      }
+    }
+    if (lane == 0) L->out = mono_value(u, N);
+  }
+  __syncthreads();
+  return L->out;
+}
+
+// WALK: the decode launch, whose sum is block_softmax_sum's.
+template <bool WALK>
 __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   __shared__ float red[4];
+  __shared__ uint64_t tab_g[32];
   __shared__ float s_inv;
   __shared__ int s_on;
-  __shared__ uint64_t tab_g[32];
   lu64* tab = (lu64*)tab_g;
   lfloat* e = (lfloat*)lds_generic;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -367,14 +470,23 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   if (x0 != x0) mx = x0;
   for (uint32_t j = tid; j < t; j += 256) e[j] = expf_glibc_t(e[j] - mx, tab);
   __syncthreads();
-  if (tid == 0) {  // the sequential sum of softmax_inplace
-    const float sum = seq_sum_lds(e, t);
-    s_on = sum > 0.0f;
-    s_inv = 1.0f / sum;
+  bool on;
+  float inv;
+  if constexpr (WALK) {
+    __shared__ SoftmaxSumLds ssl;  // only in the decode instantiation
+    const float sum = block_softmax_sum(e, t, &ssl);  // the sequential sum of softmax_inplace
+    on = sum > 0.0f;
+    inv = 1.0f / sum;
+  } else {
+    if (tid == 0) {  // the sequential sum of softmax_inplace
+      const float sum = seq_sum_lds(e, t);
+      s_on = sum > 0.0f;
+      s_inv = 1.0f / sum;
+    }
+    __syncthreads();
+    on = s_on;
+    inv = s_inv;
   }
-  __syncthreads();
-  const bool on = s_on;
-  const float inv = s_inv;
   for (uint32_t j = tid; j < t; j += 256) {
     const float v = e[j];
     row[j] = on ? v * inv : v;
@@ -1062,7 +1174,10 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
 }
 
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
-  hipLaunchKernelGGL(k_attn_softmax, dim3(a.H, a.n_tok), dim3(256), softmax_lds(a.t_max), st, a);
+  if (a.n_tok == 1)
+    hipLaunchKernelGGL(k_attn_softmax<true>, dim3(a.H, 1), dim3(256), softmax_lds(a.t_max), st, a);
+  else
+    hipLaunchKernelGGL(k_attn_softmax<false>, dim3(a.H, a.n_tok), dim3(256), softmax_lds(a.t_max), st, a);
 }
 
 size_t attn_dec_fused_lds(uint32_t t_max, uint32_t group) {
@@ -1111,7 +1226,9 @@ bool attn_init(uint32_t max_ctx) {
   if (max_ctx > kAttnMaxCtx) return false;
   size_t ring_lds = 0;
   for (uint32_t gq = 1; gq <= (uint32_t)kAttnMaxGroup; gq++) ring_lds = std::max(ring_lds, pv_ring_lds(gq));
-  return hipFuncSetAttribute((const void*)k_attn_softmax, hipFuncAttributeMaxDynamicSharedMemorySize,
+  return hipFuncSetAttribute((const void*)k_attn_softmax<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_softmax<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_smpv_dec, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)kDecFusedLds) == hipSuccess &&

@@ -114,3 +114,26 @@ RLH_MONO_QUAL bool mono_dec_leaves(int u, uint32_t n, uint32_t dec) {
   const uint32_t floor_n = u == -149 ? 0u : (RLH_MONO_TOP >> 1);
   return dec >= n - floor_n;
 }
+
+// The softmax-sum walk (the attention softmax's sum over positions): the
+// terms are split into runs; each run's pair is made at the binade that an
+// approximate prefix sum predicts for its start (mono_binade of that
+// estimate). Walking the runs in order, a run's pair applies when the exact
+// state lies in that binade and the run does not leave it; otherwise its
+// terms are added with f32 adds from mono_value(u, N) and the new state is
+// taken with mono_state. The prediction only chooses between the two
+// paths, never the result.
+RLH_MONO_QUAL int mono_binade(float s) {
+  int u;
+  uint32_t n;
+  mono_state(s, &u, &n);
+  return u;
+}
+
+template <typename P>
+RLH_MONO_QUAL MonoFn mono_run_pair(P x, uint32_t k, int u) {
+  MonoFn f = mono_identity();
+  for (uint32_t i = 0; i < k; i++) f = mono_then(f, mono_elem(x[i], u));
+  return f;
+}
+

@@ -7,6 +7,14 @@
 //               exclusive scan of increment pairs; the first lane that may
 //               leave the binade or reach the stop threshold replays its
 //               terms with real f32 steps; the next pass starts after it.
+// shim_softwalk: the attention softmax's sum (block_softmax_sum): 256 runs
+//               of K terms (K a multiple of 4), each run's pair at the
+//               binade its approximate f32 prefix predicts (mode 1 / 2 move
+//               every prediction one binade up / down, mode 3 alternates, to
+//               force the replay path); the runs are taken 64 at a time: a
+//               scan of their pairs at the current binade, the first run that
+//               misses it or may leave it replayed with f32 adds, the scan
+//               resumed after it.
 // shim_runwalk: k_run_pairs + k_run_walk — runs of R terms with pairs at the
 //               three candidate binades from the f64 prefix estimate, walked
 //               T runs per pass; the first run that may leave the binade, or
@@ -225,6 +233,66 @@ uint32_t shim_runwalk(int dec, const float* y, uint32_t len, float s0, int T, in
   }
   *val = s;
   return len;
+}
+
+uint32_t shim_softwalk(const float* x, uint32_t n, int mode, float* out, uint64_t* replays) {
+  const uint32_t K = (((n + 255) / 256) + 3) & ~3u;
+  const uint32_t nr = (n + K - 1) / K;
+  std::vector<float> loc(nr), pre(nr);
+  std::vector<MonoFn> f(nr);
+  std::vector<int> ur(nr);
+  for (uint32_t r = 0; r < nr; r++) {
+    float a = 0.0f;
+    for (uint32_t j = r * K; j < std::min(n, r * K + K); j++) a += x[j];
+    loc[r] = a;
+  }
+  float acc = 0.0f;  // approximate exclusive prefix (any order would do)
+  for (uint32_t r = 0; r < nr; r++) {
+    pre[r] = acc;
+    acc += loc[r];
+    ur[r] = mono_binade(pre[r]);
+    if (mode == 1 || (mode == 3 && (r & 1))) ur[r] += 1;
+    if (mode == 2 || (mode == 3 && !(r & 1))) ur[r] -= 1;
+    const uint32_t j0 = r * K;
+    f[r] = mono_run_pair(x + j0, std::min(n, j0 + K) - j0, ur[r]);
+  }
+  int u = -149;
+  uint32_t N = 0;
+  *replays = 0;
+  for (uint32_t gb = 0; gb < nr; gb += 64) {
+    const uint32_t gl = std::min<uint32_t>(64, nr - gb);
+    uint32_t l0 = 0;
+    while (l0 < gl) {
+      // the scan: lanes l0.. in order, each run's start state while every run
+      // before it hits the binade and stays in it
+      MonoFn pre_f = mono_identity();
+      uint32_t lc = gl;
+      uint32_t nl_c = 0;
+      for (uint32_t l = l0; l < gl; l++) {
+        const uint32_t r = gb + l;
+        const uint32_t nl = N + mono_apply(pre_f, N);
+        const bool hit = ur[r] == u;
+        if (!hit || mono_inc_leaves(nl, mono_apply(f[r], nl))) {
+          lc = l;
+          nl_c = nl;
+          break;
+        }
+        pre_f = mono_then(pre_f, f[r]);
+      }
+      if (lc == gl) {
+        N += mono_apply(pre_f, N);
+        break;
+      }
+      const uint32_t k0 = (gb + lc) * K;
+      float sv = mono_value(u, nl_c);
+      for (uint32_t j = k0; j < std::min(n, k0 + K); j++) sv = sv + x[j];
+      mono_state(sv, &u, &N);
+      ++*replays;
+      l0 = lc + 1;
+    }
+  }
+  *out = mono_value(u, N);
+  return nr;
 }
 
 }  // extern "C"

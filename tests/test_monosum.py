@@ -39,6 +39,8 @@ def shim(tmp_path_factory):
     lib.shim_chain.restype = ctypes.c_uint32
     lib.shim_chain.argtypes = [ctypes.c_int, F32P, ctypes.c_uint32, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                ctypes.c_int, ctypes.c_float, F32P, ctypes.POINTER(ctypes.c_uint64)]
+    lib.shim_softwalk.restype = ctypes.c_uint32
+    lib.shim_softwalk.argtypes = [F32P, ctypes.c_uint32, ctypes.c_int, F32P, ctypes.POINTER(ctypes.c_uint64)]
     lib.shim_runwalk.restype = ctypes.c_uint32
     lib.shim_runwalk.argtypes = [ctypes.c_int, F32P, ctypes.c_uint32, ctypes.c_float, ctypes.c_int, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_float, ctypes.c_int, F32P, ctypes.POINTER(ctypes.c_uint64),
@@ -129,6 +131,28 @@ def test_run_walk_equals_sequential(shim, T, R, shift):
         for s0 in [float(np.float32(rng.random()) * total) for _ in range(3)] + [float(total), 0.0, 0.5]:
             j1, j2, b1, b2, _ = _run(shim, 1, p, s0, 2, 0.0, T, 0, (R, shift))
             assert (j1, b1) == (j2, b2), (name, s0)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2, 3])
+def test_softmax_walk_equals_sequential(shim, mode):
+    """The attention softmax's sum (block_softmax_sum in attention.hip):
+    256 runs with pairs at predicted binades, scanned 64 at a time, the
+    first miss replayed with f32 adds (modes 1-3 shift every prediction to
+    force replays): equal bits to the plain loop; with true predictions
+    few runs are replayed."""
+    rng = np.random.default_rng(11)
+    extra = [("softmax_4k%g" % sc, _softmax_terms(rng, 4160, sc)) for sc in (0.5, 4.0, 30.0)]
+    for name, y in _cases() + extra + [("short", np.float32([0.25, 1.0, 3e-8])), ("one", np.float32([0.7]))]:
+        seq = np.float32(0)
+        for v in y:
+            seq = np.float32(seq + v)
+        out, rep = ctypes.c_float(), ctypes.c_uint64()
+        nr = shim.shim_softwalk(y.ctypes.data_as(F32P), len(y), mode, ctypes.byref(out), ctypes.byref(rep))
+        assert np.float32(out.value).view(np.uint32) == seq.view(np.uint32), (name, mode)
+        if mode == 1:
+            assert rep.value == nr, name  # every prediction misses
+        if mode == 0 and name.startswith("softmax"):
+            assert rep.value < nr // 8, (name, rep.value)
 
 
 @pytest.mark.parametrize("T,E", SHAPES)
