@@ -357,6 +357,50 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
 // chains overlap each other, and the walk's LDS and extra work per term
 // made the 32B 4096-token prefill slower (1931 -> 1957 ms); decode at 4.1 K
 // positions gains (96.1 -> 97.6 tok/s). Every thread gets the sum.
+// One wave walks nr runs of K terms in order (run r: e[r K, min(t, (r + 1) K)),
+// its pair A0[r], A1[r] made at binade U[r]): a DPP scan of 64 runs' pairs
+// at a time from the exact state; the first run whose binade was mispredicted
+// or whose increments leave the binade is added with f32 adds from its exact
+// start and the scan resumes after it. Every lane returns the sum. Each
+// pass either ends its 64 runs or moves l0 past the replayed run, so the
+// walk ends.
+__device__ float wave_walk_runs(const lfloat* e, uint32_t t, uint32_t K, uint32_t nr, const RLH_LDS uint32_t* A0,
+                                const RLH_LDS uint32_t* A1, const RLH_LDS int* U) {
+  const uint32_t lane = threadIdx.x & 63;
+  int u = -149;  // the state of the sum 0
+  uint32_t N = 0;
+  for (uint32_t gb = 0; gb < nr; gb += 64) {
+    const uint32_t r = gb + lane;
+    const bool live = r < nr;
+    const uint32_t rc = live ? r : nr - 1;
+    const MonoFn fr{A0[rc], A1[rc]};
+    const int urr = U[rc];
+    uint32_t l0 = 0;
+    for (;;) {
+      const bool mine = live && lane >= l0;
+      const bool hit = urr == u;
+      const MonoFn g = mine && hit ? fr : mono_identity();
+      const MonoFn incl = wave_scan_fn(g);
+      const uint32_t nl = N + mono_apply(wave_excl_fn(incl), N);
+      const bool stop = mine && (!hit || mono_inc_leaves(nl, mono_apply(fr, nl)));
+      const uint64_t mask = __ballot(stop);
+      if (mask == 0) {
+        N += mono_apply(MonoFn{readlane_u32(incl.a0, 63), readlane_u32(incl.a1, 63)}, N);
+        break;
+      }
+      const uint32_t lc = (uint32_t)__builtin_ctzll(mask);
+      const uint32_t k0 = (gb + lc) * K;
+      const float sv = seq_sum_lds(e + k0, min(t, k0 + K) - k0, mono_value(u, readlane_u32(nl, (int)lc)));
+      mono_state(sv, &u, &N);
+      u = __builtin_amdgcn_readfirstlane(u);
+      N = (uint32_t)__builtin_amdgcn_readfirstlane((int)N);
+      if (lc == 63) break;
+      l0 = lc + 1;
+    }
+  }
+  return mono_value(u, N);
+}
+
 constexpr uint32_t kSoftmaxWalkMin = 1024;  // shorter rows: the plain chain
 struct SoftmaxSumLds {
   uint32_t a0[256], a1[256];
@@ -402,38 +446,8 @@ __device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* s
   L->u[tid] = ur;
   __syncthreads();
   if (wave == 0) {
-    const uint32_t nr = (t + K - 1) / K;
-    int u = -149;  // the state of the sum 0
-    uint32_t N = 0;
-    for (uint32_t gb = 0; gb < nr; gb += 64) {
-      const uint32_t r = gb + lane;
-      const bool live = r < nr;
-      const MonoFn fr{L->a0[r], L->a1[r]};
-      const int urr = L->u[r];
-      uint32_t l0 = 0;
-      for (;;) {
-        const bool mine = live && lane >= l0;
-        const bool hit = urr == u;
-        const MonoFn g = mine && hit ? fr : mono_identity();
-        const MonoFn incl = wave_scan_fn(g);
-        const uint32_t nl = N + mono_apply(wave_excl_fn(incl), N);
-        const bool stop = mine && (!hit || mono_inc_leaves(nl, mono_apply(fr, nl)));
-        const uint64_t mask = __ballot(stop);
-        if (mask == 0) {
-          N += mono_apply(MonoFn{readlane_u32(incl.a0, 63), readlane_u32(incl.a1, 63)}, N);
-          break;
-        }
-        const uint32_t lc = (uint32_t)__builtin_ctzll(mask);
-        const uint32_t k0 = (gb + lc) * K;
-        const float sv = seq_sum_lds(e + k0, min(t, k0 + K) - k0, mono_value(u, readlane_u32(nl, (int)lc)));
-        mono_state(sv, &u, &N);
-        u = __builtin_amdgcn_readfirstlane(u);
-        N = (uint32_t)__builtin_amdgcn_readfirstlane((int)N);
-        if (lc == 63) break;
-        l0 = lc + 1;
-      }
-    }
-    if (lane == 0) L->out = mono_value(u, N);
+    const float sum = wave_walk_runs(e, t, K, (t + K - 1) / K, L->a0, L->a1, L->u);
+    if (lane == 0) L->out = sum;
   }
   __syncthreads();
   return L->out;
