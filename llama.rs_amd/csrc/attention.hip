@@ -340,23 +340,6 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
   }
 }
 
-// grid: (H, n_tok); block 256; dynamic LDS: one row of t_max floats.
-// The softmax sum ((0 + e_0) + e_1) + ... of the t non-negative terms in LDS
-// (16-byte aligned), bit for bit as the sequential loop rounds it
-// (ops.rs:408-412), by a block of 256 threads. Thread r takes run r (K
-// consecutive terms, K a multiple of 4), predicts the binade of the running
-// sum at the run's start from an approximate f32 prefix and forms the run's
-// increment pair there (monosum.h). Wave 0 then takes the runs 64 at a
-// time: one scan of their pairs gives every run's exact start inside the
-// current binade; the first run whose prediction misses that binade or
-// whose increments leave it is added with f32 adds from its exact start,
-// and the scan resumes after it (a few runs per row: about one per doubling
-// of the sum). The prediction only chooses between the two paths. Rows with
-// a NaN or infinite term take the plain loop, and so do short rows. Only
-// the decode launch (one row per head) uses it: in prefill the blocks'
-// chains overlap each other, and the walk's LDS and extra work per term
-// made the 32B 4096-token prefill slower (1931 -> 1957 ms); decode at 4.1 K
-// positions gains (96.1 -> 97.6 tok/s). Every thread gets the sum.
 // One wave walks nr runs of K terms in order (run r: e[r K, min(t, (r + 1) K)),
 // its pair A0[r], A1[r] made at binade U[r]): a DPP scan of 64 runs' pairs
 // at a time from the exact state; the first run whose binade was mispredicted
@@ -401,6 +384,23 @@ __device__ float wave_walk_runs(const lfloat* e, uint32_t t, uint32_t K, uint32_
   return mono_value(u, N);
 }
 
+// grid: (H, n_tok); block 256; dynamic LDS: one row of t_max floats.
+// The softmax sum ((0 + e_0) + e_1) + ... of the t non-negative terms in LDS
+// (16-byte aligned), bit for bit as the sequential loop rounds it
+// (ops.rs:408-412), by a block of 256 threads. Thread r takes run r (K
+// consecutive terms, K a multiple of 4), predicts the binade of the running
+// sum at the run's start from an approximate f32 prefix and forms the run's
+// increment pair there (monosum.h). Wave 0 then takes the runs 64 at a
+// time: one scan of their pairs gives every run's exact start inside the
+// current binade; the first run whose prediction misses that binade or
+// whose increments leave it is added with f32 adds from its exact start,
+// and the scan resumes after it (a few runs per row: about one per doubling
+// of the sum). The prediction only chooses between the two paths. Rows with
+// a NaN or infinite term take the plain loop, and so do short rows. Only
+// the decode launch (one row per head) uses it: in prefill the blocks'
+// chains overlap each other, and the walk's LDS and extra work per term
+// made the 32B 4096-token prefill slower (1931 -> 1957 ms); decode at 4.1 K
+// positions gains (96.1 -> 97.6 tok/s). Every thread gets the sum.
 constexpr uint32_t kSoftmaxWalkMin = 1024;  // shorter rows: the plain chain
 struct SoftmaxSumLds {
   uint32_t a0[256], a1[256];
