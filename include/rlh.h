@@ -100,6 +100,13 @@ uint64_t rlh_row_bytes(uint32_t ggml_type, uint64_t cols);
 /* ---- model ---------------------------------------------------------------
  * Replaces Model::load (src/model.rs:150-239): the caller resolves tensors
  * (from GGUF or a generator) and hands them over one by one. */
+/* Whether this path runs a model of this config, without a device: RLH_OK,
+ * RLH_EINVAL (zero dimensions, n_head not a multiple of n_head_kv) or
+ * RLH_EUNSUP with the reason (head_dim other than 128, n_embd or n_ff not a
+ * multiple of 256, more than 8 query heads per KV head). The reference's
+ * read_config (src/model.rs:241-293) accepts these shapes; rlh_model_create
+ * and rlh_model_load_gguf apply this check before anything is uploaded. */
+int rlh_config_check(const rlh_config* cfg);
 int rlh_model_create(const rlh_config* cfg, rlh_model** out);
 /* Copies one tensor to device memory (the host bytes are borrowed only for
  * the call, as Tensor borrows the mmap, src/tensor.rs:6-35). Norm and bias
@@ -181,6 +188,23 @@ int rlh_gguf_writer_set_array(rlh_gguf_writer* w, const char* key, uint32_t elem
 int rlh_gguf_writer_add_tensor(rlh_gguf_writer* w, const char* name, uint32_t ggml_type, uint32_t n_dims,
                                const uint64_t* dims, const void* data, uint64_t nbytes);
 int rlh_gguf_writer_write(rlh_gguf_writer* w, const char* path);
+
+/* Vocabulary pruning (prune::prune_vocab, src/prune.rs:127-291): rewrites
+ * in_path (split files included) to out_path keeping every unknown,
+ * control, user-defined and byte token, every token a *_token_id key names,
+ * and the tokens whose text has no character of the dropped scripts (the
+ * reference's table of ranges: Cyrillic, CJK, Indic, ...); the rows of
+ * token_embd / output that have one row per token, the merges whose parts
+ * and result survive, and every *_token_id value remapped (as u32). All
+ * other metadata and tensors are copied. RLH_EFORMAT ("prune: ...") for a
+ * missing vocabulary, a token_type array of another length, an empty result
+ * or a named token that was dropped. `stats` (nullable) receives the counts
+ * of PruneStats. */
+typedef struct rlh_prune_stats {
+  uint64_t old_vocab, new_vocab, kept_special, kept_byte, kept_normal, dropped;
+  uint64_t merges_old, merges_new, embd_bytes_saved, out_bytes;
+} rlh_prune_stats;
+int rlh_prune_vocab(const char* in_path, const char* out_path, rlh_prune_stats* stats);
 
 /* ---- tokenizer and chat template ---------------------------------------------
  * The reference's byte-level BPE tokenizer (GPT-2 / Qwen2 flavour,
@@ -358,11 +382,11 @@ int rlh_matmul_batch(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t 
 int rlh_block_dots(uint32_t ggml_type, const void* w, uint64_t rows, uint64_t cols, const int8_t* q8, int32_t* out);
 
 /* ---- greedy argmax without allocation -----------------------------------------------
- * The greedy argmax of rlh_greedy_next (main.rs:453-463 semantics: lowest
- * index among equal maxima, NaN never wins, 0 when no value exceeds -inf)
- * over n floats the caller already holds in device memory, written to the
- * device word *token. No counterpart in the reference: for callers that
- * cannot allocate (code under HIP graph capture, tight serving loops).
+ * The greedy argmax over n floats the caller already holds in device
+ * memory, written to the device word *token: the lowest index among equal
+ * maxima wins, a NaN never wins, and the token is 0 when no value exceeds
+ * -inf. No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops).
  * Allocates nothing and does not synchronize: the two kernels are enqueued
  * on `stream` (a hipStream_t, NULL for the null stream) and the token is
  * valid once the stream reaches them. Their 256 partial (value, index)

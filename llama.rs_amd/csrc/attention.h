@@ -29,6 +29,7 @@ struct AttnArgs {
   float eps, scale;
   float* out;    // [n_tok][H*128]
   Q8Mut out_q8;  // Q8 blocks of out
+  uint32_t* err; // device error word (nullable): an expired bounded wait sets kErrAttnExp
 };
 
 // Query heads per KV head the kernels accept (1..8).

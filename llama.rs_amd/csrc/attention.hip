@@ -888,9 +888,7 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   } else if (tid < G) {  // the G sequential sums side by side, one lane each
     float sum = 0.0f;
     for (uint32_t k = 0; k < nek; k++) {
-      while (__hip_atomic_load(exp_done + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < 7u)
-        __builtin_amdgcn_s_sleep(1);
-      asm volatile("" ::: "memory");
+      wait_lds_count(exp_done + k, 7u, a.err, kErrAttnExp);
       const uint32_t n = t - k * kExpC < kExpC ? t - k * kExpC : kExpC;
       sum = seq_sum_lds(e + tid * RS + k * kExpC, n, sum);
     }

@@ -298,7 +298,7 @@ struct rlh_cache {
   float* scores = nullptr;  // attention scores [H][max_ctx]
   Q8Buf act_e{}, act_q{}, act_f{};
   // step state (device): tok, pos, step, argmax out
-  uint32_t* st_dev = nullptr;  // [0]=tok [1]=pos [2]=step [3]=argmax
+  uint32_t* st_dev = nullptr;  // [0]=tok [1]=pos [2]=step [3]=argmax [4]=wait error flags (kErr*)
   uint32_t* hist = nullptr;    // greedy history [max_ctx + 1]
   float* pv = nullptr;
   uint32_t* pi = nullptr;
@@ -342,6 +342,23 @@ float* layer_v(rlh_cache* c, uint32_t l) {
 
 enum StepKind { STEP_NOLOGITS = 0, STEP_LOGITS = 1, STEP_GREEDY = 2 };
 
+// The cache's device error word: the kernels' bounded intra-block waits set
+// a bit here when one expires (kErrMvRing, kErrMvSplit, kErrAttnExp).
+uint32_t* err_word(rlh_cache* c) { return c->st_dev + 4; }
+
+// Waits for the cache's stream and reports an expired device wait of any
+// kernel enqueued since the last reset. The flags stay set (every later
+// step fails too) until rlh_cache_reset: the K/V rows and logits of such a
+// step are not the reference's values.
+int sync_checked(rlh_cache* c) {
+  HIPCHK(hipMemcpyAsync(c->host_st + 4, err_word(c), 4, hipMemcpyDeviceToHost, c->st));
+  HIPCHK(hipStreamSynchronize(c->st));
+  if (c->host_st[4] != 0)
+    return fail(RLH_EDEVICE, "a bounded device wait expired (flags 0x" + std::to_string(c->host_st[4]) +
+                                 "); the cache holds undefined values until rlh_cache_reset");
+  return RLH_OK;
+}
+
 // The matvec launch of weight kind `kind` (the kind that names its launch:
 // RLH_T_ATTN_Q for q/k/v, RLH_T_FFN_GATE for gate/up, RLH_T_OUTPUT for the
 // logits) with the probe's next event pair when a probe of that kind runs.
@@ -352,7 +369,7 @@ void mv_launch_probed(rlh_cache* c, int kind, const MvPlan& p) {
     e1 = c->probe_ev[2 * c->probe_used + 1];
     c->probe_used++;
   }
-  mv_launch(c->st, p, e0, e1);
+  mv_launch(c->st, p, err_word(c), e0, e1);
 }
 
 // Decode attention writes only f32 (its kernels split the head dimension in
@@ -417,6 +434,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       a.t_max = (uint32_t)c->max_ctx;
       a.max_ctx = (uint32_t)c->max_ctx;
       a.n_tok = 1;
+      a.err = err_word(c);
       a.H = (int)H;
       a.KVH = (int)KVH;
       a.eps = eps;
@@ -538,19 +556,35 @@ uint64_t rlh_row_bytes(uint32_t ty, uint64_t cols) {
   return (uint64_t)type_size(ty) * (cols / (uint64_t)bs);
 }
 
-int rlh_model_create(const rlh_config* cfg, rlh_model** out) {
-  if (!cfg || !out) return fail(RLH_EINVAL, "null argument");
-  *out = nullptr;
-  int rc = ensure_device();
-  if (rc) return rc;
+int rlh_config_check(const rlh_config* cfg) {
+  if (!cfg) return fail(RLH_EINVAL, "null argument");
   if (cfg->n_layer == 0 || cfg->n_embd == 0 || cfg->n_head == 0 || cfg->n_head_kv == 0 || cfg->n_ff == 0 ||
       cfg->vocab_size == 0)
     return fail(RLH_EINVAL, "config has a zero dimension");
-  if (cfg->head_dim != 128)
-    return fail(RLH_EUNSUP, "head_dim " + std::to_string(cfg->head_dim) + " (this path implements head_dim 128)");
   if (cfg->n_head % cfg->n_head_kv != 0) return fail(RLH_EINVAL, "n_head must be a multiple of n_head_kv");
+  // Shapes the reference runs (model.rs:249-268 reads any head_dim; rows of
+  // any whole number of blocks, tensor.rs:28-30) that this path refuses up
+  // front, before any tensor is read or uploaded:
+  if (cfg->head_dim != 128)
+    return fail(RLH_EUNSUP, "head_dim " + std::to_string(cfg->head_dim) +
+                                ": the attention kernels are built for 128-value heads (one K/V row per lane pair "
+                                "of 64, the NeoX RoPE table of 64 pairs), as Qwen3 and Qwen2.5 from 1.5B up use; "
+                                "Qwen2.5-0.5B-shaped models (head_dim 64) are not supported on this path");
   if (cfg->n_embd % 256 != 0 || cfg->n_ff % 256 != 0)
-    return fail(RLH_EUNSUP, "n_embd and n_ff must be multiples of 256");
+    return fail(RLH_EUNSUP, "n_embd " + std::to_string(cfg->n_embd) + " / n_ff " + std::to_string(cfg->n_ff) +
+                                ": the device weight layout tiles rows in 256-value items, so n_embd and n_ff "
+                                "must be multiples of 256");
+  if (cfg->n_head / cfg->n_head_kv > (uint32_t)kAttnMaxGroup)
+    return fail(RLH_EUNSUP, "more than 8 query heads per KV head");
+  return RLH_OK;
+}
+
+int rlh_model_create(const rlh_config* cfg, rlh_model** out) {
+  if (!cfg || !out) return fail(RLH_EINVAL, "null argument");
+  *out = nullptr;
+  int rc = rlh_config_check(cfg);
+  if (rc) return rc;
+  if ((rc = ensure_device())) return rc;
   rlh_model* m = new rlh_model();
   m->cfg = *cfg;
   m->layers.resize(cfg->n_layer);
@@ -834,6 +868,9 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
 
 int rlh_cache_reset(rlh_cache* c) {
   if (!c) return fail(RLH_EINVAL, "null cache");
+  HIPCHK(hipStreamSynchronize(c->st));
+  c->host_st[4] = 0;  // clear the wait error flags
+  HIPCHK(hipMemcpyAsync(err_word(c), c->host_st + 4, 4, hipMemcpyHostToDevice, c->st));
   c->len = 0;
   c->logits_valid = false;
   return RLH_OK;
@@ -866,8 +903,7 @@ static int check_forward_args(rlh_model* m, rlh_cache* c) {
 static int copy_logits(rlh_cache* c, float* logits) {
   if (logits)
     HIPCHK(hipMemcpyAsync(logits, c->logits, (size_t)c->m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, c->st));
-  HIPCHK(hipStreamSynchronize(c->st));
-  return RLH_OK;
+  return sync_checked(c);
 }
 
 int rlh_forward_one(rlh_model* m, rlh_cache* c, uint32_t token, uint64_t pos, float* logits) {
@@ -984,6 +1020,7 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       a.scale = scale;
       a.out = c->attnb;
       a.out_q8 = c->act_qb;
+      a.err = err_word(c);
       launch_attn_scores(st, a, false);
       launch_attn_softmax(st, a);
       launch_attn_pv(st, a, false);
@@ -1012,7 +1049,7 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
   mv_plan_set_f32(p, c->scratch);
   mv_plan_add(p, ow.dm, c->logits, nullptr);
   mv_plan_finish(p);
-  mv_launch(st, p);
+  mv_launch(st, p, err_word(c));
   HIPCHK(hipGetLastError());
   return RLH_OK;
 }
@@ -1103,7 +1140,7 @@ int rlh_generate_greedy(rlh_model* m, rlh_cache* c, uint32_t first, uint64_t n_s
   for (uint64_t i = 0; i < n; i++)
     if ((rc = run_step(c, STEP_GREEDY, (int64_t)i))) return rc;
   HIPCHK(hipMemcpyAsync(out_tokens, c->hist, (n + 1) * 4, hipMemcpyDeviceToHost, c->st));
-  HIPCHK(hipStreamSynchronize(c->st));
+  if ((rc = sync_checked(c))) return rc;
   c->len += n;
   if (n > 0) {
     c->logits_valid = true;
@@ -1196,8 +1233,9 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
   DevBuf<float> dx, dy, dd;
   DevBuf<int8_t> dq;
   DevBuf<int32_t> ds, ds16;
+  DevBuf<uint32_t> derr;
   if (dx.alloc(cols) || dy.alloc(rows) || dq.alloc(cols) || dd.alloc(cols / 32) || ds.alloc(cols / 32) ||
-      ds16.alloc(cols / 16)) {
+      ds16.alloc(cols / 16) || derr.alloc(1) || hipMemset(derr.p, 0, 4)) {
     free_tensor(t);
     return fail(RLH_ENOMEM, "hipMalloc");
   }
@@ -1212,12 +1250,15 @@ int rlh_matvec(uint32_t ty, const void* w, uint64_t rows, uint64_t cols, const f
   }
   hipError_t e = hipMemcpyAsync(dx.p, x, cols * 4, hipMemcpyHostToDevice, st);
   launch_quantize_q8(st, dx.p, (uint32_t)cols, act);  // quantize_q8 once (ops.rs:104)
-  mv_launch(st, p);
+  mv_launch(st, p, derr.p);
+  uint32_t werr = 0;
   if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(y, dy.p, rows * 4, hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipMemcpyAsync(&werr, derr.p, 4, hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
   free_tensor(t);
   if (e != hipSuccess) return fail(RLH_EDEVICE, hipGetErrorString(e));
+  if (werr) return fail(RLH_EDEVICE, "a bounded device wait of the matvec expired (flags " + std::to_string(werr) + ")");
   return RLH_OK;
 }
 
@@ -1357,9 +1398,9 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   hipEvent_t e0, e1;
   HIPCHK(hipEventCreate(&e0));
   HIPCHK(hipEventCreate(&e1));
-  mv_launch(c->st, plans[0]);  // warm-up
+  mv_launch(c->st, plans[0], err_word(c));  // warm-up
   (void)hipEventRecord(e0, c->st);
-  for (int i = 0; i < iters; i++) mv_launch(c->st, plans[i % plans.size()]);
+  for (int i = 0; i < iters; i++) mv_launch(c->st, plans[i % plans.size()], err_word(c));
   (void)hipEventRecord(e1, c->st);
   hipError_t e = hipEventSynchronize(e1);
   float ms = 0.f;
@@ -1367,6 +1408,7 @@ int rlh_profile_matvec(rlh_model* m, rlh_cache* c, int kind, int iters, double* 
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("profile events: ") + hipGetErrorString(e));
+  if ((rc = sync_checked(c))) return rc;
   const double total_ms = ms;
   *avg_us = total_ms * 1000.0 / iters;
   return RLH_OK;
@@ -1392,7 +1434,10 @@ void* g_scratch_dev[kMaxDevices] = {};
 // with that device current; host code uses only this address).
 int noalloc_scratch(void** out) {
   int dev = -1;
-  HIPCHK(hipGetDevice(&dev));
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(RLH_EDEVICE, "no HIP device available (librlh needs an MI355X / gfx950 GPU)");
+  }
   if (dev < 0 || dev >= kMaxDevices) return fail(RLH_EDEVICE, "device ordinal out of range");
   std::lock_guard<std::mutex> lk(g_scratch_mu);
   if (!g_scratch_dev[dev]) {
@@ -1424,12 +1469,13 @@ int rlh_argmax_noalloc(const float* logits, uint64_t n, uint32_t* token, void* s
   if (!logits || !token) return fail(RLH_EINVAL, "null argument");
   if (n == 0 || n > kNoAllocMaxN)
     return fail(RLH_EINVAL, "n = " + std::to_string(n) + " is outside [1, " + std::to_string(kNoAllocMaxN) + "]");
-  int rc = ensure_device();
+  // only calls that are legal under stream capture: the current device, the
+  // pointers' attributes and (once per device) the scratch array's address
+  void* sp = nullptr;
+  int rc = noalloc_scratch(&sp);
   if (rc) return rc;
   if (!device_accessible(logits) || !device_accessible(token))
     return fail(RLH_EINVAL, "logits and token must be device-accessible memory");
-  void* sp = nullptr;
-  if ((rc = noalloc_scratch(&sp))) return rc;
   float* pv = (float*)sp;
   uint32_t* pi = (uint32_t*)sp + kNoAllocParts;
   launch_argmax((hipStream_t)stream, logits, (uint32_t)n, pv, pi, kNoAllocParts, token, nullptr, nullptr, nullptr);
@@ -1485,6 +1531,7 @@ int rlh_profile_decode_kernel(rlh_model* m, rlh_cache* c, int kind, uint32_t fir
   const uint32_t used = c->probe_used;
   release();
   if (e != hipSuccess) return fail(RLH_EDEVICE, std::string("kernel probe: ") + hipGetErrorString(e));
+  if ((rc = sync_checked(c))) return rc;
   c->len += (uint64_t)steps;
   c->logits_valid = true;
   *avg_us = used ? total_ms * 1000.0 / used : 0.0;
@@ -1515,6 +1562,7 @@ int rlh_profile_decode(rlh_model* m, rlh_cache* c, int iters, double* avg_us) {
   HIPCHK(hipEventElapsedTime(&ms, e0, e1));
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
+  if ((rc = sync_checked(c))) return rc;
   c->len += (uint64_t)iters;
   c->logits_valid = true;
   *avg_us = (double)ms * 1000.0 / iters;

@@ -21,6 +21,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <list>
 #include <map>
 #include <string>
 #include <unordered_map>
@@ -540,6 +541,8 @@ int rlh_model_load_gguf(const rlh_gguf* g, rlh_model** out) {
   rlh_config cfg{};
   int rc = rlh_gguf_config(g, &cfg, nullptr, 0);
   if (rc) return rc;
+  // shapes the device path cannot run are refused before anything is read
+  if ((rc = rlh_config_check(&cfg))) return rc;
   // Model::read_tokenizer requires the vocabulary (model.rs:295-300)
   const Meta* toks = find_meta(g, "tokenizer.ggml.tokens");
   if (!toks || toks->type != V_ARR || toks->elem != V_STR)
@@ -806,6 +809,277 @@ int rlh_gguf_writer_write(rlh_gguf_writer* w, const char* path) {
   }
   const bool ok = o.ok && std::fclose(f) == 0;
   if (!ok) return set_error(RLH_EIO, ("write to '" + std::string(path) + "' failed").c_str());
+  return RLH_OK;
+}
+
+}  // extern "C"
+
+// ---- prune_vocab (src/prune.rs:127-291) ---------------------------------------
+// Rewrites a GGUF file keeping only the vocabulary of a Latin + Arabic/Persian
+// (+ symbols, emoji) deployment, with the matching rows of the vocabulary-sized
+// tensors (token_embd, output): the model then decodes over a smaller logits
+// matrix. Host code; the pruned file loads like any other.
+
+namespace {
+
+// Code point ranges of the scripts the pruning drops (prune.rs:39-90) and the
+// notation blocks kept inside them (prune.rs:94). These tables decide which
+// rows the pruned file holds, so they are the reference's.
+const uint32_t kDropRanges[][2] = {
+    {0x0400, 0x052F},   {0x0530, 0x058F},   {0x0590, 0x05FF},   {0x0700, 0x07FF},   {0x0800, 0x089F},
+    {0x0900, 0x0DFF},   {0x0E00, 0x0EFF},   {0x0F00, 0x0FFF},   {0x1000, 0x109F},   {0x10A0, 0x10FF},
+    {0x1100, 0x11FF},   {0x1200, 0x139F},   {0x13A0, 0x13FF},   {0x1400, 0x167F},   {0x1680, 0x16FF},
+    {0x1700, 0x18FF},   {0x1900, 0x1DFF},   {0x1F00, 0x1FFF},   {0x2C00, 0x2C5F},   {0x2C80, 0x2CFF},
+    {0x2D00, 0x2D7F},   {0x2D80, 0x2DDF},   {0x2DE0, 0x2DFF},   {0x2E80, 0x2FFF},   {0x3000, 0x303F},
+    {0x3040, 0x30FF},   {0x3100, 0x312F},   {0x3130, 0x318F},   {0x3190, 0x31FF},   {0x3200, 0x33FF},
+    {0x3400, 0x4DBF},   {0x4DC0, 0x4DFF},   {0x4E00, 0x9FFF},   {0xA000, 0xA71F},   {0xA800, 0xAFFF},
+    {0xAB00, 0xAB2F},   {0xAB70, 0xABFF},   {0xAC00, 0xD7FF},   {0xF900, 0xFAFF},   {0xFE30, 0xFE4F},
+    {0xFE50, 0xFE6F},   {0xFF00, 0xFFEF},   {0x10000, 0x1D0FF}, {0x1D200, 0x1D3FF}, {0x1D800, 0x1EFFF},
+    {0x20000, 0x2FFFF}, {0x30000, 0x3FFFF}};
+const uint32_t kKeepAstral[][2] = {{0x1D100, 0x1D1FF}, {0x1D400, 0x1D7FF}};
+
+bool char_dropped(uint32_t u) {  // prune.rs:96-102
+  for (const auto& r : kKeepAstral)
+    if (u >= r[0] && u <= r[1]) return false;
+  for (const auto& r : kDropRanges)
+    if (u >= r[0] && u <= r[1]) return true;
+  return false;
+}
+
+// surface_kept (prune.rs:104-108): the token string is undone through the
+// byte-level alphabet (decode_token_bytes, tokenizer.rs:362-383: a character
+// of the alphabet is its byte, any other character its own UTF-8), the bytes
+// are read as lossy UTF-8, and no character may be in a dropped script.
+// U+FFFD (what lossy decoding puts for invalid bytes) is never dropped, so
+// invalid bytes are simply passed over.
+bool surface_kept(const std::string& tok, const int16_t (&cp_to_byte)[324]) {
+  std::string bytes;
+  bytes.reserve(tok.size());
+  const uint8_t* s = (const uint8_t*)tok.data();
+  for (size_t i = 0; i < tok.size();) {
+    int bad = 1;
+    const int len = rlh::utf8_seq(s, tok.size(), i, &bad);  // the string is valid UTF-8 (read lossily)
+    if (len == 0) {
+      i += (size_t)bad;
+      continue;
+    }
+    const uint32_t cp = rlh::utf8_cp(s + i, len);
+    if (cp < 324 && cp_to_byte[cp] >= 0) bytes += (char)cp_to_byte[cp];
+    else bytes.append(tok, i, (size_t)len);
+    i += (size_t)len;
+  }
+  const uint8_t* b = (const uint8_t*)bytes.data();
+  for (size_t i = 0; i < bytes.size();) {
+    int bad = 1;
+    const int len = rlh::utf8_seq(b, bytes.size(), i, &bad);
+    if (len == 0) {
+      i += (size_t)bad;
+      continue;
+    }
+    if (char_dropped(rlh::utf8_cp(b + i, len))) return false;
+    i += (size_t)len;
+  }
+  return true;
+}
+
+// MetaValue::as_string_vec (gguf.rs:82-89): an array whose elements are all strings.
+bool as_string_vec(const Meta* m, std::vector<const std::string*>* out) {
+  if (!m || m->type != V_ARR) return false;
+  out->clear();
+  for (const Meta& e : m->arr) {
+    if (e.type != V_STR) return false;
+    out->push_back(&e.s);
+  }
+  return true;
+}
+
+bool ends_with(const std::string& s, const char* suf) {
+  const size_t n = std::strlen(suf);
+  return s.size() >= n && s.compare(s.size() - n, n, suf) == 0;
+}
+
+Meta str_array(const std::vector<std::string>& v) {
+  Meta m;
+  m.type = V_ARR;
+  m.elem = V_STR;
+  for (const std::string& s : v) {
+    Meta e;
+    e.type = V_STR;
+    e.s = s;
+    m.arr.push_back(std::move(e));
+  }
+  return m;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rlh_prune_vocab(const char* in_path, const char* out_path, rlh_prune_stats* stats) {
+  if (!in_path || !out_path) return set_error(RLH_EINVAL, "null argument");
+  rlh_gguf* g = nullptr;
+  int rc = rlh_gguf_open(in_path, &g);
+  if (rc) return rc;
+  struct Closer {
+    rlh_gguf* g;
+    ~Closer() { rlh_gguf_close(g); }
+  } closer{g};
+  auto bad = [](const std::string& msg) { return set_error(RLH_EFORMAT, ("prune: " + msg).c_str()); };
+
+  std::vector<const std::string*> tokens, merges;
+  if (!as_string_vec(find_meta(g, "tokenizer.ggml.tokens"), &tokens)) return bad("tokenizer.ggml.tokens");
+  const uint64_t vocab = tokens.size();
+  std::vector<uint32_t> types(vocab, 1u);  // absent or not an array: every token normal
+  if (const Meta* tt = find_meta(g, "tokenizer.ggml.token_type"); tt && tt->type == V_ARR) {
+    types.assign(tt->arr.size(), 1u);
+    for (size_t k = 0; k < tt->arr.size(); k++) {
+      uint32_t v = 1;
+      if (as_u32(&tt->arr[k], &v)) types[k] = v;
+    }
+  }
+  if (!as_string_vec(find_meta(g, "tokenizer.ggml.merges"), &merges)) merges.clear();
+  if (types.size() != vocab) return bad("tokenizer.ggml.token_type length mismatch");
+
+  // token ids named by *_token_id keys always survive
+  std::vector<bool> pinned(vocab, false);
+  for (const auto& kv : g->meta) {
+    uint32_t id = 0;
+    if (ends_with(kv.first, "_token_id") && as_u32(&kv.second, &id) && id < vocab) pinned[id] = true;
+  }
+  int16_t cp_to_byte[324];
+  {
+    std::fill(std::begin(cp_to_byte), std::end(cp_to_byte), (int16_t)-1);
+    uint32_t n = 0;
+    for (uint32_t b = 0; b < 256; b++) {  // bytes_to_unicode (tokenizer.rs:7-32)
+      const bool direct = (b >= 0x21 && b <= 0x7e) || (b >= 0xa1 && b <= 0xac) || (b >= 0xae && b <= 0xff);
+      cp_to_byte[direct ? b : 256 + n++] = (int16_t)b;
+    }
+  }
+  rlh_prune_stats st{};
+  std::vector<bool> keep(vocab, false);
+  for (uint64_t i = 0; i < vocab; i++) {
+    const uint32_t ty = types[i];  // 2 unknown, 3 control, 4 user-defined, 6 byte
+    if (ty == 2 || ty == 3 || ty == 4 || ty == 6 || pinned[i]) {
+      keep[i] = true;
+      if (ty == 3 || ty == 4) st.kept_special++;
+      else if (ty == 6) st.kept_byte++;
+      else st.kept_normal++;
+    } else if (surface_kept(*tokens[i], cp_to_byte)) {
+      keep[i] = true;
+      st.kept_normal++;
+    }
+  }
+  std::vector<uint32_t> new_id(vocab, UINT32_MAX);
+  uint32_t next = 0;
+  for (uint64_t i = 0; i < vocab; i++)
+    if (keep[i]) new_id[i] = next++;
+  const uint64_t new_vocab = next;
+  if (new_vocab == 0) return bad("prune would remove the entire vocabulary");
+
+  // merges that still resolve inside the kept set; a token string maps to
+  // its last id, as a map built in id order keeps it
+  std::unordered_map<std::string, uint32_t> to_id;
+  for (uint64_t i = 0; i < vocab; i++) to_id[*tokens[i]] = (uint32_t)i;
+  std::vector<std::string> merges_new;
+  for (const std::string* m : merges) {
+    const size_t sp = m->find(' ');
+    if (sp == std::string::npos) continue;
+    const std::string l = m->substr(0, sp), r = m->substr(sp + 1);
+    auto li = to_id.find(l), ri = to_id.find(r), mi = to_id.find(l + r);
+    if (li != to_id.end() && ri != to_id.end() && mi != to_id.end() && keep[li->second] && keep[ri->second] &&
+        keep[mi->second])
+      merges_new.push_back(*m);
+  }
+
+  // metadata: every key of the input, then the new vocabulary, types,
+  // merges and remapped *_token_id values (written as u32)
+  rlh_gguf_writer w;
+  w.version = g->version;
+  uint32_t align = 32;
+  if (const Meta* a = find_meta(g, "general.alignment")) {
+    uint32_t v = 0;
+    if (as_u32(a, &v)) align = v;
+  }
+  w.alignment = align;
+  for (const auto& kv : g->meta) {
+    Meta m = kv.second;
+    if (m.type == V_ARR) {
+      for (const Meta& e : m.arr)
+        if (e.type == V_ARR) return bad("nested arrays are not supported by the writer");
+      if (m.arr.empty()) m.elem = V_STR;  // an empty array is written with the string tag
+    }
+    w.meta[kv.first] = std::move(m);
+  }
+  {
+    std::vector<std::string> kept_tokens;
+    Meta types_new;
+    types_new.type = V_ARR;
+    types_new.elem = V_I32;
+    for (uint64_t i = 0; i < vocab; i++) {
+      if (!keep[i]) continue;
+      kept_tokens.push_back(*tokens[i]);
+      Meta e;
+      e.type = V_I32;
+      e.i = (int32_t)types[i];
+      types_new.arr.push_back(e);
+    }
+    w.meta["tokenizer.ggml.tokens"] = str_array(kept_tokens);
+    w.meta["tokenizer.ggml.token_type"] = std::move(types_new);
+    w.meta["tokenizer.ggml.merges"] = str_array(merges_new);
+  }
+  for (const auto& kv : g->meta) {
+    uint32_t id = 0;
+    if (!ends_with(kv.first, "_token_id") || !as_u32(&kv.second, &id)) continue;
+    if (id >= vocab || new_id[id] == UINT32_MAX)
+      return bad("special token id " + std::to_string(id) + " ('" + kv.first + "') was pruned");
+    Meta m;
+    m.type = V_U32;
+    m.u = new_id[id];
+    w.meta[kv.first] = m;
+  }
+
+  // tensors in file order; token_embd / output with one row per token keep
+  // the rows of the kept tokens
+  std::list<std::vector<uint8_t>> owned;  // stable addresses for the writer
+  for (const std::string& name : g->order) {
+    const Info& t = g->tensors.at(name);
+    const void* data = nullptr;
+    uint64_t nb = 0;
+    if ((rc = rlh_gguf_tensor_bytes(g, name.c_str(), &data, &nb))) return rc;
+    uint64_t rows = 1, bs = 0, ts = 0;
+    for (size_t d = 1; d < t.dims.size(); d++) rows *= t.dims[d];
+    const uint64_t cols = t.dims.empty() ? 1 : t.dims[0];
+    type_geom(t.ty, &bs, &ts);
+    if ((name == "token_embd.weight" || name == "output.weight") && rows == vocab) {
+      const uint64_t rb = cols / bs * ts;
+      Info ni = t;
+      ni.dims = {cols, new_vocab};
+      uint64_t nb_new = 0;
+      n_bytes(ni, &nb_new);
+      std::vector<uint8_t> sliced;
+      sliced.reserve(std::max<uint64_t>(nb_new, new_vocab * rb));
+      for (uint64_t i = 0; i < vocab; i++)
+        if (keep[i]) sliced.insert(sliced.end(), (const uint8_t*)data + i * rb, (const uint8_t*)data + i * rb + rb);
+      st.embd_bytes_saved += nb - sliced.size();
+      // rows of whole blocks (every ggml file): the sliced rows are the
+      // tensor's bytes; otherwise zeros fill it up to its size
+      if (sliced.size() < nb_new) sliced.resize(nb_new, 0);
+      owned.push_back(std::move(sliced));
+      w.tensors.push_back(WTensor{name, t.ty, ni.dims, owned.back().data(), nb_new});
+    } else {
+      w.tensors.push_back(WTensor{name, t.ty, t.dims, data, nb});
+    }
+  }
+  if ((rc = rlh_gguf_writer_write(&w, out_path))) return rc;
+  struct stat sb {};
+  if (stat(out_path, &sb) != 0) return set_error(RLH_EIO, ("cannot stat '" + std::string(out_path) + "'").c_str());
+  st.old_vocab = vocab;
+  st.new_vocab = new_vocab;
+  st.dropped = vocab - new_vocab;
+  st.merges_old = merges.size();
+  st.merges_new = merges_new.size();
+  st.out_bytes = (uint64_t)sb.st_size;
+  if (stats) *stats = st;
   return RLH_OK;
 }
 

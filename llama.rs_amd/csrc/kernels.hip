@@ -241,7 +241,9 @@ __global__ void __launch_bounds__(256) k_argmax_partial(const float* x, uint32_t
   __shared__ uint32_t si[256];
   float bv = -__int_as_float(0x7f800000);
   uint32_t bi = 0xffffffffu;
-  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) argmax_merge(bv, bi, x[i], i);
+  // 64-bit index: with n near 2^32 a 32-bit i += stride would wrap below n
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256)
+    argmax_merge(bv, bi, x[i], (uint32_t)i);
   sv[threadIdx.x] = bv;
   si[threadIdx.x] = bi;
   __syncthreads();

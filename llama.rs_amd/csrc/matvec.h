@@ -51,6 +51,7 @@ struct MvLaunch {
   // from xf in Q8 launches, written by the norm prologue otherwise
   const float* xf;
   uint32_t need_xf;
+  uint32_t need_q8;  // 0: every segment multiplies the f32 row (Q5_K, Q4_1, Q5_0, Q5_1), no Q8 staging
   uint32_t xf_off;  // byte offset of the f32 row in LDS
   uint32_t region_off;    // byte offset of the term tiles in LDS
   uint32_t tile_stride;   // floats per term-tile row
@@ -60,6 +61,9 @@ struct MvLaunch {
   uint32_t ring;
   uint32_t has_argmax;
   MvArgmax am;
+  // device error word (nullable): a bounded intra-block wait that expires
+  // sets its bit (kErrMvRing / kErrMvSplit) here
+  uint32_t* err;
 };
 
 // Host-side plan: segments are appended, then launched once.
@@ -104,9 +108,12 @@ void mv_plan_add(MvPlan& p, const DevMat& w, float* y, float* resid);
 void mv_plan_add_pair(MvPlan& p, const DevMat& gate, const DevMat& up, const Q8Mut& hq, float* h);
 void mv_plan_argmax(MvPlan& p, const MvArgmax& am);
 bool mv_plan_finish(MvPlan& p);
-// ev_start / ev_stop (optional, not under graph capture): events that take
-// the kernel's own start and end times (hipExtLaunchKernel), for probes.
-void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start = nullptr, hipEvent_t ev_stop = nullptr);
+// err: the device error word the launch's bounded waits report to
+// (nullable). ev_start / ev_stop (optional, not under graph capture): events
+// that take the kernel's own start and end times (hipExtLaunchKernel), for
+// probes.
+void mv_launch(hipStream_t st, const MvPlan& p, uint32_t* err, hipEvent_t ev_start = nullptr,
+               hipEvent_t ev_stop = nullptr);
 // Blocks of a single-matrix plan over `rows` rows of `cols` columns (the
 // argmax partial buffers of the logits launch hold one entry per block).
 uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols);

@@ -437,15 +437,17 @@ __device__ __forceinline__ void lds_dma4(RLH_LDS void* dst, const void* src, uin
 __device__ __forceinline__ void act_dma(const MvLaunch& L, const LAct& la) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
   const uint32_t cols = L.cols, nsb = cols >> 8, nb = cols >> 5, nslots = nsb * 17;
-  for (uint32_t s0 = wave * 64; s0 < nslots; s0 += nw * 64) {
-    const uint32_t p = s0 + lane, sb = p / 17, ch = p - sb * 17;
-    if (p < nslots && ch < 16)
-      __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.act.qs + sb * 256 + ch * 16),
-                                       (RLH_LDS void*)(la.qs + s0 * 16), 16, 0, 0);
+  if (L.need_q8) {
+    for (uint32_t s0 = wave * 64; s0 < nslots; s0 += nw * 64) {
+      const uint32_t p = s0 + lane, sb = p / 17, ch = p - sb * 17;
+      if (p < nslots && ch < 16)
+        __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.act.qs + sb * 256 + ch * 16),
+                                         (RLH_LDS void*)(la.qs + s0 * 16), 16, 0, 0);
+    }
+    lds_dma4(la.d, L.act.d, nb * 4, wave, nw);
+    lds_dma4(la.s, L.act.s, nb * 4, wave, nw);
+    lds_dma4(la.s16x32, L.act.s16, nb * 8, wave, nw);
   }
-  lds_dma4(la.d, L.act.d, nb * 4, wave, nw);
-  lds_dma4(la.s, L.act.s, nb * 4, wave, nw);
-  lds_dma4(la.s16x32, L.act.s16, nb * 8, wave, nw);
   if (L.need_xf)  // the f32 row, one 256-value super-block per wave instruction
     for (uint32_t sb = wave; sb < nsb; sb += nw)
       __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)(L.xf + sb * 256 + lane * 4),
@@ -453,7 +455,7 @@ __device__ __forceinline__ void act_dma(const MvLaunch& L, const LAct& la) {
 }
 
 __device__ __forceinline__ void act_finish(const MvLaunch& L, const LAct& la) {
-  const uint32_t nb = L.cols >> 5;
+  const uint32_t nb = L.need_q8 ? L.cols >> 5 : 0u;
   lds_barrier();
   for (uint32_t i = threadIdx.x; i < 2 * nb; i += blockDim.x) {
     const int v = ((RLH_LDS int32_t*)la.s16x32)[i];
@@ -800,11 +802,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   auto ring_wait = [&](uint32_t u) {
     const uint32_t rr = u / kP;
     if (u % kP != 0 || rr < ring) return;
-    for (uint32_t spin = 0; spin < (1u << 26); spin++) {  // bounded: wave 0 keeps consuming
-      if (__hip_atomic_load(ring_consumed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= rr - ring + 1) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    asm volatile("" ::: "memory");
+    wait_lds_count(ring_consumed, rr - ring + 1, L.err, kErrMvRing);  // wave 0 keeps consuming
   };
   auto ring_signal = [&](uint32_t u) {
     if (u % kP != kP - 1) return;
@@ -880,11 +878,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
     const lfloat* rowp = region + (lane < nrows ? lane : 0) * stride;
     for (uint32_t rr = 0; rr < nr; rr++) {
       const uint32_t s = rr % ring, tin = min(np, ntiles - rr * np), need = np * (rr / ring) + tin;
-      for (uint32_t spin = 0; spin < (1u << 26); spin++) {  // bounded: every producer reaches its tiles
-        if (__hip_atomic_load(ring_done + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
-        __builtin_amdgcn_s_sleep(1);
-      }
-      asm volatile("" ::: "memory");
+      wait_lds_count(ring_done + s, need, L.err, kErrMvRing);  // every producer reaches its tiles
       acc = seq_sum_lds(rowp + s * R * stride, tin * TJ * I::kT, acc);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0): the slot's reads are done
@@ -895,9 +889,7 @@ __device__ __forceinline__ void mv_block(const MvLaunch& L, const MvSeg& g, uint
   const uint32_t n_early = split ? kr * nwaves * TJ * I::kT : 0u;
   if (split && wave == nwaves - 1) {
     // every wave reaches kr tiles (each has at least kr), so the wait ends
-    while (__hip_atomic_load(rounds_done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < kr * nwaves)
-      __builtin_amdgcn_s_sleep(1);
-    asm volatile("" ::: "memory");
+    wait_lds_count(rounds_done, kr * nwaves, L.err, kErrMvSplit);
     misc[4 + lane] = chain(region + (lane < nrows ? lane : 0) * stride, n_early);
   }
   __syncthreads();
@@ -1014,6 +1006,7 @@ bool mv_is_float(uint32_t ty) { return ty == RLH_TYPE_F16 || ty == RLH_TYPE_F32 
 // padded f32 row when a segment is Q5_K, then the term tiles (which the norm
 // prologue borrows for the f32 input row and the norm weights).
 uint32_t plan_act_bytes(const MvPlan& p) {
+  if (!p.L.need_q8) return 0u;
   const uint32_t nsb = p.L.cols / 256, nb = p.L.cols / 32;
   return (nsb * kSbStride + nb * 16 + 15) & ~15u;
 }
@@ -1165,15 +1158,24 @@ bool mv_plan_finish(MvPlan& p) {
   for (uint32_t s = 0; s < p.L.nseg; s++)
     if (mv_needs_f32(p.L.seg[s].w.ty) || (p.L.seg[s].pair && mv_needs_f32(p.L.seg[s].w2.ty))) p.L.need_xf = 1;
   if (p.L.need_xf && !p.norm && !p.L.xf) return false;  // f32 products need the f32 activation
+  // a launch whose tiled segments all multiply the f32 row stages no Q8 row
+  p.L.need_q8 = 1;
+  if (!p.norm && !fl) {
+    bool all_f32 = true;
+    for (uint32_t s = 0; s < p.L.nseg; s++)
+      all_f32 = all_f32 && mv_needs_f32(p.L.seg[s].w.ty) && (!p.L.seg[s].pair || mv_needs_f32(p.L.seg[s].w2.ty));
+    if (all_f32) p.L.need_q8 = 0;
+  }
   p.slot_stride = slots + 1;  // float plans: a row's chain results
   p.float_stage = fl ? mv_float_stage_bytes(nm, R) : 0u;
-  if (plan_lds(p, R, nm) > kMaxLds) return false;
+  // a whole-row plan that exceeds the LDS may still run as a ring plan below
+  const bool whole_fits = plan_lds(p, R, nm) <= kMaxLds;
   // A grid just above the blocks the GPU holds at once would run a second,
   // short round of blocks after the first (every block pays its prologue and
   // tail again, and most CUs idle meanwhile): then blocks of twice the rows,
   // when those fit in one round (the 32B q/k/v launch: 320 blocks of 32 rows
   // at one block per CU, 160 of 64)
-  if (tiled_any && !fl && nm == 1 && 2 * R <= 64 && plan_lds(p, 2 * R, nm) <= kMaxLds) {
+  if (whole_fits && tiled_any && !fl && nm == 1 && 2 * R <= 64 && plan_lds(p, 2 * R, nm) <= kMaxLds) {
     const uint32_t b0 = plan_blocks(p, R), b1 = plan_blocks(p, 2 * R);
     const uint32_t s0 = mv_resident_blocks(p, R, tr, ntj), s1 = mv_resident_blocks(p, 2 * R, tr, ntj);
     if (s0 && s1 && b0 > s0 && b0 <= 2 * s0 && b1 <= s1) R *= 2;
@@ -1187,12 +1189,15 @@ bool mv_plan_finish(MvPlan& p) {
   // once (32B ffn_down: four producers, 74 KB, two blocks per CU)
   // (RLH_MV_RING=1 in the environment takes a ring plan wherever one
   // applies, with the most producers that fit the LDS: the tests run the
-  // ring on small shapes and every tiled type with it)
+  // ring on small shapes and every tiled type with it). Rows whose whole-row
+  // terms do not fit the LDS at all (the f32-product types past ~12288
+  // values: the f32 row alone takes 1 KB per 256 values) take the ring plan
+  // with the most producers that fit.
   uint32_t ring_np = 0;
   const uint32_t tj = tiled_any ? p.L.seg[0].w.tj : 1u;
   if (tiled_any && !fl && nm == 1 && !p.norm && R == tr && ntj >= 2) {
     const char* env = std::getenv("RLH_MV_RING");
-    const bool force = env && env[0] == '1';
+    const bool force = (env && env[0] == '1') || !whole_fits;
     const uint32_t b = plan_blocks(p, R), s = force ? 0u : mv_resident_blocks(p, R, tr, ntj);
     if (force || (s && b > s))
       for (uint32_t np = std::min<uint32_t>(7, ntj); np >= 2 && !ring_np; np--)  // np + 1 <= 8 waves (launch bound)
@@ -1200,8 +1205,15 @@ bool mv_plan_finish(MvPlan& p) {
             (force || mv_resident(p, 64 * (np + 1), ring_lds(p, R, np, tj, 2), true) >= b))
           ring_np = np;
   }
+  if (!ring_np && !whole_fits) return false;
   p.L.rows_per_blk = R;
   p.L.ring = ring_np ? 2u : 0u;
+  // The ring waits end because a producer waits only for round r - ring to
+  // be consumed before writing round r, and wave 0 consumes the rounds in
+  // order: this needs 1 <= ring <= 3 (the LDS counters the kernel keeps), at
+  // least one producer wave beside wave 0 within the 8-wave launch bound, and
+  // one row tile per block (equal rounds in every block).
+  if (ring_np && !(p.L.ring >= 1 && p.L.ring <= 3 && ring_np + 1 <= 8 && R == tr)) return false;
   p.L.tile_stride = ring_np ? ring_stride(p, ring_np, tj) : std::max(nsb * p.max_terms + 4, p.slot_stride);
   p.L.xf_off = plan_act_bytes(p);
   p.L.region_off = p.L.xf_off + plan_xf_bytes(p);
@@ -1236,16 +1248,18 @@ uint32_t mv_blocks_for(uint32_t ty, uint32_t rows, uint32_t cols) {
   return p.blocks;
 }
 
-void mv_launch(hipStream_t st, const MvPlan& p, hipEvent_t ev_start, hipEvent_t ev_stop) {
+void mv_launch(hipStream_t st, const MvPlan& p, uint32_t* err, hipEvent_t ev_start, hipEvent_t ev_stop) {
+  MvLaunch L = p.L;
+  L.err = err;
   const bool pair = p.L.nseg == 1 && p.L.seg[0].pair;
   uint32_t ty = p.L.seg[0].w.ty;
   for (uint32_t s = 1; s < p.L.nseg; s++)
     if (p.L.seg[s].w.ty != ty) ty = 0;
   const MvKernel k = pair ? mv_kernel<2>(ty) : (p.L.ring ? mv_kernel<1, true>(ty) : mv_kernel<1>(ty));
   if (ev_start || ev_stop)
-    hipExtLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, ev_start, ev_stop, 0, p.L);
+    hipExtLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, ev_start, ev_stop, 0, L);
   else
-    hipLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, p.L);
+    hipLaunchKernelGGL(k, dim3(p.blocks), dim3(64 * p.waves), p.lds, st, L);
 }
 
 bool mv_set_max_lds(size_t bytes) {

@@ -178,6 +178,32 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ---------------------------------------------------------------------------
+// Bounded waits on an LDS counter written by other waves of the same block.
+// Every such wait ends by construction (the producers it waits for never
+// wait on it); the bound turns a broken invariant into an error instead of a
+// hang or silently wrong values: once kWaitPolls polls (~1.8 s of sleeps)
+// have passed, the wave gives up, lane 0 sets `bit` in the device error word
+// `err` (nullable) and the host reports RLH_EDEVICE after the step. The wait
+// is wave-uniform (every lane reads the same counter).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kWaitPolls = 1u << 26;
+constexpr uint32_t kErrMvRing = 1u, kErrMvSplit = 2u, kErrAttnExp = 4u;
+
+__device__ __forceinline__ void wait_lds_count(const RLH_LDS uint32_t* ctr, uint32_t need, uint32_t* err,
+                                               uint32_t bit) {
+  for (uint32_t spin = 0;; spin++) {
+    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= need) break;
+    if (spin == kWaitPolls) {
+      if (err && (threadIdx.x & 63) == 0)
+        __hip_atomic_fetch_or(err, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
 // Exact AVX2 reduction tree over 32 "slot" accumulators held in lanes 0..31
 // of a wave: slot 8k+l is lane l of the reference's accumulator a_k.
 //   A_l = (a0_l + a1_l) + (a2_l + a3_l)            (simd.rs:308, 370)

@@ -56,6 +56,13 @@ class Config(ctypes.Structure):
                 ("vocab_size", ctypes.c_uint32), ("has_qk_norm", ctypes.c_uint32), ("has_output", ctypes.c_uint32)]
 
 
+class PruneStats(ctypes.Structure):
+    """`PruneStats` of src/prune.rs:113-124."""
+    _fields_ = [(f, ctypes.c_uint64) for f in ("old_vocab", "new_vocab", "kept_special", "kept_byte",
+                                                "kept_normal", "dropped", "merges_old", "merges_new",
+                                                "embd_bytes_saved", "out_bytes")]
+
+
 @dataclass
 class ModelSpec:
     """Shape and per-tensor ggml types of a synthetic Qwen3 model."""
@@ -151,6 +158,12 @@ SPECS = {
     "tiny-mix": ModelSpec("tiny-mix", 2, 256, 512, 4, 2, 1000, False,
                           {T_ATTN_Q: F16, T_ATTN_K: Q8_0, T_ATTN_V: Q5_1, T_ATTN_OUTPUT: BF16, T_FFN_GATE: Q4_1,
                            T_FFN_UP: Q5_0, T_FFN_DOWN: F32, T_TOKEN_EMBD: Q4_0, T_OUTPUT: Q5_K}, n_ctx=512),
+    # f32-product types with a 13056-wide FFN: ffn_down rows too long for the
+    # whole-row decode plan (the launch stages the f32 row only and takes a
+    # ring plan)
+    "tiny-longff-q5": ModelSpec("tiny-longff-q5", 2, 256, 13056, 4, 2, 1000, False,
+                                {**_all(Q5_0, tied=False), T_FFN_DOWN: Q5_1, T_FFN_UP: Q4_1, T_FFN_GATE: Q4_1},
+                                n_ctx=512),
     # 8 query heads per KV head (the 32B grouping) and a long context window
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
     # 4 query heads per KV head (the 4B / 8B grouping) and a long context window
@@ -158,6 +171,12 @@ SPECS = {
     # 1 and 2 query heads per KV head with a long context window
     "tiny-g1-q4km": ModelSpec("tiny-g1-q4km", 2, 256, 512, 2, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
     "tiny-g2-q4km": ModelSpec("tiny-g2-q4km", 2, 256, 512, 4, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    # groups that do not divide the kernels' 64-wide tiles: 3, 5 (Qwen3-14B's
+    # 40/8), 6 and 7 (Qwen2.5-7B's 28/4) query heads per KV head
+    "tiny-g3-q4km": ModelSpec("tiny-g3-q4km", 2, 256, 512, 6, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    "tiny-g5-q4km": ModelSpec("tiny-g5-q4km", 2, 256, 512, 10, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    "tiny-g6-q4km": ModelSpec("tiny-g6-q4km", 2, 256, 512, 12, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
+    "tiny-g7-q4km": ModelSpec("tiny-g7-q4km", 2, 256, 512, 14, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=4096),
     # 104 query heads (13312-wide attention rows: attn_output takes Q8 blocks
     # from the attention kernels instead of quantizing the row itself)
     "tiny-wide-q4km": ModelSpec("tiny-wide-q4km", 2, 256, 512, 104, 13, 1000, True, _q4km(True, Q4_K, None),
@@ -256,6 +275,7 @@ def load():
         "rlh_last_error": (ctypes.c_char_p, []),
         "rlh_version": (ctypes.c_char_p, []),
         "rlh_row_bytes": (U64, [U32, U64]),
+        "rlh_config_check": (I32, [ctypes.POINTER(Config)]),
         "rlh_model_create": (I32, [ctypes.POINTER(Config), ctypes.POINTER(P)]),
         "rlh_model_set_tensor": (I32, [P, I32, I32, U32, P, U64, U64]),
         "rlh_model_finalize": (I32, [P]),
@@ -327,6 +347,7 @@ def load():
         "rlh_gguf_writer_set_array": (I32, [P, ctypes.c_char_p, U32, P, U64]),
         "rlh_gguf_writer_add_tensor": (I32, [P, ctypes.c_char_p, U32, U32, P, P, U64]),
         "rlh_gguf_writer_write": (I32, [P, ctypes.c_char_p]),
+        "rlh_prune_vocab": (I32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(PruneStats)]),
         "rlh_tokenizer_create": (I32, [P, U64, P, U64, P, U64, U32, U32, ctypes.POINTER(P)]),
         "rlh_tokenizer_from_gguf": (I32, [P, ctypes.POINTER(P)]),
         "rlh_tokenizer_destroy": (None, [P]),
@@ -746,6 +767,15 @@ def write_gguf(path, meta, tensors, version=3, alignment=32):
         check(lib.rlh_gguf_writer_write(w, os.fsencode(path)))
     finally:
         lib.rlh_gguf_writer_destroy(w)
+
+
+def prune_vocab(in_path, out_path):
+    """prune::prune_vocab (prune.rs:127-291) through rlh_prune_vocab; returns
+    the PruneStats counts as a dict."""
+    lib = load()
+    st = PruneStats()
+    check(lib.rlh_prune_vocab(os.fsencode(in_path), os.fsencode(out_path), ctypes.byref(st)))
+    return {f: getattr(st, f) for f, _ in PruneStats._fields_}
 
 
 def model_gguf_meta(spec, n_ctx=None, vocab_tokens=None, extra=None):

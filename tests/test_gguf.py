@@ -240,6 +240,62 @@ def test_architecture_gate_and_missing_keys(tmp_path):
     assert e.value.code == rlh.RLH_EFORMAT and b"embedding_length" in rlh.load().rlh_last_error()
 
 
+def _qwen2_meta(n_embd, n_ff, n_head, n_head_kv, key_length=None):
+    m = {"general.architecture": (rlh.GGUF_STR, "qwen2"), "qwen2.block_count": (rlh.GGUF_U32, 1),
+         "qwen2.embedding_length": (rlh.GGUF_U32, n_embd), "qwen2.feed_forward_length": (rlh.GGUF_U32, n_ff),
+         "qwen2.attention.head_count": (rlh.GGUF_U32, n_head),
+         "qwen2.attention.head_count_kv": (rlh.GGUF_U32, n_head_kv),
+         "tokenizer.ggml.tokens": (rlh.GGUF_ARR, (rlh.GGUF_STR, ["a", "b", "c"]))}
+    if key_length is not None:
+        m["qwen2.attention.key_length"] = (rlh.GGUF_U32, key_length)
+    return m
+
+
+@pytest.mark.parametrize("shape,reason", [
+    ((896, 4864, 14, 2, None), b"head_dim 64"),      # Qwen2.5-0.5B: head_dim 896 / 14
+    ((1024, 3072, 16, 8, 64), b"head_dim 64"),       # key_length given explicitly
+    ((2048, 5000, 16, 2, 128), b"multiples of 256"),  # n_ff not a multiple of 256
+    ((1152, 3072, 9, 3, 128), b"multiples of 256"),   # n_embd 1152 = 4.5 x 256
+    ((2048, 4096, 16, 1, 128), b"more than 8 query heads")])
+def test_unsupported_shapes_refused_before_upload(tmp_path, shape, reason):
+    """Shapes Model::read_config accepts (model.rs:249-268: any head_dim;
+    rows of any whole number of blocks, tensor.rs:28-30) but this path does
+    not run are refused by rlh_config_check, which rlh_model_load_gguf
+    applies right after reading the config: RLH_EUNSUP with the reason,
+    before the vocabulary or any tensor is read and before a device is
+    needed (this test runs without a GPU). The config itself still reads."""
+    n_embd, n_ff, n_head, n_head_kv, kl = shape
+    meta = _qwen2_meta(n_embd, n_ff, n_head, n_head_kv, kl)
+    p = tmp_path / "shape.gguf"
+    rlh.write_gguf(p, meta, [("token_embd.weight", rlh.F32, [4, 3], np.zeros(12, np.float32))])
+    lib = rlh.load()
+    with rlh.Gguf(p) as g:
+        c, arch = g.config()
+        assert arch == "qwen2" and c.n_embd == n_embd and c.head_dim == (kl or n_embd // n_head)
+        assert lib.rlh_config_check(ctypes.byref(c)) == rlh.RLH_EUNSUP
+        assert reason in lib.rlh_last_error()
+        h = ctypes.c_void_p()
+        assert lib.rlh_model_load_gguf(g.h, ctypes.byref(h)) == rlh.RLH_EUNSUP
+        assert reason in lib.rlh_last_error() and not h.value
+        hm = ctypes.c_void_p()
+        assert lib.rlh_model_create(ctypes.byref(c), ctypes.byref(hm)) == rlh.RLH_EUNSUP and not hm.value
+
+
+def test_supported_shapes_pass_config_check():
+    """Every benchmark model and every test spec passes rlh_config_check, and
+    the checks on zero dimensions and head divisibility come first."""
+    lib = rlh.load()
+    for name, spec in rlh.SPECS.items():
+        c = spec.config()
+        assert lib.rlh_config_check(ctypes.byref(c)) == rlh.RLH_OK, (name, lib.rlh_last_error())
+    c = rlh.SPECS["tiny-q4km"].config()
+    c.n_head_kv = 3
+    assert lib.rlh_config_check(ctypes.byref(c)) == rlh.RLH_EINVAL
+    c.n_head_kv = 0
+    assert lib.rlh_config_check(ctypes.byref(c)) == rlh.RLH_EINVAL
+    assert lib.rlh_config_check(None) == rlh.RLH_EINVAL
+
+
 def test_synthetic_model_file(tmp_path):
     """A seeded synthetic model written as a Qwen3 GGUF: the config it
     resolves is the spec's, every tensor is found by its GGUF name with the

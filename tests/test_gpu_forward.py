@@ -167,14 +167,24 @@ def test_decode_attention_g4_paths(max_ctx, n_prompt):
 
 @pytest.mark.parametrize("name,max_ctx,n_prompt", [("tiny-g1-q4km", 64, 30), ("tiny-g1-q4km", 2000, 200),
                                                    ("tiny-g2-q4km", 64, 30), ("tiny-g2-q4km", 2000, 130),
+                                                   ("tiny-g3-q4km", 64, 30), ("tiny-g3-q4km", 1200, 1100),
+                                                   ("tiny-g3-q4km", 3000, 1300),
+                                                   ("tiny-g5-q4km", 64, 30), ("tiny-g5-q4km", 3000, 1300),
+                                                   ("tiny-g6-q4km", 64, 30), ("tiny-g6-q4km", 3000, 700),
+                                                   ("tiny-g7-q4km", 64, 30), ("tiny-g7-q4km", 3000, 1300),
                                                    ("tiny-wide-q4km", 64, 20), ("tiny-wide-q4km", 3000, 100)])
 def test_decode_attention_groupings(name, max_ctx, n_prompt):
-    """Decode attention with 1 and 2 query heads per KV head (the resident-V
-    kernel for short caches, the softmax + streamed-ring PV kernels past
-    ~1500 positions) and with 13312-wide attention rows, where attn_output
-    reads the Q8 blocks the attention kernels write (the fused streamed
-    kernel for 64 positions, the softmax kernel + the streamed PV kernel
-    for 3000). Logits bit-exact."""
+    """Decode attention with 1, 2 and 3 query heads per KV head (the
+    resident-V kernel for short caches, the softmax + streamed-ring PV
+    kernels past ~1200-1500 positions), with 5, 6 and 7 (groups that do not
+    divide the prefill kernels' 64 (token, head) pairs or the decode
+    kernels' 64-lane chains: ragged pair tiles, 8-wide ring slices) and with
+    13312-wide attention rows, where attn_output reads the Q8 blocks the
+    attention kernels write (the fused streamed kernel for 64 positions, the
+    softmax kernel + the streamed PV kernel for 3000). Prompts of 700-1300
+    tokens run the prefill in two or three 512-token chunks, and decode rows
+    of 1024 positions or more take the softmax sum by monosum run pairs.
+    Logits bit-exact."""
     print(f"decode attention {name} max_ctx {max_ctx} prompt {n_prompt}", flush=True)
     spec, tensors, m, om = _get(name)
     prompt = rlh.synth_tokens(66, n_prompt, spec.vocab)

@@ -122,11 +122,29 @@ RING_TYPES = [Q4_K, Q6_K, Q8_0, Q4_0, Q5_K, Q4_1, Q5_0, Q5_1]
 @pytest.mark.parametrize("ty", RING_TYPES)
 @pytest.mark.parametrize("rows,cols", [(33, 2048), (100, 2560), (48, 4096), (7, 9728), (20, 12288), (9, 25600)])
 def test_matvec_ring_plan_bit_exact(ty, rows, cols, monkeypatch):
-    if ty in (Q4_1, Q5_0, Q5_1) and cols > 12288:
-        pytest.skip("no decode plan at this row length: the f32 row and the whole-row terms exceed the LDS budget")
     print(f"ring matvec ty={ty} {rows}x{cols}", flush=True)
     monkeypatch.setenv("RLH_MV_RING", "1")
     rng = np.random.default_rng(rows * 3 + cols + ty)
+    bs, ts = BLOCK[ty]
+    w = random_blocks(ty, rows * cols // bs, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = rlh.matvec(ty, w, rows, cols, x)
+    ref = oracle.matmul(ty, w, rows, cols, x, oracle.MODE_DEFAULT)
+    assert np.array_equal(bits(got), bits(ref)), f"max diff {np.max(np.abs(got - ref))}"
+
+
+@pytest.mark.parametrize("ty", [Q4_1, Q5_0, Q5_1, Q5_K])
+@pytest.mark.parametrize("rows,cols", [(300, 13056), (130, 25600), (70, 27648)])
+def test_matvec_long_rows_f32_types(ty, rows, cols):
+    """Rows of the f32-product types (quant.rs:528-539: every block
+    dequantized, then dot_f32_avx2 against the f32 activation) longer than
+    12288 values: the f32 row staged in LDS and the row's whole terms no
+    longer fit together, so the launch stages no Q8 row (these types never
+    read it) and takes a ring plan on its own (no RLH_MV_RING). 13056 values
+    are 51 super-blocks (one item per tile, 51 tiles per row), 25600 the 32B
+    FFN width, 27648 the Qwen2.5-32B FFN width. Bit-exact."""
+    print(f"long-row matvec ty={ty} {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows + cols + 7 * ty)
     bs, ts = BLOCK[ty]
     w = random_blocks(ty, rows * cols // bs, rng)
     x = rng.standard_normal(cols).astype(np.float32)

@@ -68,11 +68,12 @@ def test_matmul_batch_bit_exact(ty, rows, cols, n):
 
 
 @pytest.mark.parametrize("name", ["tiny-q4_1", "tiny-q5_0", "tiny-q5_1", "tiny-f16", "tiny-bf16", "tiny-f32",
-                                  "tiny-mix"])
+                                  "tiny-mix", "tiny-longff-q5"])
 def test_forward_bit_exact(name):
-    """Every matrix (and the embedding / logits matrix) in one type, or the
-    mix of eight types: prefill of 11 tokens (3 in the n % 4 tail), then
-    decode with greedy tokens; the KV cache afterwards."""
+    """Every matrix (and the embedding / logits matrix) in one type, the mix
+    of eight types, or Q4_1/Q5_0/Q5_1 with a 13056-wide FFN (ffn_down takes
+    the ring plan in decode): prefill of 11 tokens (3 in the n % 4 tail),
+    then decode with greedy tokens; the KV cache afterwards."""
     print(f"forward {name}", flush=True)
     spec = rlh.SPECS[name]
     tensors = rlh.synth_model(spec, 777)

@@ -10,7 +10,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 C_SCALARS = {"int": "c_int", "uint32_t": "u32", "uint64_t": "u64", "int32_t": "i32", "int8_t": "i8", "int64_t": "i64",
              "float": "f32", "double": "f64", "char": "c_char", "void": "c_void",
              "rlh_config": "RlhConfig", "rlh_model": "RlhModel", "rlh_cache": "RlhCache",
-             "rlh_sampling_params": "RlhSamplingParams", "rlh_gguf": "RlhGguf",
+             "rlh_sampling_params": "RlhSamplingParams", "rlh_gguf": "RlhGguf", "rlh_prune_stats": "RlhPruneStats",
              "rlh_gguf_writer": "RlhGgufWriter", "rlh_tokenizer": "RlhTokenizer", "rlh_dsampler": "RlhDsampler"}
 
 
