@@ -84,3 +84,51 @@ def test_missing_tensor_is_reported(tmp_path):
         rlh.load_model_gguf(p, spec)
     assert e.value.code == rlh.RLH_ESTATE
     assert b"blk.1.ffn_up.weight" in rlh.load().rlh_last_error()
+
+
+def test_pruned_model_decodes_like_the_oracle(tmp_path):
+    """prune_vocab (prune.rs:127-291) on a synthetic model whose vocabulary
+    is one third CJK: the pruned file loads onto the device and decodes
+    bit-exact against the oracle over the pruned tensors (token_embd and
+    output hold only the kept rows), and its logits are the unpruned model's
+    logits at the kept ids, for the same prompt."""
+    import prune_ref
+
+    spec = rlh.SPECS["tiny-q4km-untied"]
+    tensors = rlh.synth_model(spec, 80)
+    # byte-level token strings: "w<i>", or a CJK character for every third id
+    b2u = {b: ch for ch, b in prune_ref._U2B.items()}
+    vocab = ["".join(b2u[b] for b in (f"w{i}" if i % 3 else chr(0x4E00 + i)).encode()) for i in range(spec.vocab)]
+    src, dst = tmp_path / "full.gguf", tmp_path / "pruned.gguf"
+    rlh.write_model_gguf(src, spec, tensors, vocab_tokens=vocab)
+    st = rlh.prune_vocab(src, dst)
+    keep = [i for i in range(spec.vocab) if i % 3 or i == 0]  # id 0 is the bos token: pinned
+    assert st["new_vocab"] == len(keep) and st["dropped"] == spec.vocab - len(keep)
+    new_spec = rlh.ModelSpec("pruned", spec.n_layer, spec.n_embd, spec.n_ff, spec.n_head, spec.n_head_kv,
+                             len(keep), spec.tied, spec.types, spec.head_dim, spec.rope_theta, spec.rms_eps,
+                             spec.n_ctx)
+    pruned = []
+    for kind, layer, ty, cols, rows, buf in tensors:
+        if kind in (rlh.T_TOKEN_EMBD, rlh.T_OUTPUT):
+            rb = len(buf) // rows
+            buf = np.ascontiguousarray(buf.reshape(rows, rb)[keep]).reshape(-1)
+            rows = len(keep)
+        pruned.append((kind, layer, ty, cols, rows, buf))
+    with rlh.Gguf(dst) as g:
+        for kind, layer, ty, cols, rows, buf in pruned:
+            assert np.array_equal(g.tensor_bytes(rlh.gguf_tensor_name(kind, layer)), buf)
+    m = rlh.load_model_gguf(dst, new_spec)
+    full = rlh.Model(spec, tensors)
+    try:
+        _decode_matches_oracle(m, new_spec, pruned)
+        prompt_new = rlh.synth_tokens(42, 9, len(keep))
+        prompt_old = np.array([keep[i] for i in prompt_new], np.uint32)
+        c, cf = m.new_cache(16), full.new_cache(16)
+        lp = c.forward_into(prompt_new, 0)
+        lf = cf.forward_into(prompt_old, 0)
+        assert np.array_equal(bits(lp), bits(lf[keep]))
+        c.close()
+        cf.close()
+    finally:
+        m.close()
+        full.close()

@@ -241,3 +241,113 @@ def test_split_dequant_q4k_matches_scalar():
     tmp = np.empty(32, np.float32)
     assert lib.orc_split_dequant(8, src.ctypes.data, 32, tmp.ctypes.data) == 0
     assert lib.orc_split_dequant(12, src.ctypes.data, 100, tmp.ctypes.data) == 0
+
+
+def _f32(x):
+    return np.float32(x)
+
+
+def _wide_q8(rng, cols):
+    """Activations spread over 2^-6 .. 2^6 per 32-value block (scales of very
+    different sizes), so reordering the row's float terms changes the
+    rounded total in most trials."""
+    x = rng.standard_normal(cols) * np.repeat(np.exp2(rng.integers(-6, 7, cols // 32)), 32)
+    return oracle.quantize_q8(x.astype(np.float32), 1)
+
+
+@pytest.mark.parametrize("ty", [12, 14, 8, 2])
+def test_int_dot_float_combine_bit_exact(ty):
+    """The integer dots' float combines in the reference's expression and
+    order, restated step by step in float32 from the independent decoder's
+    integers and scales, bit for bit against the oracle's row:
+    Q4_K (simd.rs:556-581) total += da*(d1*i1 - mm1*sa) + db*(d2*i2 - mm2*sb)
+    per 64-value group, d1 = d*sc, mm1 = dmin*m;
+    Q6_K (simd.rs:612-663) total += d*sc*(ss - 32*sa)*da, left to right, in
+    the order half, sub, c (16-value groups 8*half + 2*c + sub);
+    Q4_0 (simd.rs:856-863) total += d*(i0 + i1 - 8*sum) as f32 * scale;
+    Q8_0 (simd.rs:882-891) total += d*i as f32 * scale."""
+    rng = np.random.default_rng(90 + ty)
+    bs, ts = BLOCK[ty]
+    cols = 2048
+    for trial in range(6):
+        w = random_blocks(ty, cols // bs, rng)
+        qs, dsc, sums, sums16 = _wide_q8(rng, cols)
+        got = oracle.dot_qk_q8_row(ty, w, (qs, dsc, sums, sums16))
+        iv = gf.int_values(ty, w)
+        a = qs.astype(np.int64)
+        b = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, ts)
+        total = _f32(0.0)
+        if ty == 12:
+            dot32 = (iv * a).reshape(-1, 32).sum(1)
+            d = gf.f16(b[:, 0], b[:, 1])
+            dmin = gf.f16(b[:, 2], b[:, 3])
+            sc, m = gf.unpack_scale_min_k4(b[:, 4:16])
+            for bi in range(b.shape[0]):
+                for g in range(4):
+                    ab = bi * 8 + 2 * g
+                    d1, mm1 = _f32(d[bi] * _f32(sc[bi, 2 * g])), _f32(dmin[bi] * _f32(m[bi, 2 * g]))
+                    d2, mm2 = _f32(d[bi] * _f32(sc[bi, 2 * g + 1])), _f32(dmin[bi] * _f32(m[bi, 2 * g + 1]))
+                    ta = _f32(dsc[ab] * _f32(_f32(d1 * _f32(dot32[ab])) - _f32(mm1 * _f32(sums[ab]))))
+                    tb = _f32(dsc[ab + 1] * _f32(_f32(d2 * _f32(dot32[ab + 1])) - _f32(mm2 * _f32(sums[ab + 1]))))
+                    total = _f32(total + _f32(ta + tb))
+        elif ty == 14:
+            dot16 = (iv * a).reshape(-1, 16).sum(1)
+            d = gf.f16(b[:, 208], b[:, 209])
+            scl = b[:, 192:208].view(np.int8)
+            for bi in range(b.shape[0]):
+                for half in range(2):
+                    for sub in range(2):
+                        for c in range(4):
+                            g16 = bi * 16 + half * 8 + 2 * c + sub
+                            s = _f32(scl[bi, half * 8 + sub + 2 * c])
+                            diff = _f32(_f32(dot16[g16]) - _f32(_f32(32.0) * _f32(sums16[g16])))
+                            term = _f32(_f32(_f32(d[bi] * s) * diff) * dsc[bi * 8 + half * 4 + c])
+                            total = _f32(total + term)
+        else:
+            dot32 = (iv * a).reshape(-1, 32).sum(1)
+            d = gf.f16(b[:, 0], b[:, 1])
+            for bi in range(b.shape[0]):
+                i = dot32[bi] - 8 * int(sums[bi]) if ty == 2 else dot32[bi]
+                total = _f32(total + _f32(_f32(d[bi] * _f32(i)) * dsc[bi]))
+        assert np.float32(got).view(np.uint32) == total.view(np.uint32), (trial, got, total)
+
+
+def test_rmsnorm_core_bit_exact():
+    """rmsnorm_core (simd.rs:282-326) restated in float32 with FMA emulated in
+    f64 (exact product, one rounding): accumulator a_m lane l takes elements
+    32i + 8m + l while 32 remain, then a_0 takes whole 8-blocks, the lanes
+    combine as (a0 + a1) + (a2 + a3) and the hsum tree ((A0+A4)+(A2+A6)) +
+    ((A1+A5)+(A3+A7)), the scalar tail adds v*v rounded; s = 1/sqrt(ss/n +
+    eps); out = (x*s)*w. Bit-exact on wide-range rows of every tail length."""
+    lib = oracle.load()
+    rng = np.random.default_rng(77)
+
+    def fma(x, y, z):
+        return _f32(np.float64(x) * np.float64(y) + np.float64(z))
+
+    for n in (32, 40, 47, 64, 96, 1000, 1024, 4101):
+        for trial in range(3):
+            x = (rng.standard_normal(n) * np.exp2(rng.integers(-6, 7, n))).astype(np.float32)
+            w = (1.0 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+            acc = [[_f32(0.0)] * 8 for _ in range(4)]
+            i = 0
+            while i + 32 <= n:
+                for mm in range(4):
+                    for l in range(8):
+                        v = x[i + 8 * mm + l]
+                        acc[mm][l] = fma(v, v, acc[mm][l])
+                i += 32
+            while i + 8 <= n:
+                for l in range(8):
+                    acc[0][l] = fma(x[i + l], x[i + l], acc[0][l])
+                i += 8
+            A = [_f32(_f32(acc[0][l] + acc[1][l]) + _f32(acc[2][l] + acc[3][l])) for l in range(8)]
+            ss = _f32(_f32(_f32(A[0] + A[4]) + _f32(A[2] + A[6])) + _f32(_f32(A[1] + A[5]) + _f32(A[3] + A[7])))
+            while i < n:
+                ss = _f32(ss + _f32(x[i] * x[i]))
+                i += 1
+            s = _f32(_f32(1.0) / np.sqrt(_f32(_f32(ss / _f32(n)) + _f32(1e-6))))
+            want = ((x * s).astype(np.float32) * w).astype(np.float32)
+            got = np.empty(n, np.float32)
+            lib.orc_rmsnorm_avx2(got.ctypes.data, x.ctypes.data, w.ctypes.data, n, 1e-6)
+            assert np.array_equal(bits(got), bits(want)), (n, trial)
