@@ -353,9 +353,12 @@ uint32_t* err_word(rlh_cache* c) { return c->st_dev + 4; }
 int sync_checked(rlh_cache* c) {
   HIPCHK(hipMemcpyAsync(c->host_st + 4, err_word(c), 4, hipMemcpyDeviceToHost, c->st));
   HIPCHK(hipStreamSynchronize(c->st));
-  if (c->host_st[4] != 0)
-    return fail(RLH_EDEVICE, "a bounded device wait expired (flags 0x" + std::to_string(c->host_st[4]) +
+  if (c->host_st[4] != 0) {
+    char buf[16];
+    std::snprintf(buf, sizeof buf, "0x%08x", c->host_st[4]);
+    return fail(RLH_EDEVICE, std::string("a bounded device wait expired (flags ") + buf +
                                  "); the cache holds undefined values until rlh_cache_reset");
+  }
   return RLH_OK;
 }
 
@@ -822,6 +825,10 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   uint64_t E = cfg.n_embd, F = cfg.n_ff, qd = (uint64_t)cfg.n_head * cfg.head_dim,
            kvd = (uint64_t)cfg.n_head_kv * cfg.head_dim;
   size_t kvbytes = (size_t)cfg.n_layer * max_ctx * kvd * 4;
+  // scratch holds the f32 rmsnorm row of the logits launch (E floats) and
+  // vocabulary- or F-sized temporaries: E can exceed both (a small or pruned
+  // vocabulary)
+  const size_t scratch_bytes = (size_t)std::max<uint64_t>(std::max<uint64_t>(cfg.vocab_size, F), E) * 4;
   bool ok = hipStreamCreate(&c->st) == hipSuccess && hipMalloc((void**)&c->kc, kvbytes) == hipSuccess &&
             hipMalloc((void**)&c->scores, (size_t)cfg.n_head * max_ctx * 4) == hipSuccess &&
             hipMalloc((void**)&c->vc, kvbytes) == hipSuccess && hipMalloc((void**)&c->x, E * 4) == hipSuccess &&
@@ -829,7 +836,7 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
             hipMalloc((void**)&c->v, kvd * 4) == hipSuccess && hipMalloc((void**)&c->attn, qd * 4) == hipSuccess &&
             hipMalloc((void**)&c->g, F * 4) == hipSuccess && hipMalloc((void**)&c->u, F * 4) == hipSuccess &&
             hipMalloc((void**)&c->logits, (size_t)cfg.vocab_size * 4) == hipSuccess &&
-            hipMalloc((void**)&c->scratch, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) == hipSuccess &&
+            hipMalloc((void**)&c->scratch, scratch_bytes) == hipSuccess &&
             hipMalloc((void**)&c->st_dev, 64) == hipSuccess &&
             hipMalloc((void**)&c->hist, (max_ctx + 2) * 4) == hipSuccess &&
             hipMalloc((void**)&c->pv, (size_t)npv * 4) == hipSuccess &&
@@ -847,7 +854,7 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
     return rc;
   }
   if (hipMemset(c->st_dev, 0, 64) != hipSuccess || hipMemset(c->kc, 0, kvbytes) != hipSuccess ||
-      hipMemset(c->vc, 0, kvbytes) != hipSuccess || hipMemset(c->scratch, 0, (size_t)std::max<uint64_t>(cfg.vocab_size, F) * 4) != hipSuccess ||
+      hipMemset(c->vc, 0, kvbytes) != hipSuccess || hipMemset(c->scratch, 0, scratch_bytes) != hipSuccess ||
       hipMemset(c->act_e.qs, 0, E) != hipSuccess || hipMemset(c->act_e.d, 0, E / 32 * 4) != hipSuccess ||
       hipMemset(c->act_e.s, 0, E / 32 * 4) != hipSuccess || hipMemset(c->act_e.s16, 0, E / 16 * 4) != hipSuccess) {
     cache_free(c);

@@ -164,6 +164,10 @@ SPECS = {
     "tiny-longff-q5": ModelSpec("tiny-longff-q5", 2, 256, 13056, 4, 2, 1000, False,
                                 {**_all(Q5_0, tied=False), T_FFN_DOWN: Q5_1, T_FFN_UP: Q4_1, T_FFN_GATE: Q4_1},
                                 n_ctx=512),
+    # hidden width above both the vocabulary and the FFN width (a small or
+    # pruned vocabulary): the cache's f32 temporaries must hold E floats
+    "tiny-smallvocab": ModelSpec("tiny-smallvocab", 2, 1024, 512, 8, 4, 300, False, _q4km(False, Q4_K, Q6_K),
+                                 n_ctx=512),
     # 8 query heads per KV head (the 32B grouping) and a long context window
     "tiny-g8-q4km": ModelSpec("tiny-g8-q4km", 2, 256, 512, 16, 2, 1000, True, _q4km(True, Q4_K, None), n_ctx=8192),
     # 4 query heads per KV head (the 4B / 8B grouping) and a long context window

@@ -42,7 +42,8 @@ def _greedy_ref(oc, prompt, n_gen):
     return logits, toks, per_step
 
 
-@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8_0", "tiny-q4_0", "tiny-q4km-untied", "small-q4km"])
+@pytest.mark.parametrize("name", ["tiny-q4km", "tiny-q8_0", "tiny-q4_0", "tiny-q4km-untied", "small-q4km",
+                                  "tiny-smallvocab"])
 def test_prefill_and_decode_bit_exact(name):
     print(f"forward parity {name}", flush=True)
     spec, tensors, m, om = _get(name)
