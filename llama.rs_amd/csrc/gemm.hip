@@ -39,8 +39,9 @@ typedef RLH_LDS uint8_t lbyte;
 constexpr uint32_t kTile = 64;                          // tokens and rows per block
 constexpr uint32_t kXStride = 272;                      // LDS bytes per token per super-block (16-byte pad)
 constexpr uint32_t kXBytes = kTile * kXStride;          // 17408
-constexpr uint32_t kDBytes = kTile * 8 * 4;             // da of 8 blocks per token
-constexpr uint32_t kStageBytes = kXBytes + 2 * kDBytes;  // + sums (Q4_K)
+constexpr uint32_t kDBytes = kTile * 8 * 4;             // da of 8 blocks per token, block-major [8][64]
+constexpr uint32_t kRBytes = kTile * 4 * 16;            // Q4_K row scales: [4 groups][64 rows] float4
+constexpr uint32_t kStageBytes = kXBytes + 2 * kDBytes + kRBytes;  // + sums as f32 (Q4_K), + row scales
 
 __device__ __forceinline__ uint64_t g8(const uint8_t* p) { return *(const RLH_GLOBAL uint64_t*)p; }
 __device__ __forceinline__ u32x4_t g16(const uint8_t* p) { return *(const RLH_GLOBAL u32x4_t*)p; }
@@ -70,15 +71,24 @@ struct Lane {
   uint32_t q, i16, tw, rw;
 };
 
-// Token-scale view of a staged super-block.
+// View of a staged super-block. The token scales and sums are block-major
+// ([block][token], so the four tokens a lane owns are one 16-byte read) for
+// Q4_K, Q8_0 and Q4_0, token-major ([token][block]) for Q6_K.
 struct StageView {
-  const lbyte* xs;      // [64][kXStride] Q8 bytes
-  const RLH_LDS float* d;    // [64][8] block scales
-  const RLH_LDS int32_t* s;  // [64][8] block sums
+  const lbyte* xs;            // [64][kXStride] Q8 bytes
+  const RLH_LDS float* d;     // block scales
+  const RLH_LDS float* s;     // Q4_K: block sums, as f32 (exact: |sum| <= 4064), block-major
+  const RLH_LDS f32x4_t* rs;  // Q4_K, [4][64]: {d*sc, dmin*m} of sub-blocks 2g, 2g+1 of each row
 };
 
 __device__ __forceinline__ StageView view(const lbyte* buf) {
-  return StageView{buf, (const RLH_LDS float*)(buf + kXBytes), (const RLH_LDS int32_t*)(buf + kXBytes + kDBytes)};
+  return StageView{buf, (const RLH_LDS float*)(buf + kXBytes), (const RLH_LDS float*)(buf + kXBytes + kDBytes),
+                   (const RLH_LDS f32x4_t*)(buf + kXBytes + 2 * kDBytes)};
+}
+
+// The lane's four tokens' values of block kb (scales or sums).
+__device__ __forceinline__ f32x4_t tok4(const RLH_LDS float* t, const Lane& ln, uint32_t tr, uint32_t kb) {
+  return *(const RLH_LDS f32x4_t*)(t + kb * kTile + 32 * ln.tw + 16 * tr + 4 * ln.q);
 }
 
 // A operands of block kb (0..7 inside the super-block) for token tile tr.
@@ -103,17 +113,18 @@ template <uint32_t TY>
 struct GT;
 
 // Q4_K: lane k-range 8q..8q+7 of block 2g is the low nibbles of item bytes
-// 16 + 32g + 8q .. +8, of block 2g+1 their high nibbles.
+// 16 + 32g + 8q .. +8, of block 2g+1 their high nibbles. The row scales
+// d*sc and dmin*m (get_scale_min_k4, quant.rs:176-185) are staged once per
+// super-block for the block's 64 rows (stage_store), not decoded per lane.
 template <>
 struct GT<RLH_TYPE_Q4_K> {
-  static constexpr bool kNeedS = true;
+  static constexpr bool kNeedS = true;  // block sums and row scales staged
+  static constexpr bool kBlockMajor = true;
   struct W {
-    u32x4_t hdr;
     uint64_t qs[4];
   };
   __device__ __forceinline__ static void load(W& r, const DevMat& w, uint32_t row, uint32_t j, uint32_t q) {
     const ItemPtr p = item_ptr(w, row, j);
-    r.hdr = g16(at(p, 0));
 #pragma unroll
     for (int g = 0; g < 4; g++) r.qs[g] = g8(at(p, 16 + 32 * g + 8 * q));
   }
@@ -128,52 +139,28 @@ struct GT<RLH_TYPE_Q4_K> {
         alo[tr] = a_frag(v, ln, tr, 2 * g);
         ahi[tr] = a_frag(v, ln, tr, 2 * g + 1);
       }
-      float d1[2], mm1[2], d2[2], mm2[2];
+      f32x4_t rsc[2];  // {d1, mm1, d2, mm2} of the lane's rows
       uint64_t blo[2], bhi[2];
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) {
         const uint64_t qg = g == 0 ? w[tc].qs[0] : (g == 1 ? w[tc].qs[1] : (g == 2 ? w[tc].qs[2] : w[tc].qs[3]));
         blo[tc] = qg & m4;
         bhi[tc] = (qg >> 4) & m4;
-        const float d = f16_to_f32(w[tc].hdr.x & 0xffff), dmin = f16_to_f32(w[tc].hdr.x >> 16);
-        const uint32_t s0 = w[tc].hdr.y, s1 = w[tc].hdr.z, s2 = w[tc].hdr.w;
-        const uint32_t sh1 = 16 * (g & 1), sh2 = sh1 + 8;
-        uint32_t sc1, m1, sc2, m2;  // get_scale_min_k4 (quant.rs:176-185), j = 2g, 2g+1
-        if (g < 2) {
-          sc1 = (s0 >> sh1) & 63;
-          m1 = (s1 >> sh1) & 63;
-          sc2 = (s0 >> sh2) & 63;
-          m2 = (s1 >> sh2) & 63;
-        } else {
-          sc1 = ((s2 >> sh1) & 0xF) | (((s0 >> sh1) >> 6 & 3) << 4);
-          m1 = ((s2 >> sh1) >> 4 & 0xF) | (((s1 >> sh1) >> 6 & 3) << 4);
-          sc2 = ((s2 >> sh2) & 0xF) | (((s0 >> sh2) >> 6 & 3) << 4);
-          m2 = ((s2 >> sh2) >> 4 & 0xF) | (((s1 >> sh2) >> 6 & 3) << 4);
-        }
-        d1[tc] = d * (float)sc1;
-        mm1[tc] = dmin * (float)m1;
-        d2[tc] = d * (float)sc2;
-        mm2[tc] = dmin * (float)m2;
+        rsc[tc] = v.rs[g * kTile + 32 * ln.rw + 16 * tc + ln.i16];
       }
 #pragma unroll
       for (int tr = 0; tr < 2; tr++) {
-        float da[4], db[4], sa[4], sb[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const uint32_t tok = 32 * ln.tw + 16 * tr + 4 * ln.q + e;
-          da[e] = v.d[tok * 8 + 2 * g];
-          db[e] = v.d[tok * 8 + 2 * g + 1];
-          sa[e] = (float)v.s[tok * 8 + 2 * g];
-          sb[e] = (float)v.s[tok * 8 + 2 * g + 1];
-        }
+        const f32x4_t da = tok4(v.d, ln, tr, 2 * g), db = tok4(v.d, ln, tr, 2 * g + 1);
+        const f32x4_t sa = tok4(v.s, ln, tr, 2 * g), sb = tok4(v.s, ln, tr, 2 * g + 1);
 #pragma unroll
         for (int tc = 0; tc < 2; tc++) {
           const v4i c1 = mfma(alo[tr], blo[tc]);
           const v4i c2 = mfma(ahi[tr], bhi[tc]);
+          const float d1 = rsc[tc].x, mm1 = rsc[tc].y, d2 = rsc[tc].z, mm2 = rsc[tc].w;
 #pragma unroll
           for (int e = 0; e < 4; e++)  // simd.rs:581
-            acc[tr][tc][e] = acc[tr][tc][e] + (da[e] * (d1[tc] * (float)c1[e] - mm1[tc] * sa[e]) +
-                                               db[e] * (d2[tc] * (float)c2[e] - mm2[tc] * sb[e]));
+            acc[tr][tc][e] = acc[tr][tc][e] + (da[e] * (d1 * (float)c1[e] - mm1 * sa[e]) +
+                                               db[e] * (d2 * (float)c2[e] - mm2 * sb[e]));
         }
       }
     }
@@ -186,6 +173,7 @@ struct GT<RLH_TYPE_Q4_K> {
 template <>
 struct GT<RLH_TYPE_Q6_K> {
   static constexpr bool kNeedS = false;
+  static constexpr bool kBlockMajor = false;  // four blocks of one token per read
   struct W {
     uint64_t ql[2][2], qh[2];
     u32x4_t sc;
@@ -245,7 +233,7 @@ struct GT<RLH_TYPE_Q6_K> {
         }
       }
       long a[2][4];
-      f32x4_t da[2][4];  // [tr][e] -> da of blocks 4h..4h+3
+      f32x4_t da[2][4];  // [tr][e] -> da of blocks 4h..4h+3 (token-major staging)
 #pragma unroll
       for (int tr = 0; tr < 2; tr++) {
 #pragma unroll
@@ -291,6 +279,7 @@ struct GT<RLH_TYPE_Q6_K> {
 template <>
 struct GT<RLH_TYPE_Q8_0> {
   static constexpr bool kNeedS = false;
+  static constexpr bool kBlockMajor = true;
   struct W {
     uint64_t qs[8];
     u32x4_t dv;
@@ -322,9 +311,7 @@ struct GT<RLH_TYPE_Q8_0> {
 #pragma unroll
       for (int tr = 0; tr < 2; tr++) {
         const long a = a_frag(v, ln, tr, k);
-        float da[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) da[e] = v.d[(32 * ln.tw + 16 * tr + 4 * ln.q + e) * 8 + k];
+        const f32x4_t da = tok4(v.d, ln, tr, k);
 #pragma unroll
         for (int tc = 0; tc < 2; tc++) {
           const v4i ci = mfma(a, qs[tc][0]);
@@ -352,6 +339,7 @@ struct GT<RLH_TYPE_Q8_0> {
 template <>
 struct GT<RLH_TYPE_Q4_0> {
   static constexpr bool kNeedS = false;
+  static constexpr bool kBlockMajor = true;
   struct W {
     uint64_t qs[8];
     u32x4_t dv;
@@ -389,9 +377,7 @@ struct GT<RLH_TYPE_Q4_0> {
 #pragma unroll
       for (int tr = 0; tr < 2; tr++) {
         const long a = a_frag(v, ln, tr, k);
-        float da[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) da[e] = v.d[(32 * ln.tw + 16 * tr + 4 * ln.q + e) * 8 + k];
+        const f32x4_t da = tok4(v.d, ln, tr, k);
 #pragma unroll
         for (int tc = 0; tc < 2; tc++) {
           const v4i ci = mfma(a, b[tc]);
@@ -415,59 +401,138 @@ struct GT<RLH_TYPE_Q4_0> {
 
 // Stages super-block j of the block's 64 tokens: Q8 bytes into the padded
 // [64][272] layout (17 slots of 16 bytes per token, the 17th unused), the 8
-// block scales and (Q4_K) the 8 block sums per token. Slot p of the staged
-// super-block is thread p % 256's job p / 256. The copy goes through
-// registers: stage_load issues the global loads at the top of a super-block
-// step and stage_store writes them to LDS at its end, so their latency hides
-// behind the step's products. (Copies straight into LDS, global_load_lds,
-// measured ~0.5 us per instruction per wave here: the step's copies took as
-// long as its products.) Slots past the valid tokens or the 17th slot of a
+// block scales of every token, and for Q4_K the 8 block sums (as f32) and the
+// 64 rows' scale headers turned into {d*sc, dmin*m} pairs. Scales and sums
+// are stored block-major ([block][token]) for the types that read them four
+// tokens at a time (Q4_K, Q8_0, Q4_0), token-major for Q6_K (four blocks of
+// one token at a time). The copy goes through registers: stage_load issues
+// the global loads at the top of a super-block step and stage_store writes
+// them to LDS at its end, so their latency hides behind the step's products.
+// (Copies straight into LDS, global_load_lds, measured ~0.5 us per
+// instruction per wave here: the step's copies took as long as its
+// products.) Jobs of thread t, wave w = t / 64 (every role is whole waves,
+// so the branches are uniform): jobs 0-3 Q8 slots t + 256k; job 4 Q8 slots
+// 1024-1087 (wave 0), the scales (waves 1-2: 128 slots of 16 bytes, token
+// (t - 64) / 2, blocks 4 ((t - 64) & 1) .. +3), the sums of tokens 0-31
+// (wave 3, Q4_K); job 5 (Q4_K) the sums of tokens 32-63 (wave 0) and the
+// row headers (wave 1). Slots past the valid tokens or the 17th slot of a
 // token load a clamped, valid address and are not stored.
-constexpr uint32_t kStageJobs = 6;  // ceil((64 * 17 + 2 * 64 * 2) / 256)
+constexpr uint32_t kStageJobs = 6;
 
 struct StageRegs {
   u32x4_t v[kStageJobs];
-  const uint8_t* src[kStageJobs];  // job k's source for the current super-block
+  const uint8_t* src[kStageJobs];  // job k's source for the current super-block (not the header job)
   uint32_t keep;                   // bit k: job k is stored
-  uint32_t small;                  // bit k: job k is a scale or sum slot (32-byte step per super-block)
+  uint32_t sub4, sub5;             // jobs 4/5: scale or sum slot (token * 2 + half), or the header row
 };
 
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // Sources of super-block 0; super-block j + 1 is 256 bytes further for Q8
-// bytes and 32 bytes for scales and sums.
-__device__ __forceinline__ void stage_init(StageRegs& r, const GemmArgs& a, uint32_t t0, bool need_s) {
-  const uint32_t cols = a.w.cols, nb = cols / 32;
-  const uint32_t nx = kTile * 17, nd = kTile * 2, total = nx + nd + (need_s ? nd : 0);
+// bytes and 32 bytes for scales and sums; the header job addresses item
+// (row, j) itself.
+__device__ __forceinline__ void stage_init(StageRegs& r, const GemmArgs& a, uint32_t t0, bool q4k) {
+  const uint32_t cols = a.w.cols, nb = cols / 32, t = threadIdx.x, w = wave_id();
   r.keep = 0;
-  r.small = 0;
+  auto q8_job = [&](uint32_t k, uint32_t p) {
+    const uint32_t tok = p / 17, ch = p - tok * 17;
+    r.keep |= (ch < 16 && t0 + tok < a.n) ? 1u << k : 0u;
+    r.src[k] = (const uint8_t*)a.x.qs + (size_t)min(t0 + tok, a.n - 1) * cols + 16 * min(ch, 15u);
+  };
+  auto small_job = [&](uint32_t k, const void* base, uint32_t slot) {
+    const uint32_t tok = slot >> 1;
+    r.keep |= t0 + tok < a.n ? 1u << k : 0u;
+    r.src[k] = (const uint8_t*)base + ((size_t)min(t0 + tok, a.n - 1) * nb + 4 * (slot & 1)) * 4;
+  };
 #pragma unroll
-  for (uint32_t k = 0; k < kStageJobs; k++) {
-    const uint32_t p = threadIdx.x + 256 * k, pc = p < total ? p : total - 1;
-    if (pc < nx) {
-      const uint32_t tok = pc / 17, ch = pc - tok * 17;
-      r.keep |= (p < total && ch < 16 && t0 + tok < a.n) ? 1u << k : 0u;
-      r.src[k] = (const uint8_t*)a.x.qs + (size_t)min(t0 + tok, a.n - 1) * cols + 16 * min(ch, 15u);
+  for (uint32_t k = 0; k < 4; k++) q8_job(k, t + 256 * k);
+  r.sub4 = r.sub5 = 0;
+  r.src[4] = r.src[5] = (const uint8_t*)a.x.d;
+  if (w == 0) {
+    q8_job(4, t + 1024);
+  } else if (w <= 2) {
+    r.sub4 = t - 64;
+    small_job(4, a.x.d, r.sub4);
+  } else if (q4k) {
+    r.sub4 = t - 192;
+    small_job(4, a.x.s, r.sub4);
+  }
+  if (q4k && w == 0) {
+    r.sub5 = t + 64;
+    small_job(5, a.x.s, r.sub5);
+  } else if (q4k && w == 1) {
+    r.sub5 = t - 64;
+    r.keep |= 1u << 5;
+  }
+}
+
+__device__ __forceinline__ void stage_load(StageRegs& r, const GemmArgs& a, uint32_t row0, uint32_t j, bool q4k) {
+  const uint32_t w = wave_id();
+#pragma unroll
+  for (uint32_t k = 0; k < 5; k++) {
+    r.v[k] = *(const RLH_GLOBAL u32x4_t*)r.src[k];
+    r.src[k] += (k < 4 || w == 0) ? 256 : 32;
+  }
+  if (q4k && w == 0) {
+    r.v[5] = *(const RLH_GLOBAL u32x4_t*)r.src[5];
+    r.src[5] += 32;
+  } else if (q4k && w == 1) {  // the row's d, dmin and 12 scale bytes (item bytes 0..15)
+    r.v[5] = *(const RLH_GLOBAL u32x4_t*)item_ptr(a.w, min(row0 + r.sub5, a.w.rows - 1), j).base;
+  }
+}
+
+// A scale or sum slot (token slot >> 1, blocks 4 (slot & 1) .. +3) into LDS.
+__device__ __forceinline__ void store_small(lbyte* buf, bool sum, bool block_major, uint32_t slot, const u32x4_t& v) {
+  RLH_LDS float* base = (RLH_LDS float*)(buf + kXBytes + (sum ? kDBytes : 0u));
+  const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  if (block_major) {
+    RLH_LDS float* t = base + 4 * (slot & 1) * kTile + (slot >> 1);
+#pragma unroll
+    for (int i = 0; i < 4; i++) t[i * kTile] = sum ? (float)(int32_t)w4[i] : __uint_as_float(w4[i]);
+  } else {
+    *(RLH_LDS u32x4_t*)(base + 4 * slot) = v;
+  }
+}
+
+template <bool kBlockMajor>
+__device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf, bool q4k) {
+  const uint32_t t = threadIdx.x, w = wave_id();
+#pragma unroll
+  for (uint32_t k = 0; k < 4; k++)
+    if (r.keep >> k & 1u) *(RLH_LDS u32x4_t*)(buf + (t + 256 * k) * 16) = r.v[k];
+  if (r.keep >> 4 & 1u) {
+    if (w == 0) *(RLH_LDS u32x4_t*)(buf + (t + 1024) * 16) = r.v[4];
+    else store_small(buf, w == 3, kBlockMajor, r.sub4, r.v[4]);
+  }
+  if (q4k && (r.keep >> 5 & 1u)) {
+    if (w == 0) {
+      store_small(buf, true, kBlockMajor, r.sub5, r.v[5]);
     } else {
-      const uint32_t r0 = pc - (pc < nx + nd ? nx : nx + nd), tok = r0 >> 1;
-      r.keep |= (p < total && t0 + tok < a.n) ? 1u << k : 0u;
-      r.small |= 1u << k;
-      const uint8_t* base = pc < nx + nd ? (const uint8_t*)a.x.d : (const uint8_t*)a.x.s;
-      r.src[k] = base + ((size_t)min(t0 + tok, a.n - 1) * nb + 4 * (r0 & 1)) * 4;
+      // get_scale_min_k4 (quant.rs:176-185) of the 8 sub-blocks; the pairs
+      // d*sc, dmin*m of sub-blocks 2g, 2g+1 (exact in f32: an f16 times a
+      // 6-bit integer)
+      const u32x4_t v = r.v[5];
+      RLH_LDS f32x4_t* rs = (RLH_LDS f32x4_t*)(buf + kXBytes + 2 * kDBytes);
+      const float dd = f16_to_f32(v.x & 0xffff), dmin = f16_to_f32(v.x >> 16);
+      const uint32_t s0 = v.y, s1 = v.z, s2 = v.w;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        uint32_t sc[2], m[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const uint32_t sh = 16 * (g & 1) + 8 * h;
+          if (g < 2) {
+            sc[h] = (s0 >> sh) & 63;
+            m[h] = (s1 >> sh) & 63;
+          } else {
+            sc[h] = ((s2 >> sh) & 0xF) | (((s0 >> sh) >> 6 & 3) << 4);
+            m[h] = ((s2 >> sh) >> 4 & 0xF) | (((s1 >> sh) >> 6 & 3) << 4);
+          }
+        }
+        rs[g * kTile + r.sub5] = f32x4_t{dd * (float)sc[0], dmin * (float)m[0], dd * (float)sc[1], dmin * (float)m[1]};
+      }
     }
   }
-}
-
-__device__ __forceinline__ void stage_load(StageRegs& r) {
-#pragma unroll
-  for (uint32_t k = 0; k < kStageJobs; k++) {
-    r.v[k] = *(const RLH_GLOBAL u32x4_t*)r.src[k];
-    r.src[k] += (r.small >> k & 1u) ? 32 : 256;
-  }
-}
-
-__device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf) {
-#pragma unroll
-  for (uint32_t k = 0; k < kStageJobs; k++)
-    if (r.keep >> k & 1u) *(RLH_LDS u32x4_t*)(buf + (threadIdx.x + 256 * k) * 16) = r.v[k];
 }
 
 template <uint32_t TY>
@@ -502,13 +567,13 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
 #pragma unroll
   for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
   stage_init(sr, a, t0, G::kNeedS);
-  stage_load(sr);
-  stage_store(sr, lds);
+  stage_load(sr, a, r0, 0, G::kNeedS);
+  stage_store<G::kBlockMajor>(sr, lds, G::kNeedS);
   __syncthreads();
   for (uint32_t j = 0; j < nsb; j++) {
     const bool more = j + 1 < nsb;
     if (more) {
-      stage_load(sr);
+      stage_load(sr, a, r0, j + 1, G::kNeedS);
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) G::load(wn[tc], a.w, rowc[tc], j + 1, ln.q);
     }
@@ -516,7 +581,7 @@ __global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
     if (more) {
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) wc[tc] = wn[tc];
-      stage_store(sr, lds + ((j + 1) & 1) * kStageBytes);  // that buffer was freed by the last barrier
+      stage_store<G::kBlockMajor>(sr, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS);  // freed by the last barrier
     }
     __syncthreads();  // the next stage is in LDS; the current buffer is free
   }

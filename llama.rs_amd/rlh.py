@@ -12,7 +12,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "librlh.so")
+LIB_PATH = os.environ.get("RLH_LIB") or os.path.join(_HERE, "librlh.so")  # RLH_LIB: another build of the library
 
 # ggml type ids (src/quant.rs:26-41)
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 6, 7, 8, 12, 13, 14, 30
