@@ -51,9 +51,12 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8, published
 
 WORKLOADS = rlh.WORKLOADS
 
-# CPU oracle sample per workload: (prompt tokens prefilled in each mode,
-# greedy decode tokens), sized for roughly 10-30 s of host work.
-CPU_SAMPLE = {1: (48, 32), 2: (48, 128), 3: (128, 64), 4: (128, 64), 5: (32, 8)}
+# CPU oracle sample per workload: (prompt tokens prefilled in the default
+# mode, prompt tokens prefilled with RUST_LLAMA_BATCH_INT=1, greedy decode
+# tokens after the default-mode prefill), sized for roughly 10-30 s of host
+# work. Where the default-mode prefill is the workload's whole prompt, the
+# CPU decodes at the start of the GPU's decode window.
+CPU_SAMPLE = {1: (48, 48, 32), 2: (48, 48, 128), 3: (256, 128, 64), 4: (512, 128, 32), 5: (32, 32, 8)}
 
 METRIC = "decode tok/s, prefill tok/s, % HBM roofline"
 MODEL_NAMES = {"qwen3-0.6b-q4km": "Qwen3-0.6B Q4_K_M", "qwen3-0.6b-q8_0": "Qwen3-0.6B Q8_0",
@@ -101,22 +104,22 @@ def run_pass(cache, prompt, n_decode, sampled, params, never):
     return prefill_s, time.perf_counter() - t1, recent[P:].copy()
 
 
-def cpu_baseline(spec, tensors, prompt, n_prompt, n_decode):
+def cpu_baseline(spec, tensors, prompt, n_prompt, n_prompt_int, n_decode):
     """The oracle on the host cores: prefill of n_prompt tokens in the
-    reference's default mode (f32 fused products, as shipped) and with
-    RUST_LLAMA_BATCH_INT=1, then n_decode greedy tokens in the default mode
-    (AVX2 integer path), by the cmd_bench protocol."""
+    reference's default mode (f32 fused products, as shipped), then n_decode
+    greedy tokens in the default mode (AVX2 integer path), by the cmd_bench
+    protocol; then a prefill of n_prompt_int tokens with
+    RUST_LLAMA_BATCH_INT=1."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
     lib = oracle.load()
     threads = lib.orc_get_threads()
     om = oracle.OracleModel(spec, tensors)
-    oc = om.new_cache(n_prompt + n_decode + 1)
-    p = prompt[:n_prompt]
+    oc = om.new_cache(max(n_prompt + n_decode, n_prompt_int) + 1)
     t0 = time.time()
-    res_def, toks = oc.bench(p, n_decode, oracle.MODE_DEFAULT, warmup=False)
-    res_int, _ = oc.bench(p, 0, oracle.MODE_BATCH_INT, warmup=False)
+    res_def, toks = oc.bench(prompt[:n_prompt], n_decode, oracle.MODE_DEFAULT, warmup=False)
+    res_int, _ = oc.bench(prompt[:n_prompt_int], 0, oracle.MODE_BATCH_INT, warmup=False)
     wall = time.time() - t0
     oc.close()
     om.close()
@@ -124,6 +127,21 @@ def cpu_baseline(spec, tensors, prompt, n_prompt, n_decode):
             "prefill_tok_s_default": res_def.prompt_len / res_def.prefill_s,
             "prefill_tok_s_batch_int": res_int.prompt_len / res_int.prefill_s,
             "generated": res_def.generated, "threads": threads, "wall_s": wall}
+
+
+def trace_launch_us(config):
+    """Average duration of the dominant kernel (k_mv<TY, 2>) over the decode
+    launches of the committed rocprofv3 kernel trace of this workload
+    (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", f"decode_prefill_kernels_{config}_stats.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("#   decode passes,") and "avg" in line:
+                    return float(line.split("avg", 1)[1].split("us")[0])
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def measured_traffic(config):
@@ -263,6 +281,12 @@ def main():
     probe_steps = max(1, min(args.probe_steps, n_decode))
     mv_us, mv_launches = cache.profile_decode_kernel(rlh.T_FFN_GATE, cache.greedy_next(), probe_steps)
     mv_gbs = pair_bytes / (mv_us * 1e-6) / 1e9
+    # the same kernel launched back to back (one event pair around them all,
+    # rotating over every layer's weights so that they stream from HBM), and
+    # its average over the decode launches of the committed kernel trace
+    b2b_launches = spec.n_layer * 8
+    b2b_us = cache.profile_matvec(rlh.T_FFN_GATE, b2b_launches)
+    tr_us = trace_launch_us(config)
     traffic = measured_traffic(config)
 
     model_name = MODEL_NAMES[config]
@@ -300,6 +324,13 @@ def main():
                      "achieved": round(mv_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(mv_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "avg_launch_us": round(mv_us, 3), "launches_timed": int(mv_launches),
+                     "timing": "HIP events bound to each launch inside decode steps (about 0.9 us longer than "
+                               "an unbound launch)",
+                     "back_to_back_us": round(b2b_us, 3), "back_to_back_launches": b2b_launches,
+                     "frac_back_to_back": round(pair_bytes / (b2b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "trace_us": tr_us,
+                     "frac_trace": (round(pair_bytes / (tr_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                    if tr_us else None),
                      "bytes_per_launch": int(pair_bytes)},
         "decode": "sampled" if sampled else "greedy",
         "sampled_decode_tok_s": sampled_tok_s,
@@ -309,15 +340,17 @@ def main():
     if args.no_cpu:
         out["cpu_baseline"] = None
     else:
-        cp, cd = CPU_SAMPLE[args.workload]
-        r = cpu_baseline(spec, tensors, prompt, cp, cd)
+        cp, ci, cd = CPU_SAMPLE[args.workload]
+        r = cpu_baseline(spec, tensors, prompt, cp, ci, cd)
         out["cpu_baseline"] = {
             "value": round(r["decode_tok_s"], 3), "unit": "tok/s", "cores": r["threads"], "kind": "port",
             "prefill_tok_s_default": round(r["prefill_tok_s_default"], 2),
             "prefill_tok_s_batch_int": round(r["prefill_tok_s_batch_int"], 2),
             "sample": f"oracle (C++ restatement of the reference's AVX2 path) on {config}, {r['threads']} threads: "
-                      f"{cp}-token prefill in the default mode and with RUST_LLAMA_BATCH_INT=1, then "
-                      f"{r['generated']} greedy decode tokens (cmd_bench protocol; {r['wall_s']:.1f}s of host work)"}
+                      f"{cp}-token prefill in the default mode, then {r['generated']} greedy decode tokens at "
+                      f"KV {cp} -> {cp + r['generated']} (the GPU decodes KV {n_prompt} -> {n_prompt + n_decode}), "
+                      f"then a {ci}-token prefill with RUST_LLAMA_BATCH_INT=1 (cmd_bench protocol; "
+                      f"{r['wall_s']:.1f}s of host work)"}
         log(f"cpu oracle: decode {r['decode_tok_s']:.2f} tok/s, prefill {r['prefill_tok_s_default']:.2f} "
             f"(default) / {r['prefill_tok_s_batch_int']:.2f} (BATCH_INT) tok/s, {r['threads']} threads")
 
