@@ -30,6 +30,9 @@ struct AttnArgs {
   float* out;    // [n_tok][H*128]
   Q8Mut out_q8;  // Q8 blocks of out
   uint32_t* err; // device error word (nullable): an expired bounded wait sets kErrAttnExp
+  // test knob of the decode softmax's exact parallel sum (0 in use): shifts
+  // the walk's predicted binades so that runs replay (block_softmax_sum)
+  int walk_shift;
 };
 
 // Query heads per KV head the kernels accept (1..8).

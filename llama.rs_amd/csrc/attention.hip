@@ -408,7 +408,12 @@ struct SoftmaxSumLds {
   float wsum[4];
   float out;
 };
-__device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* sl) {
+// shift (a test knob, 0 in use): 1 / 2 move every run's predicted binade
+// one up / down, 3 every third run's one up (scans that pass runs, then
+// stop); a shifted prediction never equals the exact state's binade, so
+// each such run is replayed from its exact start, and the sum must not
+// change.
+__device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* sl, int shift) {
   RLH_LDS SoftmaxSumLds* L = (RLH_LDS SoftmaxSumLds*)sl;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (t < kSoftmaxWalkMin) {
@@ -439,7 +444,8 @@ __device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* s
   }
   float base = 0.0f;
   for (uint32_t w = 0; w < wave; w++) base += L->wsum[w];
-  const int ur = mono_binade(base + inc - a);
+  int ur = mono_binade(base + inc - a);
+  if (shift) ur += shift == 1 ? 1 : (shift == 2 ? -1 : (tid % 3 == 0 ? 1 : 0));
   const MonoFn f = mono_run_pair(e + j0, j1 - j0, ur);
   L->a0[tid] = f.a0;
   L->a1[tid] = f.a1;
@@ -488,7 +494,7 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   float inv;
   if constexpr (WALK) {
     __shared__ SoftmaxSumLds ssl;  // only in the decode instantiation
-    const float sum = block_softmax_sum(e, t, &ssl);  // the sequential sum of softmax_inplace
+    const float sum = block_softmax_sum(e, t, &ssl, a.walk_shift);  // the sequential sum of softmax_inplace
     on = sum > 0.0f;
     inv = 1.0f / sum;
   } else {

@@ -308,6 +308,7 @@ struct rlh_cache {
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
   bool debug = false;
   bool use_graphs = true;  // RLH_GRAPHS=0 launches the same kernels eagerly
+  int walk_shift = 0;      // RLH_SOFTMAX_WALK_SHIFT=1|2|3: a test knob of the decode softmax sum (AttnArgs::walk_shift)
   float* dbg = nullptr;  // [L][kDbgTokens][E]
   uint64_t dbg_tokens = 0;
   bool logits_valid = false;
@@ -438,6 +439,7 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
       a.max_ctx = (uint32_t)c->max_ctx;
       a.n_tok = 1;
       a.err = err_word(c);
+      a.walk_shift = c->walk_shift;
       a.H = (int)H;
       a.KVH = (int)KVH;
       a.eps = eps;
@@ -862,6 +864,8 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   }
   const char* env = std::getenv("RLH_GRAPHS");
   c->use_graphs = !(env && std::strcmp(env, "0") == 0);
+  const char* wenv = std::getenv("RLH_SOFTMAX_WALK_SHIFT");
+  if (wenv && wenv[0] >= '1' && wenv[0] <= '3' && wenv[1] == 0) c->walk_shift = wenv[0] - '0';
   if (c->use_graphs &&
       ((rc = capture(c, STEP_LOGITS, &c->g_logits)) || (rc = capture(c, STEP_NOLOGITS, &c->g_nologits)) ||
        (rc = capture(c, STEP_GREEDY, &c->g_greedy)))) {

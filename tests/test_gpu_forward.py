@@ -388,3 +388,41 @@ def test_qwen2_biases_bit_exact():
         oc.close()
         m.close()
         om.close()
+
+
+@pytest.mark.parametrize("n_prompt", [1100, 4100])
+def test_softmax_walk_replays_bit_exact(n_prompt, monkeypatch):
+    """The decode softmax's exact parallel sum (rows of 1024 positions or
+    more; 8 query heads per KV head take k_attn_softmax) with its replay
+    paths forced by RLH_SOFTMAX_WALK_SHIFT, which moves the runs' predicted
+    binades: 1 every run's one up, 2 one down (every run is replayed from
+    its exact start, a walk pass per run, stops at every lane of a 64-run
+    group including the last), 3 every third run's one up (scans that pass
+    two runs, then stop). The sum, and so every logit, must not change:
+    bit-exact against the oracle's sequential loop in every mode, six decode
+    steps each, and equal to the unforced run."""
+    print(f"softmax walk replays, prompt {n_prompt}", flush=True)
+    spec, tensors, m, om = _get("tiny-g8-q4km")
+    prompt = rlh.synth_tokens(78, n_prompt, spec.vocab)
+    max_ctx = n_prompt + 16
+    lib = oracle.load()
+    oc = om.new_cache(max_ctx)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    toks, refs = [lib.orc_argmax(rg.ctypes.data, len(rg))], []
+    for i in range(6):
+        rg = oc.forward_into(np.array([toks[-1]], np.uint32), n_prompt + i, oracle.MODE_DEFAULT)
+        refs.append(rg)
+        toks.append(lib.orc_argmax(rg.ctypes.data, len(rg)))
+    oc.close()
+    for mode in ("0", "1", "2", "3"):
+        print(f"  walk shift mode {mode}", flush=True)
+        monkeypatch.setenv("RLH_SOFTMAX_WALK_SHIFT", mode)
+        c = m.new_cache(max_ctx)
+        try:
+            c.forward_into(prompt, 0)
+            for i in range(6):
+                lg = c.forward_into(np.array([toks[i]], np.uint32), n_prompt + i)
+                assert np.array_equal(bits(lg), bits(refs[i])), \
+                    f"mode {mode} step {i}: logits differ (rel {rel_l2(lg, refs[i]):.2e})"
+        finally:
+            c.close()
