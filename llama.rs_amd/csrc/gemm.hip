@@ -244,20 +244,26 @@ struct GT<RLH_TYPE_Q6_K> {
           da[tr][e] = *(const RLH_LDS f32x4_t*)(v.d + tok * 8 + 4 * h);
         }
       }
-      // terms in the order s = 0 (c = 0..3), then s = 1 (simd.rs:630-665)
+      // terms in the order s = 0 (c = 0..3), then s = 1 (simd.rs:630-665);
+      // the four products of a (s, c) step are issued before their
+      // combines, so no combine waits on the product just issued
 #pragma unroll
       for (int s = 0; s < 2; s++) {
         const bool keep = (s == 1) == sub1;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
+          v4i ci[2][2];
+#pragma unroll
+          for (int tr = 0; tr < 2; tr++)
+#pragma unroll
+            for (int tc = 0; tc < 2; tc++) ci[tr][tc] = mfma(a[tr][c], keep ? bq[tc][c] : 0ull);
 #pragma unroll
           for (int tr = 0; tr < 2; tr++) {
 #pragma unroll
             for (int tc = 0; tc < 2; tc++) {
-              const v4i ci = mfma(a[tr][c], keep ? bq[tc][c] : 0ull);
 #pragma unroll
               for (int e = 0; e < 4; e++)  // simd.rs:663
-                acc[tr][tc][e] = acc[tr][tc][e] + dsc[tc][s][c] * (float)ci[e] * da[tr][e][c];
+                acc[tr][tc][e] = acc[tr][tc][e] + dsc[tc][s][c] * (float)ci[tr][tc][e] * da[tr][e][c];
             }
           }
         }
