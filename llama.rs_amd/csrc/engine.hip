@@ -309,6 +309,11 @@ struct rlh_cache {
   bool debug = false;
   bool use_graphs = true;  // RLH_GRAPHS=0 launches the same kernels eagerly
   int walk_shift = 0;      // RLH_SOFTMAX_WALK_SHIFT=1|2|3: a test knob of the decode softmax sum (AttnArgs::walk_shift)
+  // prefill: the attn_k and attn_v products run on two more streams beside
+  // attn_q's (their 1024-row grids fill a quarter of the GPU on their own);
+  // null when RLH_PREFILL_STREAMS=0 or their creation failed (one stream)
+  hipStream_t side[2] = {nullptr, nullptr};
+  hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
   float* dbg = nullptr;  // [L][kDbgTokens][E]
   uint64_t dbg_tokens = 0;
   bool logits_valid = false;
@@ -798,6 +803,11 @@ static void cache_free(rlh_cache* c) {
     if (p) (void)hipFree(p);
   if (c->host_st) (void)hipHostFree(c->host_st);
   if (c->ds) rlh_dsampler_destroy(c->ds);
+  for (int i = 0; i < 2; i++) {
+    if (c->side[i]) (void)hipStreamDestroy(c->side[i]);
+    if (c->ev_join[i]) (void)hipEventDestroy(c->ev_join[i]);
+  }
+  if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
 }
@@ -864,6 +874,17 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
   }
   const char* env = std::getenv("RLH_GRAPHS");
   c->use_graphs = !(env && std::strcmp(env, "0") == 0);
+  const char* senv = std::getenv("RLH_PREFILL_STREAMS");
+  if (!(senv && std::strcmp(senv, "0") == 0)) {
+    bool sok = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming) == hipSuccess;
+    for (int i = 0; i < 2 && sok; i++)
+      sok = hipStreamCreate(&c->side[i]) == hipSuccess &&
+            hipEventCreateWithFlags(&c->ev_join[i], hipEventDisableTiming) == hipSuccess;
+    if (!sok) {  // one stream then; what was created is released with the cache
+      c->side[0] = c->side[1] = nullptr;
+      (void)hipGetLastError();
+    }
+  }
   const char* wenv = std::getenv("RLH_SOFTMAX_WALK_SHIFT");
   if (wenv && wenv[0] >= '1' && wenv[0] <= '3' && wenv[1] == 0) c->walk_shift = wenv[0] - '0';
   if (c->use_graphs &&
@@ -997,20 +1018,40 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
     // products give the last n % 4 tokens of the call the single-token order)
     const uint64_t n4_all = n - n % 4;
     const uint32_t n4 = (uint32_t)std::min<uint64_t>(mtok, n4_all > c0 ? n4_all - c0 : 0);
-    auto product = [&](const DevMat& w, const Q8Buf& q8, const float* xf, float* y, float* resid) {
+    auto product_on = [&](hipStream_t s, const DevMat& w, const Q8Buf& q8, const float* xf, float* y,
+                          float* resid) {
       if (gemm_supported(w.ty))
-        launch_gemm(st, w, q8, mtok, y, resid);
+        launch_gemm(s, w, q8, mtok, y, resid);
       else
-        launch_gemm_f32(st, w, xf, mtok, n4, y, resid);
+        launch_gemm_f32(s, w, xf, mtok, n4, y, resid);
+    };
+    auto product = [&](const DevMat& w, const Q8Buf& q8, const float* xf, float* y, float* resid) {
+      product_on(st, w, q8, xf, y, resid);
     };
     float* xn = m->f32_route ? c->xnb : nullptr;  // f32 rmsnorm rows, when a product needs them
     launch_embed(st, m->token_embd.dm, c->tokb + c0, mtok, c->xb);
     for (uint32_t l = 0; l < cfg.n_layer; l++) {
       Layer& L = m->layers[l];
       launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, xn);
-      product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
-      product(L.k.dm, c->act_eb, xn, c->kb, nullptr);
-      product(L.v.dm, c->act_eb, xn, c->vb, nullptr);
+      if (c->side[0] && c->side[1]) {
+        // k and v beside q: the side streams start after the norm and the
+        // main stream waits for both before the next kernel reads k and v
+        // (nothing writes the norm's outputs before that join)
+        HIPCHK(hipEventRecord(c->ev_fork, st));
+        HIPCHK(hipStreamWaitEvent(c->side[0], c->ev_fork, 0));
+        HIPCHK(hipStreamWaitEvent(c->side[1], c->ev_fork, 0));
+        product_on(c->side[0], L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        product_on(c->side[1], L.v.dm, c->act_eb, xn, c->vb, nullptr);
+        HIPCHK(hipEventRecord(c->ev_join[0], c->side[0]));
+        HIPCHK(hipEventRecord(c->ev_join[1], c->side[1]));
+        product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
+        HIPCHK(hipStreamWaitEvent(st, c->ev_join[0], 0));
+        HIPCHK(hipStreamWaitEvent(st, c->ev_join[1], 0));
+      } else {
+        product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
+        product(L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        product(L.v.dm, c->act_eb, xn, c->vb, nullptr);
+      }
       launch_qk_norm_rope_kv(st, c->qb, c->kb, c->vb, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
                              cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
                              (int)H, (int)KVH, mtok, eps);
