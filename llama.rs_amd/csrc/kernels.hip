@@ -212,15 +212,25 @@ __global__ void __launch_bounds__(64) k_qk_norm_rope_kv(float* q, float* k, cons
 // model.rs:722-724, 565-567), then quantize_q8 of h (ffn_down input).
 // grid covers n_total = n_tokens * F elements, 256 per block.
 // ---------------------------------------------------------------------------
+// Four consecutive values per thread (16-byte loads), eight threads per Q8
+// block of 32; the expf table in LDS. n_total is a multiple of 32, so a
+// block of 32 values never straddles the end.
 __global__ void __launch_bounds__(256) k_swiglu_q8(const float* g, const float* u, uint32_t n_total, Q8Out out,
                                                    float* h_out) {
-  uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (blockIdx.x * 256 + (threadIdx.x & ~31u) >= n_total) return;
-  float x = g[i];
-  float sl = x / (1.0f + expf_glibc(-x));
-  float h = sl * u[i];
-  if (h_out) h_out[i] = h;
-  q8_quant_block32(h, out, i / 32);
+  __shared__ uint64_t tab_g[32];
+  lu64* tab = (lu64*)tab_g;
+  exp_tab_to_lds(tab);
+  __syncthreads();
+  const uint32_t i4 = blockIdx.x * 256 + threadIdx.x;  // float4 index
+  if (blockIdx.x * 256 + (threadIdx.x & ~7u) >= n_total / 4) return;
+  const float4 x = ((const float4*)g)[i4], uu = ((const float4*)u)[i4];
+  // ops.rs:393-395 per value: silu(x) = x / (1 + exp(-x)), times up
+  const float h0 = (x.x / (1.0f + expf_glibc_t(-x.x, tab))) * uu.x;
+  const float h1 = (x.y / (1.0f + expf_glibc_t(-x.y, tab))) * uu.y;
+  const float h2 = (x.z / (1.0f + expf_glibc_t(-x.z, tab))) * uu.z;
+  const float h3 = (x.w / (1.0f + expf_glibc_t(-x.w, tab))) * uu.w;
+  if (h_out) ((float4*)h_out)[i4] = float4{h0, h1, h2, h3};
+  q8_quant_block8x4(h0, h1, h2, h3, out, i4 / 8);
 }
 
 // ---------------------------------------------------------------------------
@@ -360,7 +370,7 @@ void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, 
 
 void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
                       float* h_out) {
-  hipLaunchKernelGGL(k_swiglu_q8, dim3((n_total + 255) / 256), dim3(256), 0, st, g, u, n_total, q8out(out), h_out);
+  hipLaunchKernelGGL(k_swiglu_q8, dim3((n_total / 4 + 255) / 256), dim3(256), 0, st, g, u, n_total, q8out(out), h_out);
 }
 
 void launch_argmax_final(hipStream_t st, const float* pv, const uint32_t* pi, uint32_t nparts, uint32_t* tok_out,
