@@ -306,13 +306,19 @@ struct rlh_cache {
   uint32_t* host_st = nullptr;  // pinned staging for tok/pos
   rlh_dsampler* ds = nullptr;   // device sampler (rlh_sample_next), made on first use
   hipGraphExec_t g_logits = nullptr, g_nologits = nullptr, g_greedy = nullptr;
+  // kGreedyBatch greedy steps in one graph (each step reads the token and
+  // position its predecessor's argmax left on the device): one graph launch
+  // per kGreedyBatch tokens of rlh_generate_greedy
+  hipGraphExec_t g_greedy_n = nullptr;
   bool debug = false;
   bool use_graphs = true;  // RLH_GRAPHS=0 launches the same kernels eagerly
   int walk_shift = 0;      // RLH_SOFTMAX_WALK_SHIFT=1|2|3: a test knob of the decode softmax sum (AttnArgs::walk_shift)
   // prefill: the attn_k and attn_v products run on two more streams beside
   // attn_q's (their 1024-row grids fill a quarter of the GPU on their own);
-  // null when RLH_PREFILL_STREAMS=0 or their creation failed (one stream)
+  // side_ok false when RLH_PREFILL_STREAMS=0 or their creation failed (one
+  // stream then; what was created is released with the cache)
   hipStream_t side[2] = {nullptr, nullptr};
+  bool side_ok = false;
   hipEvent_t ev_fork = nullptr, ev_join[2] = {nullptr, nullptr};
   float* dbg = nullptr;  // [L][kDbgTokens][E]
   uint64_t dbg_tokens = 0;
@@ -505,10 +511,12 @@ void enqueue_step(rlh_cache* c, StepKind kind, int64_t dbg_slot) {
   }
 }
 
-int capture(rlh_cache* c, StepKind kind, hipGraphExec_t* out) {
+constexpr uint64_t kGreedyBatch = 8;
+
+int capture(rlh_cache* c, StepKind kind, hipGraphExec_t* out, uint64_t steps = 1) {
   hipGraph_t g = nullptr;
   HIPCHK(hipStreamBeginCapture(c->st, hipStreamCaptureModeThreadLocal));
-  enqueue_step(c, kind, -1);
+  for (uint64_t i = 0; i < steps; i++) enqueue_step(c, kind, -1);
   HIPCHK(hipStreamEndCapture(c->st, &g));
   hipError_t e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
   (void)hipGraphDestroy(g);
@@ -790,6 +798,7 @@ static void cache_free(rlh_cache* c) {
   if (c->g_logits) (void)hipGraphExecDestroy(c->g_logits);
   if (c->g_nologits) (void)hipGraphExecDestroy(c->g_nologits);
   if (c->g_greedy) (void)hipGraphExecDestroy(c->g_greedy);
+  if (c->g_greedy_n) (void)hipGraphExecDestroy(c->g_greedy_n);
   void* ptrs[] = {c->kc, c->vc, c->scores, c->x, c->q, c->k, c->v, c->attn, c->g, c->u, c->logits, c->scratch,
                   c->act_e.qs, c->act_e.d, c->act_e.s, c->act_e.s16, c->act_q.qs, c->act_q.d, c->act_q.s,
                   c->act_q.s16, c->act_f.qs, c->act_f.d, c->act_f.s, c->act_f.s16, c->st_dev, c->hist, c->pv,
@@ -880,16 +889,15 @@ int rlh_cache_create(rlh_model* m, uint64_t max_ctx, rlh_cache** out) {
     for (int i = 0; i < 2 && sok; i++)
       sok = hipStreamCreate(&c->side[i]) == hipSuccess &&
             hipEventCreateWithFlags(&c->ev_join[i], hipEventDisableTiming) == hipSuccess;
-    if (!sok) {  // one stream then; what was created is released with the cache
-      c->side[0] = c->side[1] = nullptr;
-      (void)hipGetLastError();
-    }
+    c->side_ok = sok;
+    if (!sok) (void)hipGetLastError();
   }
   const char* wenv = std::getenv("RLH_SOFTMAX_WALK_SHIFT");
   if (wenv && wenv[0] >= '1' && wenv[0] <= '3' && wenv[1] == 0) c->walk_shift = wenv[0] - '0';
   if (c->use_graphs &&
       ((rc = capture(c, STEP_LOGITS, &c->g_logits)) || (rc = capture(c, STEP_NOLOGITS, &c->g_nologits)) ||
-       (rc = capture(c, STEP_GREEDY, &c->g_greedy)))) {
+       (rc = capture(c, STEP_GREEDY, &c->g_greedy)) ||
+       (rc = capture(c, STEP_GREEDY, &c->g_greedy_n, kGreedyBatch)))) {
     std::string msg = g_err;
     cache_free(c);
     return fail(rc, msg);
@@ -1033,7 +1041,7 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
     for (uint32_t l = 0; l < cfg.n_layer; l++) {
       Layer& L = m->layers[l];
       launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, xn);
-      if (c->side[0] && c->side[1]) {
+      if (c->side_ok) {
         // k and v beside q: the side streams start after the norm and the
         // main stream waits for both before the next kernel reads k and v
         // (nothing writes the norm's outputs before that join)
@@ -1189,7 +1197,10 @@ int rlh_generate_greedy(rlh_model* m, rlh_cache* c, uint32_t first, uint64_t n_s
   c->host_st[2] = 0;
   HIPCHK(hipMemcpyAsync(c->st_dev, c->host_st, 12, hipMemcpyHostToDevice, c->st));
   HIPCHK(hipMemcpyAsync(c->hist, c->host_st, 4, hipMemcpyHostToDevice, c->st));
-  for (uint64_t i = 0; i < n; i++)
+  uint64_t i = 0;
+  if (!c->debug && c->use_graphs && c->g_greedy_n)
+    for (; i + kGreedyBatch <= n; i += kGreedyBatch) HIPCHK(hipGraphLaunch(c->g_greedy_n, c->st));
+  for (; i < n; i++)
     if ((rc = run_step(c, STEP_GREEDY, (int64_t)i))) return rc;
   HIPCHK(hipMemcpyAsync(out_tokens, c->hist, (n + 1) * 4, hipMemcpyDeviceToHost, c->st));
   if ((rc = sync_checked(c))) return rc;
