@@ -21,6 +21,10 @@
 // k_attn_softmax: one block per (head, token): the row in LDS, max and exp
 // in parallel, the sequential sum in one lane, probabilities written back
 // over the scores.
+// k_attn_softmax_rows (prefill rows up to 4032 positions): 4, 8 or 16
+// consecutive tokens of a head per block, one wave per 1, 2 or 4 rows for the
+// parallel parts and the sequential sums of all rows side by side in the
+// lanes of one wave.
 // k_attn_pv_dec (decode): one block per (KV head, 32-wide slice of the head
 // dimension). V slices and probabilities stream through double-buffered LDS
 // chunks while one lane per (head, dimension) runs its ordered saxpy chain.
@@ -46,6 +50,8 @@ namespace {
 
 constexpr int kHd = 128;
 constexpr int kPosTile = 64;    // positions per scores block
+// k_attn_softmax_rows: row stride in floats (t_max rounded up to 64, plus 4)
+__host__ __device__ constexpr uint32_t softmax_rows_stride(uint32_t t_max) { return ((t_max + 63) & ~63u) + 4; }
 constexpr int kKStride = 132;   // floats per staged K row (permuted + 4 pad)
 constexpr int kQkComb = 16;     // (token, head) combinations per scores block
 constexpr int kDecChunk = 256;  // positions per LDS chunk, decode PV
@@ -510,6 +516,108 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   for (uint32_t j = tid; j < t; j += 256) {
     const float v = e[j];
     row[j] = on ? v * inv : v;
+  }
+}
+
+// grid: (H, ceil(n_tok / (4 RW))); block 256; dynamic LDS: 4 RW rows of
+// softmax_rows_stride(t_max) floats. The prefill softmax of 4 RW consecutive
+// tokens of one head, with k_attn_softmax<false>'s arithmetic: wave w loads
+// rows w RW .. w RW + RW - 1 (max, exponentials) and scales them; the
+// sequential sums of all rows run side by side in the first 4 RW lanes of
+// wave 0, one dependent add per term for all rows at once. Every row is
+// padded with +0 terms to T, the block's longest row rounded up to 4: the
+// sum starts at +0 and its terms are never negative, so a +0 term leaves it
+// unchanged. The row stride is 4 words above a multiple of 64, so the
+// lanes' 16-byte reads fall in distinct banks. A row past the last token has
+// t = 0: no loads, no stores, and every wave reaches the block's barriers.
+template <int RW>
+__global__ void __launch_bounds__(256) k_attn_softmax_rows(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds_generic[];
+  __shared__ uint64_t tab_g[32];
+  __shared__ float s_inv[4 * RW];
+  __shared__ int s_on[4 * RW];
+  lu64* tab = (lu64*)tab_g;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t S = softmax_rows_stride(a.t_max), p0 = a.pos0[0], y0 = blockIdx.y * (4 * RW);
+  const uint32_t T = (p0 + min(y0 + 4 * RW, a.n_tok) + 3) & ~3u;
+  constexpr int KL = 16 / RW;  // loads per lane and row in flight together
+  uint32_t t[RW];
+  float mx[RW];
+  const float* rows[RW];
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+    const uint32_t y = y0 + wave * RW + i;
+    t[i] = y < a.n_tok ? p0 + y + 1 : 0;
+    rows[i] = a.scores + ((size_t)min(y, a.n_tok - 1) * a.H + blockIdx.x) * a.t_stride;
+    mx[i] = -__int_as_float(0x7f800000);
+  }
+  // the wave's longest row is its last valid one; a -inf stand-in past a
+  // row's end leaves its max unchanged (fmaxf never returns NaN from a
+  // non-NaN max, so the max is never NaN)
+  const uint32_t tw = t[0] ? p0 + min(y0 + wave * RW + RW, a.n_tok) : 0;
+  for (uint32_t b = 0; b < tw; b += 64 * KL) {
+    float v[RW][KL];
+#pragma unroll
+    for (int i = 0; i < RW; i++)
+#pragma unroll
+      for (int k = 0; k < KL; k++) {
+        const uint32_t j = b + lane + 64 * k;
+        v[i][k] = j < t[i] ? ld_gf(rows[i] + j) : -__int_as_float(0x7f800000);
+      }
+#pragma unroll
+    for (int i = 0; i < RW; i++) {
+      lfloat* e = (lfloat*)lds_generic + (wave * RW + i) * S;
+#pragma unroll
+      for (int k = 0; k < KL; k++) {
+        const uint32_t j = b + lane + 64 * k;
+        if (j < t[i]) e[j] = v[i][k];
+        mx[i] = fmaxf(mx[i], v[i][k]);
+      }
+    }
+  }
+  exp_tab_to_lds(tab);
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx[i] = fmaxf(mx[i], __shfl_xor(mx[i], m));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+    lfloat* e = (lfloat*)lds_generic + (wave * RW + i) * S;
+    float m = mx[i];
+    if (t[i]) {  // a NaN first score gives NaN (the reference's max loop)
+      const float x0 = e[0];
+      if (x0 != x0) m = x0;
+    }
+    // four terms per lane (16-byte LDS accesses); the words past t hold
+    // nothing loaded, and their exponentials are replaced by +0
+    for (uint32_t j = 4 * lane; j < T; j += 256) {
+      const f32x4_t x = *(const lf32x4*)(e + j);
+      const float y0 = expf_glibc_t(x.x - m, tab), y1 = expf_glibc_t(x.y - m, tab);
+      const float y2 = expf_glibc_t(x.z - m, tab), y3 = expf_glibc_t(x.w - m, tab);
+      *(lf32x4*)(e + j) = f32x4_t{j < t[i] ? y0 : 0.0f, j + 1 < t[i] ? y1 : 0.0f, j + 2 < t[i] ? y2 : 0.0f,
+                                  j + 3 < t[i] ? y3 : 0.0f};
+    }
+  }
+  __syncthreads();
+  if (tid < 4 * RW) {  // the sequential sums of softmax_inplace (ops.rs:408-412)
+    const float sum = seq_sum_lds((lfloat*)lds_generic + tid * S, T);
+    s_on[tid] = sum > 0.0f;
+    s_inv[tid] = 1.0f / sum;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < RW; i++) {
+    const uint32_t r = wave * RW + i;
+    const lfloat* e = (const lfloat*)lds_generic + r * S;
+    float* row = (float*)rows[i];
+    const bool on = s_on[r];
+    const float inv = s_inv[r];
+    for (uint32_t j = lane; j < t[i]; j += 64) {
+      const float v = e[j];
+      row[j] = on ? v * inv : v;
+    }
   }
 }
 
@@ -1179,6 +1287,12 @@ __global__ void __launch_bounds__(512) k_attn_pv_pre(AttnArgs a) {
 
 size_t softmax_lds(uint32_t t_max) { return (size_t)((t_max + 3) & ~3u) * 4; }
 
+// k_attn_softmax_rows: at most this much LDS per block (16 rows of up to 960
+// positions, 8 up to 1984, 4 up to 4032); longer rows take
+// k_attn_softmax<false>.
+constexpr size_t kSoftmaxRowsLds = 65536;
+size_t softmax_rows_lds(uint32_t t_max, int rw) { return (size_t)4 * rw * softmax_rows_stride(t_max) * 4; }
+
 }  // namespace
 
 void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
@@ -1194,6 +1308,15 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
   if (a.n_tok == 1)
     hipLaunchKernelGGL(k_attn_softmax<true>, dim3(a.H, 1), dim3(256), softmax_lds(a.t_max), st, a);
+  else if (softmax_rows_lds(a.t_max, 4) <= kSoftmaxRowsLds)
+    hipLaunchKernelGGL(k_attn_softmax_rows<4>, dim3(a.H, (a.n_tok + 15) / 16), dim3(256),
+                       softmax_rows_lds(a.t_max, 4), st, a);
+  else if (softmax_rows_lds(a.t_max, 2) <= kSoftmaxRowsLds)
+    hipLaunchKernelGGL(k_attn_softmax_rows<2>, dim3(a.H, (a.n_tok + 7) / 8), dim3(256), softmax_rows_lds(a.t_max, 2),
+                       st, a);
+  else if (softmax_rows_lds(a.t_max, 1) <= kSoftmaxRowsLds)
+    hipLaunchKernelGGL(k_attn_softmax_rows<1>, dim3(a.H, (a.n_tok + 3) / 4), dim3(256), softmax_rows_lds(a.t_max, 1),
+                       st, a);
   else
     hipLaunchKernelGGL(k_attn_softmax<false>, dim3(a.H, a.n_tok), dim3(256), softmax_lds(a.t_max), st, a);
 }
@@ -1248,6 +1371,12 @@ bool attn_init(uint32_t max_ctx) {
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_softmax<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_softmax_rows<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kSoftmaxRowsLds) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_softmax_rows<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kSoftmaxRowsLds) == hipSuccess &&
+         hipFuncSetAttribute((const void*)k_attn_softmax_rows<4>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kSoftmaxRowsLds) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_smpv_dec, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)kDecFusedLds) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_dec_v, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -21,6 +21,13 @@
 #ifndef RLH_EXPF_QUAL
 #error "define RLH_EXPF_QUAL before including expf_glibc.h"
 #endif
+// RLH_EXPF_KEEP(v): an optional barrier the includer may define that makes
+// the compiler compute v where it stands, for every input (in GPU code an
+// empty asm that reads and writes v's register; the compiler would
+// otherwise move the main path into a branch around the special cases).
+#ifndef RLH_EXPF_KEEP
+#define RLH_EXPF_KEEP(v) ((void)0)
+#endif
 
 // T[i] = bits(2^(i/32)) - (i << 47), i = 0..31 (as an initializer list).
 #define RLH_EXP2_TABLE_INIT                                                                                   \
@@ -41,16 +48,14 @@
 #define RLH_EXPF_C1 (0x1.ebfce50fac4f3p-3 / 32.0 / 32.0)
 #define RLH_EXPF_C2 (0x1.62e42ff0c52d6p-1 / 32.0)
 
+// The main path runs for every x and the special cases replace its value
+// after it by selects (no branch: in a GPU loop the branches cost more than
+// the arithmetic). For NaN, infinite or huge x the main path's value is
+// discarded; its integer arithmetic wraps and its table index stays in 0..31.
 template <class Tab>
 RLH_EXPF_QUAL float expf_glibc_t(float x, Tab tab) {
   const uint32_t ux = __builtin_bit_cast(uint32_t, x);
   const uint32_t abstop = (ux >> 20) & 0x7ff;
-  if (abstop >= 0x42b) {                                   // |x| >= 88 or NaN
-    if (ux == 0xff800000u) return 0.0f;                    // -inf
-    if (abstop >= 0x7f8) return x + x;                     // +inf or NaN
-    if (x > 0x1.62e42ep6f) return __builtin_bit_cast(float, 0x7f800000u);  // overflow
-    if (x < -0x1.9fe368p6f) return 0.0f;                   // underflow
-  }
   const double xd = (double)x;
   double kd = __builtin_fma(RLH_EXPF_INV_LN2_N, xd, RLH_EXPF_SHIFT);
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
@@ -63,5 +68,15 @@ RLH_EXPF_QUAL float expf_glibc_t(float x, Tab tab) {
   double y = __builtin_fma(RLH_EXPF_C2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y = y * s;
-  return (float)y;
+  // |x| >= 88 or NaN (below 88 none of these conditions holds): underflow
+  // below -0x1.9fe368p6 (and -inf) gives 0, overflow above 0x1.62e42ep6
+  // +inf, +inf and NaN x + x; one select each, on the bit patterns (so that
+  // NaN results keep x + x's payload)
+  uint32_t rb = __builtin_bit_cast(uint32_t, (float)y), nb = __builtin_bit_cast(uint32_t, x + x);
+  RLH_EXPF_KEEP(rb);
+  RLH_EXPF_KEEP(nb);
+  rb = x < -0x1.9fe368p6f ? 0u : rb;
+  rb = x > 0x1.62e42ep6f ? 0x7f800000u : rb;
+  rb = (abstop >= 0x7f8) & (ux != 0xff800000u) ? nb : rb;
+  return __builtin_bit_cast(float, rb);
 }

@@ -32,6 +32,7 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h16) {
 // over every float (tests/test_host_expf.py).
 // ---------------------------------------------------------------------------
 #define RLH_EXPF_QUAL __device__ __forceinline__
+#define RLH_EXPF_KEEP(v) __asm__ volatile("" : "+v"(v))
 #include "expf_glibc.h"
 
 __device__ __constant__ static const uint64_t kExp2Tab[32] = RLH_EXP2_TABLE_INIT;

@@ -298,6 +298,26 @@ def test_long_prefill_chunks_and_continuation():
     oc.close()
 
 
+def test_prefill_softmax_row_kernels():
+    """Prefill rows up to 4096 positions take the softmax kernel with one wave
+    per row (four rows per block), longer rows the kernel with one block per
+    row: a 4300-token prompt in 512-token chunks uses the first for the chunks
+    that end at or below position 4096 and the second for the last chunk.
+    Logits and the last layer's K/V rows bit-exact against the oracle."""
+    spec, tensors, m, om = _get("tiny-g4-q4km")
+    prompt = rlh.synth_tokens(77, 4300, spec.vocab)
+    c = m.new_cache(4400)
+    oc = om.new_cache(4400)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg), bits(rg)), f"logits differ (rel {rel_l2(lg, rg):.2e})"
+    for which in (0, 1):
+        l = spec.n_layer - 1
+        assert np.array_equal(bits(c.read_kv(l, which, 4300)), bits(oc.read_kv(l, which, 4300)))
+    c.close()
+    oc.close()
+
+
 def test_nan_logits_argmax_semantics():
     """NaN logits: every 8th row of the untied output matrix has a NaN Q6_K
     scale, so every logits block starts with a NaN row and logits[0] is NaN.
