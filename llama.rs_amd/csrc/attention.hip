@@ -280,7 +280,9 @@ __device__ __forceinline__ void qk_step(float (&acc)[32], const float (&qm)[8], 
 
 __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
+  __shared__ __attribute__((aligned(16))) float qv_g[kPreQkComb * kHd];
   lfloat* kt = (lfloat*)kt_g;
+  lfloat* qv = (lfloat*)qv_g;
   const uint32_t G = (uint32_t)(a.H / a.KVH), TP = (uint32_t)kPreQkComb / G;
   const uint32_t ntiles = (a.t_max + kPosTile - 1) / kPosTile;
   const uint32_t g = blockIdx.x / ntiles, tile = blockIdx.x % ntiles;
@@ -302,21 +304,39 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
   // the wave's first q is loaded with the K tile
   const uint32_t tt0 = j0 > pos_first ? j0 - pos_first : 0u;
   const uint32_t ncomb = ntok * G;
-  auto q_load = [&](float (&qm)[8], uint32_t c) {
-    const uint32_t cc = min(c, ncomb - 1), tt = cc / G, h = g * G + cc % G;
-    const float* qs = a.q + (size_t)(tok0 + tt) * qd + h * kHd + (lane & 15);
+  // the block's q vectors are staged in LDS with the K tile, element
+  // 16 m + r of a combination at r * 8 + m, so that lane r of every row of
+  // 16 lanes reads its eight elements in two 16-byte reads
+  float4 qr[8];
 #pragma unroll
-    for (int m = 0; m < 8; m++) qm[m] = ld_gf(qs + 16 * m);
-  };
-  float qa[8], qb[8];
-  uint32_t c = tt0 * G + wave;
-  q_load(qa, c);
+  for (int i = 0; i < 8; i++) {
+    const uint32_t ci = tid + 256u * i, cb = min(ci >> 5, ncomb - 1), f4 = ci & 31;
+    qr[i] = ld_gf4(a.q + (size_t)(tok0 + cb / G) * qd + (g * G + cb % G) * kHd + 4 * f4);
+  }
 #pragma unroll
   for (int i = 0; i < 8; i++) {
     const uint32_t ci = tid + 256u * i, jl = ci >> 5, f4 = ci & 31;
     *(lf32x4*)(kt + jl * kKStride + 4 * f4) = f32x4_t{kr[i].x, kr[i].y, kr[i].z, kr[i].w};
   }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const uint32_t ci = tid + 256u * i, cb = ci >> 5, f4 = ci & 31;
+    lfloat* qd0 = qv + cb * kHd + 4 * (f4 & 3) * 8 + (f4 >> 2);
+    qd0[0] = qr[i].x;
+    qd0[8] = qr[i].y;
+    qd0[16] = qr[i].z;
+    qd0[24] = qr[i].w;
+  }
+  auto q_load = [&](float (&qm)[8], uint32_t c) {
+    const lf32x4* qp = (const lf32x4*)(qv + min(c, ncomb - 1) * kHd + (lane & 15) * 8);
+    const f32x4_t u0 = qp[0], u1 = qp[1];
+    qm[0] = u0.x, qm[1] = u0.y, qm[2] = u0.z, qm[3] = u0.w;
+    qm[4] = u1.x, qm[5] = u1.y, qm[6] = u1.z, qm[7] = u1.w;
+  };
+  float qa[8], qb[8];
+  uint32_t c = tt0 * G + wave;
   __syncthreads();
+  q_load(qa, c);
   const uint32_t j = j0 + lane;
   f32x4_t kreg[32];
 #pragma unroll
@@ -1242,19 +1262,22 @@ __global__ void __launch_bounds__(512) k_attn_pv_pre(AttnArgs a) {
     if (more) load(j0 + kPreChunk);
     // positions below t_lo are taken by every chain
     const uint32_t jf = t_lo > j0 ? (t_lo - j0 < jn ? t_lo - j0 : jn) : 0u;
+    // every chain runs here, branch-free, with all its p reads issued before
+    // the arithmetic (a chain past the last token reads rows of ps that hold
+    // nothing and is never stored)
     uint32_t jj = 0;
     for (; jj + 4 <= jf; jj += 4) {
       const float v0 = vs[jj * kHd + d], v1 = vs[(jj + 1) * kHd + d];
       const float v2 = vs[(jj + 2) * kHd + d], v3 = vs[(jj + 3) * kHd + d];
+      f32x4_t p[NC];
+#pragma unroll
+      for (int i = 0; i < NC; i++) p[i] = *(const lf32x4*)(ps + (qtr + 4 * i) * CS + jj);
 #pragma unroll
       for (int i = 0; i < NC; i++) {
-        if (tlim[i]) {
-          const f32x4_t p = *(const lf32x4*)(ps + (qtr + 4 * i) * CS + jj);
-          o[i] = p.x * v0 + o[i];
-          o[i] = p.y * v1 + o[i];
-          o[i] = p.z * v2 + o[i];
-          o[i] = p.w * v3 + o[i];
-        }
+        o[i] = p[i].x * v0 + o[i];
+        o[i] = p[i].y * v1 + o[i];
+        o[i] = p[i].z * v2 + o[i];
+        o[i] = p[i].w * v3 + o[i];
       }
     }
     for (; jj < jn; jj++) {
