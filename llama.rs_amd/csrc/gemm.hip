@@ -541,8 +541,12 @@ __device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf, bool
   }
 }
 
+// Q4_K fits 166 VGPRs when asked for three waves per SIMD (no scratch), so a
+// CU holds three of its blocks (3 x 51 KB of LDS); the other types keep the
+// allocator's choice.
 template <uint32_t TY>
-__global__ void __launch_bounds__(256) k_gemm(GemmArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TY == RLH_TYPE_Q4_K ? 3 : 1)))
+k_gemm(GemmArgs a) {
   using G = GT<TY>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_generic[];
   lbyte* lds = (lbyte*)lds_generic;
