@@ -1041,28 +1041,38 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
     for (uint32_t l = 0; l < cfg.n_layer; l++) {
       Layer& L = m->layers[l];
       launch_rmsnorm_q8(st, c->xb, L.attn_norm.p, E, mtok, eps, c->act_eb, xn);
+      // Without a v bias the v product writes the chunk's V cache rows
+      // itself ([position][KVH * hd], the product's own [token][rows]
+      // layout from row p0), and nothing reads them before the PV kernel.
+      const bool v_direct = L.bv.p == nullptr;
+      float* vdst = v_direct ? layer_v(c, l) + (size_t)p0 * KVH * hd : c->vb;
+      bool v_pending = false;  // the main stream has yet to wait for the v stream
       if (c->side_ok) {
-        // k and v beside q: the side streams start after the norm and the
-        // main stream waits for both before the next kernel reads k and v
-        // (nothing writes the norm's outputs before that join)
+        // k and v beside q: the side streams start after the norm; the main
+        // stream waits for k before the next kernel reads it, and for v
+        // there too when v goes through vb, else just before the PV kernel
+        // (nothing writes the norm's outputs before either join)
         HIPCHK(hipEventRecord(c->ev_fork, st));
         HIPCHK(hipStreamWaitEvent(c->side[0], c->ev_fork, 0));
         HIPCHK(hipStreamWaitEvent(c->side[1], c->ev_fork, 0));
+        product_on(c->side[1], L.v.dm, c->act_eb, xn, vdst, nullptr);
         product_on(c->side[0], L.k.dm, c->act_eb, xn, c->kb, nullptr);
-        product_on(c->side[1], L.v.dm, c->act_eb, xn, c->vb, nullptr);
         HIPCHK(hipEventRecord(c->ev_join[0], c->side[0]));
         HIPCHK(hipEventRecord(c->ev_join[1], c->side[1]));
         product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
         HIPCHK(hipStreamWaitEvent(st, c->ev_join[0], 0));
-        HIPCHK(hipStreamWaitEvent(st, c->ev_join[1], 0));
+        if (v_direct)
+          v_pending = true;
+        else
+          HIPCHK(hipStreamWaitEvent(st, c->ev_join[1], 0));
       } else {
         product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
         product(L.k.dm, c->act_eb, xn, c->kb, nullptr);
-        product(L.v.dm, c->act_eb, xn, c->vb, nullptr);
+        product(L.v.dm, c->act_eb, xn, vdst, nullptr);
       }
-      launch_qk_norm_rope_kv(st, c->qb, c->kb, c->vb, L.bq.p, L.bk.p, L.bv.p, cfg.has_qk_norm ? L.q_norm.p : nullptr,
-                             cfg.has_qk_norm ? L.k_norm.p : nullptr, m->rope_cs, pos, layer_k(c, l), layer_v(c, l),
-                             (int)H, (int)KVH, mtok, eps);
+      launch_qk_norm_rope_kv(st, c->qb, c->kb, v_direct ? nullptr : c->vb, L.bq.p, L.bk.p, L.bv.p,
+                             cfg.has_qk_norm ? L.q_norm.p : nullptr, cfg.has_qk_norm ? L.k_norm.p : nullptr,
+                             m->rope_cs, pos, layer_k(c, l), layer_v(c, l), (int)H, (int)KVH, mtok, eps);
       AttnArgs a{};
       a.q = c->qb;
       a.rope_cs = m->rope_cs;
@@ -1083,6 +1093,7 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       a.err = err_word(c);
       launch_attn_scores(st, a, false);
       launch_attn_softmax(st, a);
+      if (v_pending) HIPCHK(hipStreamWaitEvent(st, c->ev_join[1], 0));
       launch_attn_pv(st, a, false);
       product(L.o.dm, c->act_qb, c->attnb, nullptr, c->xb);
       launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, xn);

@@ -196,12 +196,14 @@ __global__ void __launch_bounds__(64) k_qk_norm_rope_kv(float* q, float* k, cons
       float* kd = kcache + (size_t)pos * kvd + h * hd;
       kd[i] = y0;
       kd[i + 64] = y1;
-      const float* vs = v + (size_t)t * kvd + h * hd;
-      float* vd = vcache + (size_t)pos * kvd + h * hd;
-      for (int j = lane; j < hd; j += 64) {
-        float x = vs[j];
-        if (bv) x = x + bv[h * hd + j];
-        vd[j] = x;
+      if (v) {  // null: the v product wrote its rows into the cache itself
+        const float* vs = v + (size_t)t * kvd + h * hd;
+        float* vd = vcache + (size_t)pos * kvd + h * hd;
+        for (int j = lane; j < hd; j += 64) {
+          float x = vs[j];
+          if (bv) x = x + bv[h * hd + j];
+          vd[j] = x;
+        }
       }
     }
   }
