@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
 // s+32, s+64, s+96, A_l = (slot l + slot l+8) + (slot l+16 + slot l+24),
 // then the AVX2 tree (simd.rs:328-377).
 // grid: (KVH * ntiles, ceil(n_tok / TP)), TP = kPreQkComb / G; block 256.
-constexpr int kPreQkComb = 64;
+constexpr int kPreQkComb = 64;  // a multiple of 8 (the q staging: 256 threads x float4)
 
 // acc[i] = fma(q_e, k_i, acc[i]) for the 8 elements e = 16m + R0 + i, whose
 // q_e is lane R0 + i of every row of 16 lanes in qm (v_fmac_f32 takes it by
@@ -307,9 +307,10 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
   // the block's q vectors are staged in LDS with the K tile, element
   // 16 m + r of a combination at r * 8 + m, so that lane r of every row of
   // 16 lanes reads its eight elements in two 16-byte reads
-  float4 qr[8];
+  constexpr int kQv = kPreQkComb / 8;  // float4s of q per thread (32 per combination)
+  float4 qr[kQv];
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < kQv; i++) {
     const uint32_t ci = tid + 256u * i, cb = min(ci >> 5, ncomb - 1), f4 = ci & 31;
     qr[i] = ld_gf4(a.q + (size_t)(tok0 + cb / G) * qd + (g * G + cb % G) * kHd + 4 * f4);
   }
@@ -319,8 +320,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
     *(lf32x4*)(kt + jl * kKStride + 4 * f4) = f32x4_t{kr[i].x, kr[i].y, kr[i].z, kr[i].w};
   }
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const uint32_t ci = tid + 256u * i, cb = ci >> 5, f4 = ci & 31;
+  for (int i = 0; i < kQv; i++) {
+    const uint32_t ci = tid + 256u * i, cb = ci >> 5, f4 = ci & 31;  // cb < kPreQkComb
     lfloat* qd0 = qv + cb * kHd + 4 * (f4 & 3) * 8 + (f4 >> 2);
     qd0[0] = qr[i].x;
     qd0[8] = qr[i].y;
