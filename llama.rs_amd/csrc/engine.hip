@@ -1055,8 +1055,8 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
         HIPCHK(hipEventRecord(c->ev_fork, st));
         HIPCHK(hipStreamWaitEvent(c->side[0], c->ev_fork, 0));
         HIPCHK(hipStreamWaitEvent(c->side[1], c->ev_fork, 0));
-        product_on(c->side[1], L.v.dm, c->act_eb, xn, vdst, nullptr);
         product_on(c->side[0], L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        product_on(c->side[1], L.v.dm, c->act_eb, xn, vdst, nullptr);
         HIPCHK(hipEventRecord(c->ev_join[0], c->side[0]));
         HIPCHK(hipEventRecord(c->ev_join[1], c->side[1]));
         product(L.q.dm, c->act_eb, xn, c->qb, nullptr);

@@ -149,18 +149,25 @@ __global__ void __launch_bounds__(256) k_dequant(DevMat w, float* out) {
 // Per head: (+bias), QK-norm (rmsnorm_head, ops.rs:365-390 -> simd.rs:282-326
 // in place), NeoX RoPE (ops.rs:426-446) from the host-built glibc cos/sin
 // table, and the K/V write at pos (model.rs:642-656, 466-506).
-// grid.x = H + KVH heads (q heads first), grid.y = tokens; block 64.
-// q/k/v are token-major [n][dim]; pos of token t is pos0[0] + t.
+// Four (head, token) items per block of 256 threads, one per wave (item
+// i = token * (H + KVH) + head, q heads first); every wave reaches the
+// block's barriers, a wave past the last item works on item 0 and stores
+// nothing. q/k/v are token-major [n][dim]; pos of token t is pos0[0] + t.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(64) k_qk_norm_rope_kv(float* q, float* k, const float* v, const float* bq,
-                                                       const float* bk, const float* bv, const float* qn,
-                                                       const float* kn, const float* rope_cs, const uint32_t* pos0,
-                                                       float* kcache, float* vcache, int H, int KVH, float eps) {
+__global__ void __launch_bounds__(256) k_qk_norm_rope_kv(float* q, float* k, const float* v, const float* bq,
+                                                        const float* bk, const float* bv, const float* qn,
+                                                        const float* kn, const float* rope_cs, const uint32_t* pos0,
+                                                        float* kcache, float* vcache, int H, int KVH, float eps,
+                                                        uint32_t n_items) {
   constexpr int hd = 128;
-  __shared__ float hbuf[hd];
-  int head = blockIdx.x;
-  int t = blockIdx.y;
-  int lane = threadIdx.x;
+  __shared__ float hbuf_w[4][hd];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t item = blockIdx.x * 4 + wave;
+  const bool live = item < n_items;
+  const uint32_t it = live ? item : 0u;
+  float* hbuf = hbuf_w[wave];
+  int head = (int)(it % (uint32_t)(H + KVH));
+  int t = (int)(it / (uint32_t)(H + KVH));
   uint32_t pos = pos0[0] + (uint32_t)t;
   const int qd = H * hd, kvd = KVH * hd;
   bool is_q = head < H;
@@ -168,28 +175,33 @@ __global__ void __launch_bounds__(64) k_qk_norm_rope_kv(float* q, float* k, cons
   float* src = is_q ? q + (size_t)t * qd + h * hd : k + (size_t)t * kvd + h * hd;
   const float* bias = is_q ? bq : bk;
   const float* nw = is_q ? qn : kn;
-  for (int i = lane; i < hd; i += 64) {
-    float x = src[i];
-    if (bias) x = x + bias[h * hd + i];
-    hbuf[i] = x;
-  }
+  // every global read of the lane first (elements lane and lane + 64: the
+  // row, its bias and norm weights, the RoPE pair's cos and sin), so that
+  // they are in flight together
+  const float x0r = src[lane], x1r = src[lane + 64];
+  const float b0 = bias ? bias[h * hd + lane] : 0.0f, b1 = bias ? bias[h * hd + lane + 64] : 0.0f;
+  const float w0 = nw ? nw[lane] : 0.0f, w1 = nw ? nw[lane + 64] : 0.0f;
+  const float c = rope_cs[(size_t)pos * hd + 2 * lane];
+  const float sn = rope_cs[(size_t)pos * hd + 2 * lane + 1];
+  hbuf[lane] = bias ? x0r + b0 : x0r;
+  hbuf[lane + 64] = bias ? x1r + b1 : x1r;
   __syncthreads();
   if (nw) {
     float ss = rms_sumsq_wave(hbuf, hd);
     float s = 1.0f / sqrtf(ss / (float)hd + eps);
     __syncthreads();
-    for (int i = lane; i < hd; i += 64) hbuf[i] = hbuf[i] * s * nw[i];
+    hbuf[lane] = hbuf[lane] * s * w0;
+    hbuf[lane + 64] = hbuf[lane + 64] * s * w1;
     __syncthreads();
   }
   // RoPE pairs (i, i+64): lane i < 64 handles pair i.
   {
     int i = lane;
-    float c = rope_cs[(size_t)pos * hd + 2 * i];
-    float sn = rope_cs[(size_t)pos * hd + 2 * i + 1];
     float x0 = hbuf[i], x1 = hbuf[i + 64];
     float y0 = x0 * c - x1 * sn;
     float y1 = x0 * sn + x1 * c;
-    if (is_q) {
+    if (!live) {
+    } else if (is_q) {
       src[i] = y0;
       src[i + 64] = y1;
     } else {
@@ -366,8 +378,9 @@ void launch_qk_norm_rope_kv(hipStream_t st, float* q, float* k, const float* v, 
                             const float* bv, const float* qn, const float* kn, const float* rope_cs,
                             const uint32_t* pos0, float* kcache, float* vcache, int H, int KVH, uint32_t n_tok,
                             float eps) {
-  hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(H + KVH, n_tok), dim3(64), 0, st, q, k, v, bq, bk, bv, qn, kn, rope_cs,
-                     pos0, kcache, vcache, H, KVH, eps);
+  const uint32_t n_items = (uint32_t)(H + KVH) * n_tok;
+  hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3((n_items + 3) / 4), dim3(256), 0, st, q, k, v, bq, bk, bv, qn, kn,
+                     rope_cs, pos0, kcache, vcache, H, KVH, eps, n_items);
 }
 
 void launch_swiglu_q8(hipStream_t st, const float* g, const float* u, uint32_t n_total, const Q8Buf& out,
