@@ -501,11 +501,23 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   float* row = a.scores + ((size_t)blockIdx.y * a.H + blockIdx.x) * a.t_stride;
   // max: the reference keeps x[0] and takes every later v > max, so a NaN
   // first score gives NaN and later NaNs are skipped, as fmaxf does
+  // the row in batches of eight loads per thread in flight together (a
+  // load per iteration would make each LDS store wait for its own load in
+  // turn); a -inf stand-in past t leaves the max unchanged
   float mx = -__int_as_float(0x7f800000);
-  for (uint32_t j = tid; j < t; j += 256) {
-    const float s = ld_gf(row + j);
-    e[j] = s;
-    mx = fmaxf(mx, s);
+  for (uint32_t b = 0; b < t; b += 256 * 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t j = b + tid + 256 * k;
+      v[k] = j < t ? ld_gf(row + j) : -__int_as_float(0x7f800000);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t j = b + tid + 256 * k;
+      if (j < t) e[j] = v[k];
+      mx = fmaxf(mx, v[k]);
+    }
   }
   exp_tab_to_lds(tab);  // after the row loads: its store waits for its load
 #pragma unroll
@@ -515,7 +527,17 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float x0 = e[0];
   if (x0 != x0) mx = x0;
-  for (uint32_t j = tid; j < t; j += 256) e[j] = expf_glibc_t(e[j] - mx, tab);
+  // four terms per thread and step (16-byte LDS accesses: the row and its
+  // LDS stride are 16-byte aligned and cover t rounded up to 4); words past
+  // t keep their contents
+  const uint32_t nq = (t + 3) / 4;
+  for (uint32_t q = tid; q < nq; q += 256) {
+    const uint32_t j = 4 * q;
+    const f32x4_t x = *(const lf32x4*)(e + j);
+    const float y0 = expf_glibc_t(x.x - mx, tab), y1 = expf_glibc_t(x.y - mx, tab);
+    const float y2 = expf_glibc_t(x.z - mx, tab), y3 = expf_glibc_t(x.w - mx, tab);
+    *(lf32x4*)(e + j) = f32x4_t{y0, j + 1 < t ? y1 : x.y, j + 2 < t ? y2 : x.z, j + 3 < t ? y3 : x.w};
+  }
   __syncthreads();
   bool on;
   float inv;
@@ -534,9 +556,13 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
     on = s_on;
     inv = s_inv;
   }
-  for (uint32_t j = tid; j < t; j += 256) {
-    const float v = e[j];
-    row[j] = on ? v * inv : v;
+  for (uint32_t q = tid; q < nq; q += 256) {
+    const uint32_t j = 4 * q;
+    const f32x4_t v = *(const lf32x4*)(e + j);
+    row[j] = on ? v.x * inv : v.x;
+    if (j + 1 < t) row[j + 1] = on ? v.y * inv : v.y;
+    if (j + 2 < t) row[j + 2] = on ? v.z * inv : v.z;
+    if (j + 3 < t) row[j + 3] = on ? v.w * inv : v.w;
   }
 }
 
