@@ -1193,13 +1193,19 @@ bool mv_plan_finish(MvPlan& p) {
   // terms do not fit the LDS at all (the f32-product types past ~12288
   // values: the f32 row alone takes 1 KB per 256 values) take the ring plan
   // with the most producers that fit.
+  // Launches whose input is a finished Q8 row (no norm or quantize
+  // prologue: ffn_down after the SwiGLU kernel) take a ring plan too when
+  // all its blocks are resident: the chain wave then adds each round as it
+  // completes instead of after the other waves' first tiles (8B decode
+  // 433.1 -> 434.6, 4B 503.4 -> 506.8, 0.6B 995.3 -> 997.9 tok/s); with a
+  // quantize prologue (attn_output) the ring measured slower.
   uint32_t ring_np = 0;
   const uint32_t tj = tiled_any ? p.L.seg[0].w.tj : 1u;
   if (tiled_any && !fl && nm == 1 && !p.norm && R == tr && ntj >= 2) {
     const char* env = std::getenv("RLH_MV_RING");
     const bool force = (env && env[0] == '1') || !whole_fits;
     const uint32_t b = plan_blocks(p, R), s = force ? 0u : mv_resident_blocks(p, R, tr, ntj);
-    if (force || (s && b > s))
+    if (force || (s && b > s) || !p.quant)
       for (uint32_t np = std::min<uint32_t>(7, ntj); np >= 2 && !ring_np; np--)  // np + 1 <= 8 waves (launch bound)
         if (ring_lds(p, R, np, tj, 2) <= kMaxLds &&
             (force || mv_resident(p, 64 * (np + 1), ring_lds(p, R, np, tj, 2), true) >= b))
