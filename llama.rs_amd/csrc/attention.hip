@@ -18,6 +18,9 @@
 // k_attn_qk_pre (prefill): one block per (KV head, 64-position tile, tile of
 // query tokens); lanes own positions as above, q reaches every lane by DPP
 // row broadcasts (below). Tiles above the causal diagonal exit at once.
+// k_attn_qk_pre_p (prefill, few blocks per CU): the same work items taken
+// by resident blocks in turn, the next item's K tile and q loaded while
+// the current one is computed.
 // k_attn_softmax: one block per (head, token): the row in LDS, max and exp
 // in parallel, the sequential sum in one lane, probabilities written back
 // over the scores.
@@ -36,6 +39,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "attention.h"
@@ -235,18 +239,20 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk(AttnArgs a) {
   }
 }
 
-// Prefill scores (q already normed and roped): one block per (KV head,
-// 64-position tile, tile of kPreQkComb / G query tokens). The K tile is
-// staged in LDS once and each lane (= position) keeps its K row in
-// registers. The wave walks its (token, head) combinations with q held in
-// every row of 16 lanes (lane r of a row holds elements 16m + r in qm[m])
-// and broadcast to the row by DPP (row_newbcast), so no q element passes
-// through LDS; the next combination's q is loaded while the current one is
-// computed. Slot s (0..31) of dot_f32_avx2 is the FMA chain over elements s,
-// s+32, s+64, s+96, A_l = (slot l + slot l+8) + (slot l+16 + slot l+24),
-// then the AVX2 tree (simd.rs:328-377).
-// grid: (KVH * ntiles, ceil(n_tok / TP)), TP = kPreQkComb / G; block 256.
-constexpr int kPreQkComb = 64;  // a multiple of 8 (the q staging: 256 threads x float4)
+// Prefill scores (q already normed and roped): k_attn_qk_pre (a block per
+// work item) or k_attn_qk_pre_p (persistent), below; a work item is (KV
+// head, 64-position tile, tile of combinations / G query tokens).
+constexpr int kPreQkComb = 64;  // k_attn_qk_pre: combinations per block (a multiple of 8)
+constexpr int kPreQkItem = 32;  // k_attn_qk_pre_p: combinations per work item (a multiple of 8)
+// k_attn_qk_pre_p runs when k_attn_qk_pre's blocks would fill at most this
+// many rounds of the resident blocks: it loads an item's K tile and q while
+// the previous item is computed, but each item waits for the previous one's
+// score stores to drain (one memory counter covers both), which costs more
+// than it saves once a block has many items (8B 512-token chunk, 2.25
+// rounds: 58 -> 43 us; 32B 4096-token chunks, 12-60 rounds: 468 -> 646 us)
+constexpr uint32_t kQkPersistRounds = 6;
+// blocks of k_attn_qk_pre_p the GPU holds at once (attn_init)
+uint32_t g_qk_pre_resident = 0;
 
 // acc[i] = fma(q_e, k_i, acc[i]) for the 8 elements e = 16m + R0 + i, whose
 // q_e is lane R0 + i of every row of 16 lanes in qm (v_fmac_f32 takes it by
@@ -278,6 +284,48 @@ __device__ __forceinline__ void qk_step(float (&acc)[32], const float (&qm)[8], 
   fmac8_bcast<8>(acc, 24, qm[2 * K + 1], kreg[8 * K + 6], kreg[8 * K + 7]);
 }
 
+// Work item of the persistent prefill scores kernel: KV head g, token tile y
+// (tokens y TP .. y TP + TP - 1) and a 64-position tile at or below the
+// tile's causal diagonal; per KV head the items run y-major. count(y) is
+// the number of position tiles token tile y sees.
+struct QkItem {
+  uint32_t g, tile, tok0, ntok;
+};
+__host__ __device__ inline uint32_t qk_tiles_seen(uint32_t p0, uint32_t n_tok, uint32_t TP, uint32_t y) {
+  const uint32_t last = p0 + (n_tok < (y + 1) * TP ? n_tok : (y + 1) * TP) - 1;
+  return last / kPosTile + 1;
+}
+__host__ __device__ inline uint32_t qk_items_per_head(uint32_t p0, uint32_t n_tok, uint32_t TP) {
+  uint32_t n = 0;
+  for (uint32_t y = 0; y * TP < n_tok; y++) n += qk_tiles_seen(p0, n_tok, TP, y);
+  return n;
+}
+__device__ inline QkItem qk_item(uint32_t it, uint32_t per_g, uint32_t p0, uint32_t n_tok, uint32_t TP) {
+  QkItem q;
+  q.g = it / per_g;
+  uint32_t r = it % per_g, y = 0;
+  for (;; y++) {  // r < per_g: some token tile holds it
+    const uint32_t c = qk_tiles_seen(p0, n_tok, TP, y);
+    if (r < c) break;
+    r -= c;
+  }
+  q.tile = r;
+  q.tok0 = y * TP;
+  q.ntok = n_tok - q.tok0 < TP ? n_tok - q.tok0 : TP;
+  return q;
+}
+
+// Prefill scores (q already normed and roped): one block per (KV head,
+// 64-position tile, tile of kPreQkComb / G query tokens). The K tile is
+// staged in LDS once and each lane (= position) keeps its K row in
+// registers. The wave walks its (token, head) combinations with q held in
+// every row of 16 lanes (lane r of a row holds elements 16m + r in qm[m])
+// and broadcast to the row by DPP (row_newbcast), so no q element passes
+// through LDS; the next combination's q is loaded while the current one is
+// computed. Slot s (0..31) of dot_f32_avx2 is the FMA chain over elements s,
+// s+32, s+64, s+96, A_l = (slot l + slot l+8) + (slot l+16 + slot l+24),
+// then the AVX2 tree (simd.rs:328-377).
+// grid: (KVH * ntiles, ceil(n_tok / TP)), TP = kPreQkComb / G; block 256.
 __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
   __shared__ __attribute__((aligned(16))) float qv_g[kPreQkComb * kHd];
@@ -364,6 +412,120 @@ __global__ void __launch_bounds__(256, 2) k_attn_qk_pre(AttnArgs a) {
     if (c + 4 >= ncomb) break;
     q_load(qa, c + 8);
     one(qb, c + 4);
+  }
+}
+
+// grid: the resident blocks (at most the items); block 256. Block b takes
+// items b, b + gridDim.x, ... (exits are uniform, no waits between blocks).
+// Per item the K tile is staged in LDS and each lane (= position) keeps its
+// K row in registers; the item's q vectors sit in one of two LDS buffers in
+// their natural element order, copied there by DMA. While an item is
+// computed, the next item's K tile is loaded into registers and its q
+// vectors are copied into the other buffer, so the loads' latency is paid
+// once per block instead of once per item; the combination loop issues no
+// global loads (nothing it waits for queues behind the next item's). Lane
+// r of every row of 16 lanes reads elements 16 m + r of q (conflict-free
+// 4-byte reads) into qm[m], which the FMAs take by DPP row broadcasts
+// (fmac8_bcast). Slot s (0..31) of dot_f32_avx2 is the FMA chain over
+// elements s, s+32, s+64, s+96, A_l = (slot l + slot l+8) + (slot l+16 +
+// slot l+24), then the AVX2 tree (simd.rs:328-377).
+__global__ void __launch_bounds__(256, 2) k_attn_qk_pre_p(AttnArgs a, uint32_t per_g) {
+  __shared__ __attribute__((aligned(16))) float kt_g[kPosTile * kKStride];
+  __shared__ __attribute__((aligned(16))) float qv_g[2][kPreQkItem * kHd];
+  lfloat* kt = (lfloat*)kt_g;
+  const uint32_t G = (uint32_t)(a.H / a.KVH), TP = (uint32_t)kPreQkItem / G;
+  const uint32_t p0h = a.t_max - a.n_tok;  // the chunk's first position (the host's view of pos0)
+  const uint32_t n_items = (uint32_t)a.KVH * per_g;
+  uint32_t it = blockIdx.x;
+  if (it >= n_items) return;  // whole block, before any barrier
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t qd = (uint32_t)a.H * kHd, kvd = (uint32_t)a.KVH * kHd;
+  const uint32_t p0 = a.pos0[0];
+  // an item's K tile rows in natural element order (rows past its last
+  // token's position repeat that row)
+  auto load_k = [&](float4 (&kr)[8], const QkItem& q) {
+    const uint32_t pos_last = p0 + q.tok0 + q.ntok - 1, j0 = q.tile * kPosTile;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t c = tid + 256u * i, jl = c >> 5, f4 = c & 31, j = min(j0 + jl, pos_last);
+      kr[i] = ld_gf4(a.kcache + (size_t)j * kvd + q.g * kHd + 4 * f4);
+    }
+  };
+  // an item's q vectors into buffer b by DMA: one 1 KB copy per wave and
+  // step holds two combinations (lanes 0..31 and 32..63, 16 bytes each);
+  // combinations past the last token repeat the last one
+  auto dma_q = [&](uint32_t b, const QkItem& q) {
+    const uint32_t ncomb = q.ntok * G;
+#pragma unroll
+    for (uint32_t k = 0; k < (uint32_t)kPreQkItem / 8; k++) {
+      const uint32_t pair = wave + 4 * k, cb = min(2 * pair + lane / 32, ncomb - 1);
+      __builtin_amdgcn_global_load_lds(
+          (const RLH_GLOBAL void*)(a.q + (size_t)(q.tok0 + cb / G) * qd + (q.g * G + cb % G) * kHd + 4 * (lane % 32)),
+          (RLH_LDS void*)((lfloat*)qv_g[b] + 2 * pair * kHd), 16, 0, 0);
+    }
+  };
+  QkItem cur = qk_item(it, per_g, p0h, a.n_tok, TP);
+  float4 kr[8];
+  load_k(kr, cur);
+  dma_q(0, cur);
+  for (uint32_t n = 0;; n++) {
+    wait_vmcnt<0>();  // this wave's K rows and q copies of the item have landed
+    __syncthreads();  // ... everyone's; every wave is done with the previous kt
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t ci = tid + 256u * i, jl = ci >> 5, f4 = ci & 31;
+      *(lf32x4*)(kt + jl * kKStride + 4 * f4) = f32x4_t{kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+    }
+    __syncthreads();
+    f32x4_t kreg[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) kreg[i] = *(const lf32x4*)(kt + lane * kKStride + 4 * i);
+    const lfloat* qv = (const lfloat*)qv_g[n & 1];
+    const uint32_t nit = it + gridDim.x;
+    const bool more = nit < n_items;
+    QkItem nxt = cur;
+    if (more) {  // uniform: the next item's K tile and q vectors in flight
+      nxt = qk_item(nit, per_g, p0h, a.n_tok, TP);
+      load_k(kr, nxt);
+      dma_q((n + 1) & 1, nxt);  // that buffer's last reader was the item before this one
+    }
+    const uint32_t j0 = cur.tile * kPosTile, pos_first = p0 + cur.tok0, ncomb = cur.ntok * G;
+    const uint32_t j = j0 + lane;
+    auto q_load = [&](float (&qm)[8], uint32_t c) {
+      const lfloat* qp = qv + min(c, ncomb - 1) * kHd + (lane & 15);
+#pragma unroll
+      for (int m = 0; m < 8; m++) qm[m] = qp[16 * m];
+    };
+    auto one = [&](const float (&qm)[8], uint32_t cc) {
+      const uint32_t tt = cc / G, h = cur.g * G + cc % G;
+      float acc[32];
+#pragma unroll
+      for (int s = 0; s < 32; s++) acc[s] = 0.0f;  // fma(q, k, +0) starts each chain, as the reference
+      qk_step<0>(acc, qm, kreg);
+      qk_step<1>(acc, qm, kreg);
+      qk_step<2>(acc, qm, kreg);
+      qk_step<3>(acc, qm, kreg);
+      float A[8];
+#pragma unroll
+      for (int l = 0; l < 8; l++) A[l] = (acc[l] + acc[l + 8]) + (acc[l + 16] + acc[l + 24]);
+      const float d = ((A[0] + A[4]) + (A[2] + A[6])) + ((A[1] + A[5]) + (A[3] + A[7]));
+      if (j <= pos_first + tt) a.scores[((size_t)(cur.tok0 + tt) * a.H + h) * a.t_stride + j] = d * a.scale;
+    };
+    // tokens before tt0 see no position of the tile
+    uint32_t c = (j0 > pos_first ? j0 - pos_first : 0u) * G + wave;
+    float qa[8], qb[8];
+    q_load(qa, c);
+#pragma unroll 1
+    for (; c < ncomb; c += 8) {
+      q_load(qb, c + 4);
+      one(qa, c);
+      if (c + 4 >= ncomb) break;
+      q_load(qa, c + 8);
+      one(qb, c + 4);
+    }
+    if (!more) break;
+    it = nit;
+    cur = nxt;
   }
 }
 
@@ -1350,8 +1512,17 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
   if (fused) {
     hipLaunchKernelGGL(k_attn_qk, dim3(a.KVH * ntiles, a.n_tok), dim3(256), 0, st, a);
   } else {
-    const uint32_t TP = (uint32_t)kPreQkComb / (uint32_t)(a.H / a.KVH);
-    hipLaunchKernelGGL(k_attn_qk_pre, dim3(a.KVH * ntiles, (a.n_tok + TP - 1) / TP), dim3(256), 0, st, a);
+    const uint32_t G = (uint32_t)(a.H / a.KVH), p0 = a.t_max - a.n_tok;
+    const uint32_t TP = (uint32_t)kPreQkComb / G, blocks = (uint32_t)a.KVH * qk_items_per_head(p0, a.n_tok, TP);
+    const char* env = std::getenv("RLH_QK_PRE_GRID");  // '1': always the grid kernel (tests)
+    const bool grid_only = env && env[0] == '1';
+    if (!grid_only && g_qk_pre_resident && blocks <= kQkPersistRounds * g_qk_pre_resident) {
+      const uint32_t per_g = qk_items_per_head(p0, a.n_tok, (uint32_t)kPreQkItem / G);
+      const uint32_t n_items = (uint32_t)a.KVH * per_g;
+      hipLaunchKernelGGL(k_attn_qk_pre_p, dim3(std::min(n_items, g_qk_pre_resident)), dim3(256), 0, st, a, per_g);
+    } else {
+      hipLaunchKernelGGL(k_attn_qk_pre, dim3(a.KVH * ntiles, (a.n_tok + TP - 1) / TP), dim3(256), 0, st, a);
+    }
   }
 }
 
@@ -1415,6 +1586,14 @@ void launch_attn_pv(hipStream_t st, const AttnArgs& a, bool decode) {
 
 bool attn_init(uint32_t max_ctx) {
   if (max_ctx > kAttnMaxCtx) return false;
+  if (!g_qk_pre_resident) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)k_attn_qk_pre_p, 256, 0) == hipSuccess &&
+        cus > 0 && per_cu > 0)
+      g_qk_pre_resident = (uint32_t)(cus * per_cu);
+  }
   size_t ring_lds = 0;
   for (uint32_t gq = 1; gq <= (uint32_t)kAttnMaxGroup; gq++) ring_lds = std::max(ring_lds, pv_ring_lds(gq));
   return hipFuncSetAttribute((const void*)k_attn_softmax<true>, hipFuncAttributeMaxDynamicSharedMemorySize,

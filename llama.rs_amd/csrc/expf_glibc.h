@@ -77,6 +77,6 @@ RLH_EXPF_QUAL float expf_glibc_t(float x, Tab tab) {
   RLH_EXPF_KEEP(nb);
   rb = x < -0x1.9fe368p6f ? 0u : rb;
   rb = x > 0x1.62e42ep6f ? 0x7f800000u : rb;
-  rb = (abstop >= 0x7f8) & (ux != 0xff800000u) ? nb : rb;
+  rb = ((abstop >= 0x7f8) & (ux != 0xff800000u)) ? nb : rb;
   return __builtin_bit_cast(float, rb);
 }

@@ -318,6 +318,38 @@ def test_prefill_softmax_row_kernels():
     oc.close()
 
 
+@pytest.mark.parametrize("grid_only", ["0", "1"])
+def test_prefill_scores_kernels(monkeypatch, grid_only):
+    """Prefill scores through the persistent kernel (few blocks per CU: every
+    shape here) and, with RLH_QK_PRE_GRID=1, through the kernel with a block
+    per work item: a 4300-token prompt (9 chunks of up to 512 tokens, 4
+    query heads per KV head) and a 600-token prompt continued by 30 tokens
+    at start_pos 600 on small-q4km, logits and the last layer's K/V rows
+    bit-exact against the oracle."""
+    monkeypatch.setenv("RLH_QK_PRE_GRID", grid_only)
+    spec, tensors, m, om = _get("tiny-g4-q4km")
+    prompt = rlh.synth_tokens(91, 4300, spec.vocab)
+    c = m.new_cache(4400)
+    oc = om.new_cache(4400)
+    lg = c.forward_into(prompt, 0)
+    rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
+    assert np.array_equal(bits(lg), bits(rg)), f"logits differ (rel {rel_l2(lg, rg):.2e})"
+    c.close()
+    oc.close()
+    spec, tensors, m, om = _get("small-q4km")
+    prompt = rlh.synth_tokens(92, 600, spec.vocab)
+    more = rlh.synth_tokens(93, 30, spec.vocab)
+    c = m.new_cache(700)
+    oc = om.new_cache(700)
+    assert np.array_equal(bits(c.forward_into(prompt, 0)), bits(oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)))
+    assert np.array_equal(bits(c.forward_into(more, 600)), bits(oc.forward_into(more, 600, oracle.MODE_BATCH_INT)))
+    l = spec.n_layer - 1
+    for which in (0, 1):
+        assert np.array_equal(bits(c.read_kv(l, which, 630)), bits(oc.read_kv(l, which, 630)))
+    c.close()
+    oc.close()
+
+
 def test_nan_logits_argmax_semantics():
     """NaN logits: every 8th row of the untied output matrix has a NaN Q6_K
     scale, so every logits block starts with a NaN row and logits[0] is NaN.
