@@ -1047,27 +1047,43 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       const bool v_direct = L.bv.p == nullptr;
       float* vdst = v_direct ? layer_v(c, l) + (size_t)p0 * KVH * hd : c->vb;
       bool v_pending = false;  // the main stream has yet to wait for the v stream
+      // q and k of one type and width: one launch of both (no stream join
+      // for k on the way to the next kernel)
+      const bool qk_pair = gemm_pair_supported(L.q.dm, L.k.dm);
+      auto q_and_k = [&](hipStream_t s) {
+        if (qk_pair) {
+          launch_gemm_pair(s, L.q.dm, L.k.dm, c->act_eb, mtok, c->qb, c->kb);
+        } else {
+          product_on(s, L.q.dm, c->act_eb, xn, c->qb, nullptr);
+          product_on(s, L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        }
+      };
       if (c->side_ok) {
-        // k and v beside q: the side streams start after the norm; the main
-        // stream waits for k before the next kernel reads it, and for v
-        // there too when v goes through vb, else just before the PV kernel
-        // (nothing writes the norm's outputs before either join)
+        // v (and k, when q and k cannot share a launch) beside q: the side
+        // streams start after the norm; the main stream waits for k before
+        // the next kernel reads it, and for v there too when v goes
+        // through vb, else just before the PV kernel (nothing writes the
+        // norm's outputs before either join)
         HIPCHK(hipEventRecord(c->ev_fork, st));
-        HIPCHK(hipStreamWaitEvent(c->side[0], c->ev_fork, 0));
         HIPCHK(hipStreamWaitEvent(c->side[1], c->ev_fork, 0));
-        product_on(c->side[0], L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        if (!qk_pair) {
+          HIPCHK(hipStreamWaitEvent(c->side[0], c->ev_fork, 0));
+          product_on(c->side[0], L.k.dm, c->act_eb, xn, c->kb, nullptr);
+          HIPCHK(hipEventRecord(c->ev_join[0], c->side[0]));
+        }
         product_on(c->side[1], L.v.dm, c->act_eb, xn, vdst, nullptr);
-        HIPCHK(hipEventRecord(c->ev_join[0], c->side[0]));
         HIPCHK(hipEventRecord(c->ev_join[1], c->side[1]));
-        product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
-        HIPCHK(hipStreamWaitEvent(st, c->ev_join[0], 0));
+        if (qk_pair)
+          q_and_k(st);
+        else
+          product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
+        if (!qk_pair) HIPCHK(hipStreamWaitEvent(st, c->ev_join[0], 0));
         if (v_direct)
           v_pending = true;
         else
           HIPCHK(hipStreamWaitEvent(st, c->ev_join[1], 0));
       } else {
-        product(L.q.dm, c->act_eb, xn, c->qb, nullptr);
-        product(L.k.dm, c->act_eb, xn, c->kb, nullptr);
+        q_and_k(st);
         product(L.v.dm, c->act_eb, xn, vdst, nullptr);
       }
       launch_qk_norm_rope_kv(st, c->qb, c->kb, v_direct ? nullptr : c->vb, L.bq.p, L.bk.p, L.bv.p,

@@ -546,14 +546,23 @@ __device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf, bool
 // allocator's choice.
 template <uint32_t TY>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(TY == RLH_TYPE_Q4_K ? 3 : 1)))
-k_gemm(GemmArgs a) {
+k_gemm(GemmArgs a0) {
   using G = GT<TY>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds_generic[];
   lbyte* lds = (lbyte*)lds_generic;
   // XCD-aware tile order (see file header)
   const uint32_t b = blockIdx.x, xcd = b & 7, k = b >> 3;
-  const uint32_t tt = k % a.n_tt, rt = (k / a.n_tt) * 8 + xcd;
-  if (rt >= a.n_rt) return;  // whole block, before any barrier
+  const uint32_t tt = k % a0.n_tt, rtg = (k / a0.n_tt) * 8 + xcd;
+  if (rtg >= a0.n_rt) return;  // whole block, before any barrier
+  // the block's segment (uniform: from the block index)
+  GemmArgs a = a0;
+  uint32_t rt = rtg;
+  if (rtg >= a0.n_rt1) {
+    a.w = a0.w2;
+    a.y = a0.y2;
+    a.resid = nullptr;
+    rt = rtg - a0.n_rt1;
+  }
   const uint32_t t0 = tt * kTile, r0 = rt * kTile;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   Lane ln{lane >> 4, lane & 15, wave & 1, wave >> 1};
@@ -866,6 +875,37 @@ void launch_gemm_f32(hipStream_t st, const DevMat& w, const float* x, uint32_t n
   }
 }
 
+static void launch_gemm_args(hipStream_t st, uint32_t ty, const GemmArgs& a) {
+  const uint32_t blocks = a.n_tt * ((a.n_rt + 7) / 8) * 8;
+  const size_t lds = 2 * kStageBytes;
+  switch (ty) {
+    case RLH_TYPE_Q4_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_K>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q6_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q6_K>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q8_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q8_0>, dim3(blocks), dim3(256), lds, st, a); break;
+    case RLH_TYPE_Q4_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_0>, dim3(blocks), dim3(256), lds, st, a); break;
+    default: break;
+  }
+}
+
+bool gemm_pair_supported(const DevMat& w, const DevMat& w2) {
+  return gemm_supported(w.ty) && w2.ty == w.ty && w2.cols == w.cols;
+}
+
+void launch_gemm_pair(hipStream_t st, const DevMat& w, const DevMat& w2, const Q8Mut& x, uint32_t n, float* y,
+                      float* y2) {
+  GemmArgs a{};
+  a.w = w;
+  a.w2 = w2;
+  a.x = Q8Ptr{x.qs, x.d, x.s, x.s16};
+  a.n = n;
+  a.y = y;
+  a.y2 = y2;
+  a.n_tt = (n + kTile - 1) / kTile;
+  a.n_rt1 = (w.rows + kTile - 1) / kTile;
+  a.n_rt = a.n_rt1 + (w2.rows + kTile - 1) / kTile;
+  launch_gemm_args(st, w.ty, a);
+}
+
 void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, float* y, float* resid) {
   GemmArgs a{};
   a.w = w;
@@ -875,15 +915,8 @@ void launch_gemm(hipStream_t st, const DevMat& w, const Q8Mut& x, uint32_t n, fl
   a.resid = resid;
   a.n_tt = (n + kTile - 1) / kTile;
   a.n_rt = (w.rows + kTile - 1) / kTile;
-  const uint32_t blocks = a.n_tt * ((a.n_rt + 7) / 8) * 8;
-  const size_t lds = 2 * kStageBytes;
-  switch (w.ty) {
-    case RLH_TYPE_Q4_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_K>, dim3(blocks), dim3(256), lds, st, a); break;
-    case RLH_TYPE_Q6_K: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q6_K>, dim3(blocks), dim3(256), lds, st, a); break;
-    case RLH_TYPE_Q8_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q8_0>, dim3(blocks), dim3(256), lds, st, a); break;
-    case RLH_TYPE_Q4_0: hipLaunchKernelGGL(k_gemm<RLH_TYPE_Q4_0>, dim3(blocks), dim3(256), lds, st, a); break;
-    default: break;
-  }
+  a.n_rt1 = a.n_rt;
+  launch_gemm_args(st, w.ty, a);
 }
 
 }  // namespace rlh
