@@ -1113,8 +1113,12 @@ static int forward_batch_impl(rlh_model* m, rlh_cache* c, const uint32_t* tokens
       launch_attn_pv(st, a, false);
       product(L.o.dm, c->act_qb, c->attnb, nullptr, c->xb);
       launch_rmsnorm_q8(st, c->xb, L.ffn_norm.p, E, mtok, eps, c->act_eb, xn);
-      product(L.gate.dm, c->act_eb, xn, c->gb, nullptr);
-      product(L.up.dm, c->act_eb, xn, c->ub, nullptr);
+      if (gemm_pair_supported(L.gate.dm, L.up.dm)) {  // one launch of both (one boundary less)
+        launch_gemm_pair(st, L.gate.dm, L.up.dm, c->act_eb, mtok, c->gb, c->ub);
+      } else {
+        product(L.gate.dm, c->act_eb, xn, c->gb, nullptr);
+        product(L.up.dm, c->act_eb, xn, c->ub, nullptr);
+      }
       // h over the gate rows in place when ffn_down takes the f32 route
       const bool hf = !gemm_supported(L.down.ty);
       launch_swiglu_q8(st, c->gb, c->ub, mtok * cfg.n_ff, c->act_fb, hf ? c->gb : nullptr);
