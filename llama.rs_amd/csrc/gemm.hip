@@ -487,6 +487,31 @@ __device__ __forceinline__ void stage_load(StageRegs& r, const GemmArgs& a, uint
   }
 }
 
+// Q6_K stages super-block j by DMA straight into `buf` (global_load_lds, 16
+// bytes per lane; no staging registers): the 64 tokens' Q8 bytes (1088
+// pieces of 16 bytes, token p / 17, piece p % 17; the pad piece repeats
+// piece 15 and tokens past n repeat the last one, neither is read for a
+// kept output) and the token-major block scales (128 slots of 16 bytes).
+// Every wave issues its copies; the caller waits for them (vmcnt) and then
+// the block barrier.
+__device__ __forceinline__ void stage_dma(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf) {
+  const uint32_t cols = a.w.cols, nb = cols / 32, lane = threadIdx.x & 63, w = wave_id();
+  auto q8_piece = [&](uint32_t p0) {  // pieces p0 .. p0 + 63, p0 a multiple of 64
+    const uint32_t p = p0 + lane, tok = p / 17, ch = p - tok * 17;
+    const int8_t* src = a.x.qs + (size_t)min(t0 + tok, a.n - 1) * cols + 256 * j + 16 * min(ch, 15u);
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)src, (RLH_LDS void*)(buf + p0 * 16), 16, 0, 0);
+  };
+#pragma unroll
+  for (uint32_t k = 0; k < 4; k++) q8_piece(64 * w + 256 * k);
+  if (w == 0) q8_piece(1024);
+  if (w == 1 || w == 2) {  // scale slots (token slot >> 1, blocks 4 (slot & 1) .. +3)
+    const uint32_t slot = 64 * (w - 1) + lane, tok = slot >> 1;
+    const float* src = a.x.d + (size_t)min(t0 + tok, a.n - 1) * nb + 8 * j + 4 * (slot & 1);
+    __builtin_amdgcn_global_load_lds((const RLH_GLOBAL void*)src,
+                                     (RLH_LDS void*)(buf + kXBytes + 4 * 64 * (w - 1) * 4), 16, 0, 0);
+  }
+}
+
 // A scale or sum slot (token slot >> 1, blocks 4 (slot & 1) .. +3) into LDS.
 __device__ __forceinline__ void store_small(lbyte* buf, bool sum, bool block_major, uint32_t slot, const u32x4_t& v) {
   RLH_LDS float* base = (RLH_LDS float*)(buf + kXBytes + (sum ? kDBytes : 0u));
@@ -582,6 +607,30 @@ k_gemm(GemmArgs a0) {
       for (int e = 0; e < 4; e++) acc[tr][tc][e] = 0.0f;
 
   typename G::W wc[2], wn[2];
+  if constexpr (TY == RLH_TYPE_Q6_K) {
+    // stages by DMA (stage_dma): the copies of super-block j + 1 are issued
+    // with its weight loads and waited for before the loop's barrier
+#pragma unroll
+    for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
+    stage_dma(a, t0, 0, lds);
+    wait_vmcnt<0>();
+    __syncthreads();
+    for (uint32_t j = 0; j < nsb; j++) {
+      const bool more = j + 1 < nsb;
+      if (more) {
+        stage_dma(a, t0, j + 1, lds + ((j + 1) & 1) * kStageBytes);  // freed by the last barrier
+#pragma unroll
+        for (int tc = 0; tc < 2; tc++) G::load(wn[tc], a.w, rowc[tc], j + 1, ln.q);
+      }
+      G::compute(wc, view(lds + (j & 1) * kStageBytes), ln, acc);
+      if (more) {
+#pragma unroll
+        for (int tc = 0; tc < 2; tc++) wc[tc] = wn[tc];
+      }
+      wait_vmcnt<0>();  // this wave's copies (and weights) of super-block j + 1 have landed
+      __syncthreads();  // ... every wave's; the current buffer is free
+    }
+  } else {
   StageRegs sr;
 #pragma unroll
   for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
@@ -603,6 +652,7 @@ k_gemm(GemmArgs a0) {
       stage_store<G::kBlockMajor>(sr, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS);  // freed by the last barrier
     }
     __syncthreads();  // the next stage is in LDS; the current buffer is free
+  }
   }
 #pragma unroll
   for (int tr = 0; tr < 2; tr++)
