@@ -472,10 +472,14 @@ __device__ __forceinline__ void stage_init(StageRegs& r, const GemmArgs& a, uint
   }
 }
 
-__device__ __forceinline__ void stage_load(StageRegs& r, const GemmArgs& a, uint32_t row0, uint32_t j, bool q4k) {
+// q8_dma: the Q8 byte jobs (0..3, and job 4 of wave 0) go by DMA
+// (stage_dma_q8) and are skipped here.
+__device__ __forceinline__ void stage_load(StageRegs& r, const GemmArgs& a, uint32_t row0, uint32_t j, bool q4k,
+                                           bool q8_dma = false) {
   const uint32_t w = wave_id();
 #pragma unroll
   for (uint32_t k = 0; k < 5; k++) {
+    if (q8_dma && (k < 4 || w == 0)) continue;
     r.v[k] = *(const RLH_GLOBAL u32x4_t*)r.src[k];
     r.src[k] += (k < 4 || w == 0) ? 256 : 32;
   }
@@ -494,8 +498,8 @@ __device__ __forceinline__ void stage_load(StageRegs& r, const GemmArgs& a, uint
 // kept output) and the token-major block scales (128 slots of 16 bytes).
 // Every wave issues its copies; the caller waits for them (vmcnt) and then
 // the block barrier.
-__device__ __forceinline__ void stage_dma(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf) {
-  const uint32_t cols = a.w.cols, nb = cols / 32, lane = threadIdx.x & 63, w = wave_id();
+__device__ __forceinline__ void stage_dma_q8(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf) {
+  const uint32_t cols = a.w.cols, lane = threadIdx.x & 63, w = wave_id();
   auto q8_piece = [&](uint32_t p0) {  // pieces p0 .. p0 + 63, p0 a multiple of 64
     const uint32_t p = p0 + lane, tok = p / 17, ch = p - tok * 17;
     const int8_t* src = a.x.qs + (size_t)min(t0 + tok, a.n - 1) * cols + 256 * j + 16 * min(ch, 15u);
@@ -504,6 +508,10 @@ __device__ __forceinline__ void stage_dma(const GemmArgs& a, uint32_t t0, uint32
 #pragma unroll
   for (uint32_t k = 0; k < 4; k++) q8_piece(64 * w + 256 * k);
   if (w == 0) q8_piece(1024);
+}
+__device__ __forceinline__ void stage_dma(const GemmArgs& a, uint32_t t0, uint32_t j, lbyte* buf) {
+  const uint32_t nb = a.w.cols / 32, lane = threadIdx.x & 63, w = wave_id();
+  stage_dma_q8(a, t0, j, buf);
   if (w == 1 || w == 2) {  // scale slots (token slot >> 1, blocks 4 (slot & 1) .. +3)
     const uint32_t slot = 64 * (w - 1) + lane, tok = slot >> 1;
     const float* src = a.x.d + (size_t)min(t0 + tok, a.n - 1) * nb + 8 * j + 4 * (slot & 1);
@@ -526,14 +534,19 @@ __device__ __forceinline__ void store_small(lbyte* buf, bool sum, bool block_maj
 }
 
 template <bool kBlockMajor>
-__device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf, bool q4k) {
+__device__ __forceinline__ void stage_store(const StageRegs& r, lbyte* buf, bool q4k, bool q8_dma = false) {
   const uint32_t t = threadIdx.x, w = wave_id();
+  if (!q8_dma) {
 #pragma unroll
-  for (uint32_t k = 0; k < 4; k++)
-    if (r.keep >> k & 1u) *(RLH_LDS u32x4_t*)(buf + (t + 256 * k) * 16) = r.v[k];
+    for (uint32_t k = 0; k < 4; k++)
+      if (r.keep >> k & 1u) *(RLH_LDS u32x4_t*)(buf + (t + 256 * k) * 16) = r.v[k];
+  }
   if (r.keep >> 4 & 1u) {
-    if (w == 0) *(RLH_LDS u32x4_t*)(buf + (t + 1024) * 16) = r.v[4];
-    else store_small(buf, w == 3, kBlockMajor, r.sub4, r.v[4]);
+    if (w == 0) {
+      if (!q8_dma) *(RLH_LDS u32x4_t*)(buf + (t + 1024) * 16) = r.v[4];
+    } else {
+      store_small(buf, w == 3, kBlockMajor, r.sub4, r.v[4]);
+    }
   }
   if (q4k && (r.keep >> 5 & 1u)) {
     if (w == 0) {
@@ -631,17 +644,22 @@ k_gemm(GemmArgs a0) {
       __syncthreads();  // ... every wave's; the current buffer is free
     }
   } else {
+  // the Q8 bytes by DMA (stage_dma_q8), the block scales, sums and row
+  // scales through registers (they are converted or transposed on the way)
   StageRegs sr;
 #pragma unroll
   for (int tc = 0; tc < 2; tc++) G::load(wc[tc], a.w, rowc[tc], 0, ln.q);
   stage_init(sr, a, t0, G::kNeedS);
-  stage_load(sr, a, r0, 0, G::kNeedS);
-  stage_store<G::kBlockMajor>(sr, lds, G::kNeedS);
+  stage_dma_q8(a, t0, 0, lds);
+  stage_load(sr, a, r0, 0, G::kNeedS, true);
+  stage_store<G::kBlockMajor>(sr, lds, G::kNeedS, true);
+  wait_vmcnt<0>();
   __syncthreads();
   for (uint32_t j = 0; j < nsb; j++) {
     const bool more = j + 1 < nsb;
     if (more) {
-      stage_load(sr, a, r0, j + 1, G::kNeedS);
+      stage_dma_q8(a, t0, j + 1, lds + ((j + 1) & 1) * kStageBytes);  // freed by the last barrier
+      stage_load(sr, a, r0, j + 1, G::kNeedS, true);
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) G::load(wn[tc], a.w, rowc[tc], j + 1, ln.q);
     }
@@ -649,9 +667,10 @@ k_gemm(GemmArgs a0) {
     if (more) {
 #pragma unroll
       for (int tc = 0; tc < 2; tc++) wc[tc] = wn[tc];
-      stage_store<G::kBlockMajor>(sr, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS);  // freed by the last barrier
+      stage_store<G::kBlockMajor>(sr, lds + ((j + 1) & 1) * kStageBytes, G::kNeedS, true);
     }
-    __syncthreads();  // the next stage is in LDS; the current buffer is free
+    wait_vmcnt<0>();  // this wave's copies of super-block j + 1 have landed
+    __syncthreads();  // ... every wave's; the current buffer is free
   }
   }
 #pragma unroll
