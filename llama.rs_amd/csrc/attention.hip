@@ -1499,10 +1499,12 @@ __global__ void __launch_bounds__(512) k_attn_pv_pre(AttnArgs a) {
 
 size_t softmax_lds(uint32_t t_max) { return (size_t)((t_max + 3) & ~3u) * 4; }
 
-// k_attn_softmax_rows: at most this much LDS per block (16 rows of up to 960
-// positions, 8 up to 1984, 4 up to 4032); longer rows take
-// k_attn_softmax<false>.
+// k_attn_softmax_rows: at most this much LDS per block for 16 rows (up to
+// 960 positions) and 8 rows (up to 1984); 4 rows take up to
+// kSoftmaxRows1Lds (4988 positions: two blocks and their static arrays fit
+// one CU's 160 KB); longer rows take k_attn_softmax<false>.
 constexpr size_t kSoftmaxRowsLds = 65536;
+constexpr size_t kSoftmaxRows1Lds = 80896;
 size_t softmax_rows_lds(uint32_t t_max, int rw) { return (size_t)4 * rw * softmax_rows_stride(t_max) * 4; }
 
 }  // namespace
@@ -1535,7 +1537,7 @@ void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
   else if (softmax_rows_lds(a.t_max, 2) <= kSoftmaxRowsLds)
     hipLaunchKernelGGL(k_attn_softmax_rows<2>, dim3(a.H, (a.n_tok + 7) / 8), dim3(256), softmax_rows_lds(a.t_max, 2),
                        st, a);
-  else if (softmax_rows_lds(a.t_max, 1) <= kSoftmaxRowsLds)
+  else if (softmax_rows_lds(a.t_max, 1) <= kSoftmaxRows1Lds)
     hipLaunchKernelGGL(k_attn_softmax_rows<1>, dim3(a.H, (a.n_tok + 3) / 4), dim3(256), softmax_rows_lds(a.t_max, 1),
                        st, a);
   else
@@ -1601,7 +1603,7 @@ bool attn_init(uint32_t max_ctx) {
          hipFuncSetAttribute((const void*)k_attn_softmax<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)softmax_lds(kAttnMaxCtx)) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_softmax_rows<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)kSoftmaxRowsLds) == hipSuccess &&
+                             (int)kSoftmaxRows1Lds) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_softmax_rows<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
                              (int)kSoftmaxRowsLds) == hipSuccess &&
          hipFuncSetAttribute((const void*)k_attn_softmax_rows<4>, hipFuncAttributeMaxDynamicSharedMemorySize,

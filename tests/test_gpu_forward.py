@@ -299,21 +299,23 @@ def test_long_prefill_chunks_and_continuation():
 
 
 def test_prefill_softmax_row_kernels():
-    """Prefill rows up to 4096 positions take the softmax kernel with one wave
-    per row (four rows per block), longer rows the kernel with one block per
-    row: a 4300-token prompt in 512-token chunks uses the first for the chunks
-    that end at or below position 4096 and the second for the last chunk.
-    Logits and the last layer's K/V rows bit-exact against the oracle."""
+    """Prefill rows of up to 4988 positions take the softmax kernel with one
+    wave per row (16, 8 or 4 rows per block by row length), longer rows the
+    kernel with one block per row: a 5200-token prompt in 512-token chunks
+    uses the first for the chunks that end at or below position 4988
+    (among them the chunk ending at 4608, whose 4 rows exceed 64 KB of LDS)
+    and the second for the last two chunks (ending at 5120 and 5200). Logits and the last layer's K/V rows
+    bit-exact against the oracle."""
     spec, tensors, m, om = _get("tiny-g4-q4km")
-    prompt = rlh.synth_tokens(77, 4300, spec.vocab)
-    c = m.new_cache(4400)
-    oc = om.new_cache(4400)
+    prompt = rlh.synth_tokens(77, 5200, spec.vocab)
+    c = m.new_cache(5300)
+    oc = om.new_cache(5300)
     lg = c.forward_into(prompt, 0)
     rg = oc.forward_into(prompt, 0, oracle.MODE_BATCH_INT)
     assert np.array_equal(bits(lg), bits(rg)), f"logits differ (rel {rel_l2(lg, rg):.2e})"
     for which in (0, 1):
         l = spec.n_layer - 1
-        assert np.array_equal(bits(c.read_kv(l, which, 4300)), bits(oc.read_kv(l, which, 4300)))
+        assert np.array_equal(bits(c.read_kv(l, which, 5200)), bits(oc.read_kv(l, which, 5200)))
     c.close()
     oc.close()
 
