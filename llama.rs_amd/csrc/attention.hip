@@ -898,14 +898,20 @@ __global__ void __launch_bounds__(512) k_attn_pv_dec(AttnArgs a) {
   }
 }
 
+// LDS row stride of the decode kernels' score rows: whole 64-position
+// pieces plus 4 floats, so that the same position of different heads' rows
+// falls in different banks (the G-lane sums and the product reads touch
+// several rows per instruction)
+__host__ __device__ inline uint32_t dec_row_stride(uint32_t t_max) { return ((t_max + 63) & ~63u) + 4; }
+
 // Decode with the softmax fused: grid (KVH, 4 slices of 32 dimensions),
-// block 512, dynamic LDS: the group's G score rows (stride RS, a multiple of
-// 64). Each block computes softmax_inplace of the G rows itself (the same
-// arithmetic as k_attn_softmax): the rows arrive by global_load_lds while
-// the first V chunk's loads are in flight, max and exp run over head groups
-// of threads, lanes 0..G-1 run the G sequential sums side by side, and the
-// probabilities stay in LDS for the saxpy chains (as in k_attn_pv_dec).
-__host__ __device__ inline uint32_t dec_row_stride(uint32_t t_max) { return (t_max + 63) & ~63u; }
+// block 512, dynamic LDS: the group's G score rows (stride RS =
+// dec_row_stride). Each block computes softmax_inplace of the G rows itself
+// (the same arithmetic as k_attn_softmax): the rows arrive by
+// global_load_lds while the first V chunk's loads are in flight, max and exp
+// run over head groups of threads, lanes 0..G-1 run the G sequential sums
+// side by side, and the probabilities stay in LDS for the saxpy chains (as
+// in k_attn_pv_dec).
 
 __global__ void __launch_bounds__(512) k_attn_smpv_dec(AttnArgs a) {
   constexpr int CS = kDecChunk + 4;
@@ -1311,7 +1317,7 @@ __host__ __device__ inline uint32_t pv_ring_width(uint32_t group) { return group
 __host__ __device__ inline size_t pv_ring_lds(uint32_t group) {
   const size_t w = pv_ring_width(group);
   const size_t prod = (size_t)kPrSlots * 64 * kPrStride * 4;
-  const size_t in_slot = ((size_t)group * kPrC + (size_t)kPrC * w) * 4;
+  const size_t in_slot = ((size_t)group * kPrStride + (size_t)kPrC * w) * 4;
   return prod + kRingSlots * in_slot;
 }
 
@@ -1319,7 +1325,9 @@ __global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
   const uint32_t G = (uint32_t)(a.H / a.KVH);
   const uint32_t W = pv_ring_width(G), NL = G * W;
-  const uint32_t in_floats = G * kPrC + kPrC * W;  // p rows [G][64], then V rows [64][W]
+  // p rows [G][64] at a stride of kPrStride floats (a producer's 16-byte
+  // reads of G rows fall in distinct banks), then V rows [64][W]
+  const uint32_t in_floats = G * kPrStride + kPrC * W;
   lfloat* pr = (lfloat*)lds_generic;
   lfloat* in = pr + kPrSlots * 64 * kPrStride;
   const uint32_t d0 = blockIdx.x * W, g = blockIdx.y;
@@ -1340,12 +1348,12 @@ __global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
         const uint32_t row = min(c * kPrC + rpi * j + lane / (W / 4), t - 1);
         __builtin_amdgcn_global_load_lds(
             (const RLH_GLOBAL void*)(a.vcache + (size_t)row * kvd + g * kHd + d0 + (lane % (W / 4)) * 4),
-            (RLH_LDS void*)(slot + G * kPrC + rpi * j * W), 16, 0, 0);
+            (RLH_LDS void*)(slot + G * kPrStride + rpi * j * W), 16, 0, 0);
       } else {
         const uint32_t h = j - nvj, pos = min(c * kPrC + lane, t - 1);
         __builtin_amdgcn_global_load_lds(
             (const RLH_GLOBAL void*)(a.scores + (size_t)(g * G + h) * a.t_stride + pos),
-            (RLH_LDS void*)(slot + h * kPrC), 4, 0, 0);
+            (RLH_LDS void*)(slot + h * kPrStride), 4, 0, 0);
       }
     }
   };
@@ -1353,8 +1361,8 @@ __global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
     if (lane >= NL) return;
     const lfloat* slot = in + (c % kRingSlots) * in_floats;
     lfloat* ps = pr + (c % kPrSlots) * (64 * kPrStride) + lane * kPrStride;
-    const lfloat* pc = slot + (lane / W) * kPrC;
-    const lfloat* vc = slot + G * kPrC + lane % W;
+    const lfloat* pc = slot + (lane / W) * kPrStride;
+    const lfloat* vc = slot + G * kPrStride + lane % W;
     for (uint32_t q = pw; q < (uint32_t)kPrC / 4; q += 7) {
       const f32x4_t p = *(const lf32x4*)(pc + 4 * q);
       const lfloat* v = vc + 4 * q * W;
