@@ -1226,41 +1226,42 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
   }
   wait_vmcnt<0>();  // this wave's V pieces have landed
   lds_barrier();
-  // PV. Producer wave w = 1..7, lane l < NL (chain lane l: head h = l / 16,
-  // dimension l % 16) forms the products of the position quads w - 1,
-  // w + 6, w + 13 of a chunk, one quad at a time (more reads in flight per
-  // wave crowd the LDS the chain reads from): p_j = e_j * (1 / sum) when
-  // sum > 0 (softmax_inplace's last loop), then p_j * v_j[d], both rounded
-  // as the reference rounds them.
-  const uint32_t NL = (uint32_t)G * kVsW;  // chain lanes
+  // PV. Chain lane l < NL = G * 8 (head h = l / 8, dimension l % 8). The
+  // producers (waves 1..7) are bound by their instruction issue, so both
+  // half-waves work: lane l of wave w forms chain l % 32's products of the
+  // position quad 2 (w - 1) + l / 32 of a chunk (wave 1 also quad 14 +
+  // l / 32): p_j = e_j * (1 / sum) when sum > 0 (softmax_inplace's last
+  // loop), then p_j * v_j[d], both rounded as the reference rounds them.
+  const uint32_t NL = (uint32_t)G * kVsW;  // chain lanes (at most 32)
   const uint32_t nch = (t + kPrC - 1) / kPrC;
-  const uint32_t ph = min((uint32_t)lane, NL - 1) / kVsW;
+  const uint32_t cl = (uint32_t)lane & 31, hq = (uint32_t)lane >> 5;
+  const uint32_t ph = min(cl, NL - 1) / kVsW;
   const bool pon = s_on[ph];
   const float pinv = s_inv[ph];
   auto produce = [&](uint32_t c) {
-    if ((uint32_t)lane >= NL) return;
-    lfloat* slot = pr + (c % kPrSlots) * (64 * kPrStride) + lane * kPrStride;
+    if (cl >= NL) return;
+    lfloat* slot = pr + (c % kPrSlots) * (64 * kPrStride) + cl * kPrStride;
     const lfloat* ec = e + ph * RS + c * kPrC;  // < RS: chunks never pass the row stride
-    const lfloat* vc = vs + c * kPrC * kVsW + lane % kVsW;
-    for (uint32_t q = wave - 1; q < (uint32_t)kPrC / 4; q += 7) {
+    const lfloat* vc = vs + c * kPrC * kVsW + cl % kVsW;
+    for (uint32_t q = 2 * ((uint32_t)wave - 1) + hq; q < (uint32_t)kPrC / 4; q += 14) {
       f32x4_t x = *(const lf32x4*)(ec + 4 * q);
       if (pon) x = f32x4_t{x.x * pinv, x.y * pinv, x.z * pinv, x.w * pinv};
       const lfloat* v = vc + 4 * q * kVsW;
       *(lf32x4*)(slot + 4 * q) = f32x4_t{x.x * v[0], x.y * v[kVsW], x.z * v[2 * kVsW], x.w * v[3 * kVsW]};
     }
   };
-  if (wave != 0 && (uint32_t)lane < NL) {
+  if (wave != 0 && cl < NL) {
     // chunks 0 and 1 before the chain starts: all their reads first
-    f32x4_t px[2][3];
-    float vx[2][3][4];
+    f32x4_t px[2][2];
+    float vx[2][2][4];
 #pragma unroll
     for (int cc = 0; cc < 2; cc++) {
       const uint32_t c = min((uint32_t)cc, nch - 1);
       const lfloat* ec = e + ph * RS + c * kPrC;
-      const lfloat* vc = vs + c * kPrC * kVsW + lane % kVsW;
+      const lfloat* vc = vs + c * kPrC * kVsW + cl % kVsW;
 #pragma unroll
-      for (int i = 0; i < 3; i++) {
-        const uint32_t q = min((uint32_t)wave - 1 + 7u * i, (uint32_t)kPrC / 4 - 1);
+      for (int i = 0; i < 2; i++) {
+        const uint32_t q = min(2 * ((uint32_t)wave - 1) + hq + 14u * i, (uint32_t)kPrC / 4 - 1);
         px[cc][i] = *(const lf32x4*)(ec + 4 * q);
 #pragma unroll
         for (int r = 0; r < 4; r++) vx[cc][i][r] = vc[(4 * q + r) * kVsW];
@@ -1269,10 +1270,10 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
 #pragma unroll
     for (int cc = 0; cc < 2; cc++) {
       if ((uint32_t)cc >= nch) break;
-      lfloat* slot = pr + cc * (64 * kPrStride) + lane * kPrStride;
+      lfloat* slot = pr + cc * (64 * kPrStride) + cl * kPrStride;
 #pragma unroll
-      for (int i = 0; i < 3; i++) {
-        const uint32_t q = (uint32_t)wave - 1 + 7u * i;
+      for (int i = 0; i < 2; i++) {
+        const uint32_t q = 2 * ((uint32_t)wave - 1) + hq + 14u * i;
         if (q >= (uint32_t)kPrC / 4) break;
         f32x4_t x = px[cc][i];
         if (pon) x = f32x4_t{x.x * pinv, x.y * pinv, x.z * pinv, x.w * pinv};
@@ -1297,13 +1298,16 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
 
 // Decode PV over any context (after k_attn_softmax wrote the probabilities
 // over the scores), V and p streamed through LDS. grid (128 / W slices of W
-// dimensions, KVH), W = 16 (8 when 8 query heads share a KV head, so a block
-// never has more than 64 chains), block 512. Wave 0 lane l < NL = G * W
-// (head l / W, dimension l % W) adds the products in position order
+// dimensions, KVH), W = 8 (4 when more than 4 query heads share a KV head,
+// so a block never has more than 32 chains), block 512. Wave 0 lane l < NL
+// = G * W (head l / W, dimension l % W) adds the products in position order
 // (chain_products); waves 1..7 (producers) stream each 64-position chunk's
 // p rows and V slice into an 8-slot input ring by DMA, and form the products
-// two chunks ahead of the chain into the 3-slot product ring (quads w - 1,
-// w + 6, w + 13 of a chunk, as in k_attn_dec_v). Every producer wave issues
+// two chunks ahead of the chain into the 3-slot product ring. The producers
+// are bound by their instruction issue (two share most SIMDs), so both
+// half-waves of a producer work: lane l forms chain l % 32's products of
+// quad 2 (w - 1) + l / 32 of a chunk (and producer 1 also quad 14 + l / 32).
+// Every producer wave issues
 // exactly two DMA copies per chunk (duplicates of its last job where a chunk
 // has fewer jobs: the same bytes to the same place), so its vector-memory
 // count says when a chunk it is about to use has landed: at the end of
@@ -1312,7 +1316,7 @@ __global__ void __launch_bounds__(512) k_attn_dec_v(AttnArgs a) {
 // visible. The output is written in f32 (attn_output quantizes the row).
 constexpr int kRingSlots = 8;  // input ring: chunks c .. c + 7 resident or in flight
 
-__host__ __device__ inline uint32_t pv_ring_width(uint32_t group) { return group > 4 ? 8u : 16u; }
+__host__ __device__ inline uint32_t pv_ring_width(uint32_t group) { return group > 4 ? 4u : 8u; }
 
 __host__ __device__ inline size_t pv_ring_lds(uint32_t group) {
   const size_t w = pv_ring_width(group);
@@ -1331,7 +1335,7 @@ __global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
   lfloat* pr = (lfloat*)lds_generic;
   lfloat* in = pr + kPrSlots * 64 * kPrStride;
   const uint32_t d0 = blockIdx.x * W, g = blockIdx.y;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t kvd = (uint32_t)a.KVH * kHd;
   const uint32_t t = a.pos0[0] + 1;
   const uint32_t nch = (t + kPrC - 1) / kPrC;
@@ -1357,13 +1361,17 @@ __global__ void __launch_bounds__(512) k_attn_pv_ring(AttnArgs a) {
       }
     }
   };
+  // lane l of a producer forms chain l % 32's products of the quads
+  // 2 pw + l / 32 and (producer 0 only) 14 + l / 32 of the chunk: the two
+  // half-waves split the 16 quads, at most two per lane
+  const uint32_t cl = lane & 31, hq = lane >> 5;
   auto produce = [&](uint32_t c) {
-    if (lane >= NL) return;
+    if (cl >= NL) return;
     const lfloat* slot = in + (c % kRingSlots) * in_floats;
-    lfloat* ps = pr + (c % kPrSlots) * (64 * kPrStride) + lane * kPrStride;
-    const lfloat* pc = slot + (lane / W) * kPrStride;
-    const lfloat* vc = slot + G * kPrStride + lane % W;
-    for (uint32_t q = pw; q < (uint32_t)kPrC / 4; q += 7) {
+    lfloat* ps = pr + (c % kPrSlots) * (64 * kPrStride) + cl * kPrStride;
+    const lfloat* pc = slot + (cl / W) * kPrStride;
+    const lfloat* vc = slot + G * kPrStride + cl % W;
+    for (uint32_t q = 2 * pw + hq; q < (uint32_t)kPrC / 4; q += 14) {
       const f32x4_t p = *(const lf32x4*)(pc + 4 * q);
       const lfloat* v = vc + 4 * q * W;
       *(lf32x4*)(ps + 4 * q) = f32x4_t{p.x * v[0], p.y * v[W], p.z * v[2 * W], p.w * v[3 * W]};
