@@ -573,10 +573,11 @@ __device__ float wave_walk_runs(const lfloat* e, uint32_t t, uint32_t K, uint32_
   return mono_value(u, N);
 }
 
-// grid: (H, n_tok); block 256; dynamic LDS: one row of t_max floats.
+// grid: (H, n_tok); block kSoftmaxWalkThreads (decode) or 256 (prefill);
+// dynamic LDS: one row of t_max floats.
 // The softmax sum ((0 + e_0) + e_1) + ... of the t non-negative terms in LDS
 // (16-byte aligned), bit for bit as the sequential loop rounds it
-// (ops.rs:408-412), by a block of 256 threads. Thread r takes run r (K
+// (ops.rs:408-412), by a block of kSoftmaxWalkThreads threads. Thread r takes run r (K
 // consecutive terms, K a multiple of 4), predicts the binade of the running
 // sum at the run's start from an approximate f32 prefix and forms the run's
 // increment pair there (monosum.h). Wave 0 then takes the runs 64 at a
@@ -591,10 +592,11 @@ __device__ float wave_walk_runs(const lfloat* e, uint32_t t, uint32_t K, uint32_
 // made the 32B 4096-token prefill slower (1931 -> 1957 ms); decode at 4.1 K
 // positions gains (96.1 -> 97.6 tok/s). Every thread gets the sum.
 constexpr uint32_t kSoftmaxWalkMin = 1024;  // shorter rows: the plain chain
+constexpr uint32_t kSoftmaxWalkThreads = 1024;  // the decode launch's block: one run per thread
 struct SoftmaxSumLds {
-  uint32_t a0[256], a1[256];
-  int u[256];
-  float wsum[4];
+  uint32_t a0[kSoftmaxWalkThreads], a1[kSoftmaxWalkThreads];
+  int u[kSoftmaxWalkThreads];
+  float wsum[kSoftmaxWalkThreads / 64];
   float out;
 };
 // shift (a test knob, 0 in use): 1 / 2 move every run's predicted binade
@@ -610,7 +612,7 @@ __device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* s
     __syncthreads();
     return L->out;
   }
-  const uint32_t K = (((t + 255) / 256) + 3) & ~3u;
+  const uint32_t K = (((t + kSoftmaxWalkThreads - 1) / kSoftmaxWalkThreads) + 3) & ~3u;
   const uint32_t j0 = min(tid * K, t), j1 = min(j0 + K, t);
   float a = 0.0f;
   bool bad = false;
@@ -648,11 +650,13 @@ __device__ float block_softmax_sum(const lfloat* e, uint32_t t, SoftmaxSumLds* s
   return L->out;
 }
 
-// WALK: the decode launch, whose sum is block_softmax_sum's.
+// WALK: the decode launch (block of kSoftmaxWalkThreads), whose sum is
+// block_softmax_sum's; the prefill launch takes 256 threads per row.
 template <bool WALK>
-__global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
+__global__ void __launch_bounds__(WALK ? kSoftmaxWalkThreads : 256) k_attn_softmax(AttnArgs a) {
+  constexpr uint32_t NT = WALK ? kSoftmaxWalkThreads : 256;
   extern __shared__ __attribute__((aligned(16))) float lds_generic[];
-  __shared__ float red[4];
+  __shared__ float red[NT / 64];
   __shared__ uint64_t tab_g[32];
   __shared__ float s_inv;
   __shared__ int s_on;
@@ -667,16 +671,16 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   // load per iteration would make each LDS store wait for its own load in
   // turn); a -inf stand-in past t leaves the max unchanged
   float mx = -__int_as_float(0x7f800000);
-  for (uint32_t b = 0; b < t; b += 256 * 8) {
+  for (uint32_t b = 0; b < t; b += NT * 8) {
     float v[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const uint32_t j = b + tid + 256 * k;
+      const uint32_t j = b + tid + NT * k;
       v[k] = j < t ? ld_gf(row + j) : -__int_as_float(0x7f800000);
     }
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-      const uint32_t j = b + tid + 256 * k;
+      const uint32_t j = b + tid + NT * k;
       if (j < t) e[j] = v[k];
       mx = fmaxf(mx, v[k]);
     }
@@ -686,14 +690,15 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
   for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   if (lane == 0) red[wave] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+  for (uint32_t w = 0; w < NT / 64; w++) mx = fmaxf(mx, red[w]);
   const float x0 = e[0];
   if (x0 != x0) mx = x0;
   // four terms per thread and step (16-byte LDS accesses: the row and its
   // LDS stride are 16-byte aligned and cover t rounded up to 4); words past
   // t keep their contents
   const uint32_t nq = (t + 3) / 4;
-  for (uint32_t q = tid; q < nq; q += 256) {
+  for (uint32_t q = tid; q < nq; q += NT) {
     const uint32_t j = 4 * q;
     const f32x4_t x = *(const lf32x4*)(e + j);
     const float y0 = expf_glibc_t(x.x - mx, tab), y1 = expf_glibc_t(x.y - mx, tab);
@@ -718,7 +723,7 @@ __global__ void __launch_bounds__(256) k_attn_softmax(AttnArgs a) {
     on = s_on;
     inv = s_inv;
   }
-  for (uint32_t q = tid; q < nq; q += 256) {
+  for (uint32_t q = tid; q < nq; q += NT) {
     const uint32_t j = 4 * q;
     const f32x4_t v = *(const lf32x4*)(e + j);
     row[j] = on ? v.x * inv : v.x;
@@ -1546,7 +1551,7 @@ void launch_attn_scores(hipStream_t st, const AttnArgs& a, bool fused) {
 
 void launch_attn_softmax(hipStream_t st, const AttnArgs& a) {
   if (a.n_tok == 1)
-    hipLaunchKernelGGL(k_attn_softmax<true>, dim3(a.H, 1), dim3(256), softmax_lds(a.t_max), st, a);
+    hipLaunchKernelGGL(k_attn_softmax<true>, dim3(a.H, 1), dim3(kSoftmaxWalkThreads), softmax_lds(a.t_max), st, a);
   else if (softmax_rows_lds(a.t_max, 4) <= kSoftmaxRowsLds)
     hipLaunchKernelGGL(k_attn_softmax_rows<4>, dim3(a.H, (a.n_tok + 15) / 16), dim3(256),
                        softmax_rows_lds(a.t_max, 4), st, a);
