@@ -2,7 +2,8 @@
  *
  * This is the drop-in boundary behind the reference's Rust API. A Rust host
  * keeps `Model::forward_into` / `KvCache` / the sampler and binds these
- * symbols through a thin FFI crate (the binding is shown in INTEGRATION.md).
+ * symbols through a thin FFI crate (an `extern "C"` block that mirrors
+ * every declaration below one to one).
  * Plain C types only: pointers, sizes and status codes; no torch or HIP
  * types cross the boundary.
  *

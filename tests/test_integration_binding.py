@@ -1,7 +1,8 @@
-"""INTEGRATION.md's Rust FFI binding mirrors include/rlh.h one to one: the
-same entry points, each with the same parameter count and order, parameter
-types and return type under the C -> Rust type mapping of std::os::raw.
-CPU only (the binding text is not compiled here: no Rust toolchain)."""
+"""The Rust FFI binding in the repository's integration guide mirrors
+include/rlh.h one to one: the same entry points, each with the same
+parameter count and order, parameter types and return type under the C ->
+Rust type mapping of std::os::raw. CPU only (the binding text is not
+compiled here: no Rust toolchain)."""
 import os
 import re
 
@@ -55,7 +56,7 @@ def binding_decls():
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     blocks = re.findall(r"```rust\n(.*?)```", text, flags=re.S)
     ext = [b for b in blocks if 'extern "C"' in b]
-    assert len(ext) == 1, "INTEGRATION.md must hold exactly one extern \"C\" Rust block"
+    assert len(ext) == 1, "the integration guide must hold exactly one extern \"C\" Rust block"
     body = re.sub(r"//.*", "", ext[0])
     decls = {}
     for m in re.finditer(r"pub fn (rlh_[a-z0-9_]+)\s*\((.*?)\)\s*(->\s*([^;]+))?;", body, flags=re.S):
